@@ -1,0 +1,1175 @@
+// C ABI of libglm53_moe.so (declared in include/glm53_moe.h).
+//
+// Host-side validation, plan objects with fixed device scratch, and the
+// launch schedules of the decode and prefill paths.  No C++ exception
+// crosses the boundary: every entry point returns a status code and leaves a
+// thread-local message for glm53_last_error().
+#include <glm53_moe.h>
+
+#include <rocblas/rocblas.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "grouped.h"
+#include "kernels.h"
+#include "synth.h"
+
+using namespace glm53;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(GLM53_DEVICE_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                      \
+  do {                                           \
+    hipError_t _e = (expr);                      \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+#define CHECK_ARG(cond, ...)                                        \
+  do {                                                              \
+    if (!(cond)) return fail(GLM53_INVALID_ARGUMENT, __VA_ARGS__);  \
+  } while (0)
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline size_t round_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// Bytes of the hi/lo/scale split of a [rows, cols] activation matrix.
+size_t split_bytes(int64_t rows, int64_t cols) {
+  return 2 * round_up(static_cast<size_t>(rows * cols)) + round_up(sizeof(float) * static_cast<size_t>(rows * (cols / 128)));
+}
+
+struct SplitBuf {
+  uint8_t* hi;
+  uint8_t* lo;
+  float* scale;
+};
+
+SplitBuf carve_split(void* base, int64_t rows, int64_t cols) {
+  uint8_t* p = static_cast<uint8_t*>(base);
+  SplitBuf b;
+  b.hi = p;
+  p += round_up(static_cast<size_t>(rows * cols));
+  b.lo = p;
+  p += round_up(static_cast<size_t>(rows * cols));
+  b.scale = reinterpret_cast<float*>(p);
+  return b;
+}
+
+hipError_t split(const void* x, int64_t rows, int64_t cols, const SplitBuf& b, hipStream_t st) {
+  SplitArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_row_stride = cols;
+  a.rows = rows;
+  a.cols = cols;
+  a.hi = b.hi;
+  a.lo = b.lo;
+  a.scale = b.scale;
+  return launch_split_activations(a, st);
+}
+
+int check_linear(const glm53_linear& l, int64_t out, int64_t in, const char* name) {
+  CHECK_ARG(l.weight != nullptr && l.scale_inv != nullptr, "%s: null weight or scale", name);
+  CHECK_ARG(l.out_features == out && l.in_features == in, "%s: shape [%lld, %lld] != expected [%lld, %lld]", name,
+            (long long)l.out_features, (long long)l.in_features, (long long)out, (long long)in);
+  return GLM53_OK;
+}
+
+int check_bank(const glm53_bank* b, int64_t H, int64_t I, int64_t E) {
+  CHECK_ARG(b != nullptr, "bank is null");
+  CHECK_ARG(b->gate_up_weight && b->gate_up_scale_inv && b->down_weight && b->down_scale_inv,
+            "bank has a null buffer");
+  CHECK_ARG(b->hidden == H && b->intermediate == I && b->experts == E,
+            "bank shape (E=%lld, H=%lld, I=%lld) != plan (E=%lld, H=%lld, I=%lld)", (long long)b->experts,
+            (long long)b->hidden, (long long)b->intermediate, (long long)E, (long long)H, (long long)I);
+  return GLM53_OK;
+}
+
+int check_router(const glm53_router* r, int64_t H, int64_t E, int64_t k) {
+  CHECK_ARG(r != nullptr && r->weight != nullptr && r->bias != nullptr, "router weight/bias is null");
+  CHECK_ARG(r->hidden == H && r->experts == E, "router shape [%lld, %lld] != [%lld, %lld]", (long long)r->experts,
+            (long long)r->hidden, (long long)E, (long long)H);
+  CHECK_ARG(r->top_k == k, "router top_k %lld != plan top_k %lld", (long long)r->top_k, (long long)k);
+  return GLM53_OK;
+}
+
+std::mutex g_blas_mutex;
+rocblas_handle g_blas = nullptr;
+
+int blas_handle(rocblas_handle* out) {
+  std::lock_guard<std::mutex> lock(g_blas_mutex);
+  if (g_blas == nullptr) {
+    if (rocblas_create_handle(&g_blas) != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_create_handle failed");
+  }
+  *out = g_blas;
+  return GLM53_OK;
+}
+
+// logits[T, E] = x_f32[T, H] . W[E, H]^T in FP32 (column-major view: C' = W'^T X').
+int router_logits(const float* xf, const float* w, float* logits, int64_t T, int64_t H, int64_t E, hipStream_t st) {
+  rocblas_handle h;
+  int rc = blas_handle(&h);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_blas_mutex);
+  if (rocblas_set_stream(h, st) != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_set_stream failed");
+  const float one = 1.0f, zero = 0.0f;
+  rocblas_status s = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(E),
+                                   static_cast<rocblas_int>(T), static_cast<rocblas_int>(H), &one, w,
+                                   static_cast<rocblas_int>(H), xf, static_cast<rocblas_int>(H), &zero, logits,
+                                   static_cast<rocblas_int>(E));
+  if (s != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_sgemm failed (%d)", (int)s);
+  return GLM53_OK;
+}
+
+int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, float* scores, hipStream_t st) {
+  TopkArgs a{};
+  a.logits = logits;
+  a.bias = r->bias;
+  a.tokens = T;
+  a.experts = r->experts;
+  a.top_k = static_cast<int>(r->top_k);
+  a.routed_scaling_factor = r->routed_scaling_factor;
+  a.norm_topk_prob = r->norm_topk_prob;
+  a.ids_out = ids;
+  a.scores_out = scores;
+  HIP_TRY(launch_topk(a, st), "topk launch");
+  return GLM53_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* glm53_last_error(void) { return g_error.c_str(); }
+int glm53_abi_version(void) { return GLM53_ABI_VERSION; }
+
+// ------------------------------------------------------------ linear ------
+
+size_t glm53_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 1 || K <= 0 || K % 128 != 0 || N % 16 != 0) return 0;
+  return split_bytes(M, K) + 256;  // + the 0x7F/0xFF code flag
+}
+
+int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* stream) {
+  CHECK_ARG(n >= 0 && flag != nullptr && (n == 0 || codes != nullptr), "invalid arguments");
+  CHECK_ARG(aligned(codes, 16) || n < 16, "codes must be 16-byte aligned");
+  HIP_TRY(launch_scan_480(codes, n, flag, true, S(stream)), "scan launch");
+  return GLM53_OK;
+}
+
+int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N, const float* scale_inv,
+                     void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  CHECK_ARG(M >= 0 && K > 0 && N > 0, "invalid shape M=%lld K=%lld N=%lld", (long long)M, (long long)K, (long long)N);
+  if (M == 0) return GLM53_OK;
+  CHECK_ARG(x && weight && scale_inv && y, "null pointer argument");
+  hipStream_t st = S(stream);
+  if (M == 1 && fast_width_supported(K) && aligned(x, 16) && aligned(weight, 16)) {
+    GemvArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.weight = weight;
+    a.scale = scale_inv;
+    a.N = N;
+    a.K = K;
+    a.rows_per_wave = 4;
+    a.y = static_cast<uint16_t*>(y);
+    HIP_TRY(launch_gemv(a, st), "gemv launch");
+    return GLM53_OK;
+  }
+  const size_t need = glm53_fp8_linear_workspace_bytes(M, N, K);
+  if (need > 0 && aligned(weight, 16) && workspace != nullptr && workspace_bytes >= need) {
+    SplitBuf b = carve_split(workspace, M, K);
+    int32_t* flag = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + split_bytes(M, K));
+    HIP_TRY(launch_scan_480(weight, N * K, flag, true, st), "scan launch");
+    HIP_TRY(split(x, M, K, b, st), "split launch");
+    GroupedGemmArgs g{};
+    g.fixup = flag;
+    g.a_hi = b.hi;
+    g.a_lo = b.lo;
+    g.a_scale = b.scale;
+    g.K = K;
+    g.routes = M;
+    g.experts = 1;
+    g.weight = weight;
+    g.scale = scale_inv;
+    g.s_cols = K / 128;
+    g.N = N;
+    g.out = static_cast<uint16_t*>(y);
+    g.out_row_stride = N;
+    HIP_TRY(launch_grouped_gemm(g, GEMM_PLAIN, cdiv(M, kGroupedTileRows), st), "grouped gemm launch");
+    return GLM53_OK;
+  }
+  GenericLinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_row_stride = K;
+  a.weight = weight;
+  a.scale = scale_inv;
+  a.s_cols = cdiv(K, 128);
+  a.M = M;
+  a.G = 1;
+  a.N = N;
+  a.K = K;
+  a.rows_per_wave = 4;
+  a.tile_rows = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kGenericRows, 16384 / K)));
+  a.y = static_cast<uint16_t*>(y);
+  a.y_row_stride = N;
+  CHECK_ARG(K <= 16384, "generic path supports K <= 16384");
+  HIP_TRY(launch_linear_generic(a, st), "generic linear launch");
+  return GLM53_OK;
+}
+
+// ------------------------------------------------------------ router ------
+
+size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
+  if (tokens <= 1) return round_up(sizeof(float) * 2 * experts) + 256;
+  return round_up(sizeof(float) * tokens * hidden) + round_up(sizeof(float) * tokens * experts);
+}
+
+int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids, float* scores,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  CHECK_ARG(router && router->weight && router->bias, "router is null");
+  CHECK_ARG(router->experts > 0 && router->experts <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
+  CHECK_ARG(router->top_k > 0 && router->top_k <= kMaxTopK && router->top_k <= router->experts,
+            "top_k must be in [1, %d]", kMaxTopK);
+  CHECK_ARG(tokens >= 0, "tokens < 0");
+  if (tokens == 0) return GLM53_OK;
+  CHECK_ARG(x && ids && scores, "null pointer argument");
+  CHECK_ARG(workspace_bytes >= glm53_router_workspace_bytes(tokens, router->hidden, router->experts) && workspace,
+            "router workspace too small");
+  hipStream_t st = S(stream);
+  if (tokens == 1) {
+    float* sig = static_cast<float*>(workspace);
+    float* choice = sig + router->experts;
+    unsigned* arrivals = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(workspace) +
+                                                     round_up(sizeof(float) * 2 * router->experts));
+    HIP_TRY(hipMemsetAsync(arrivals, 0, sizeof(unsigned), st), "memset");
+    RouterArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.weight = router->weight;
+    a.bias = router->bias;
+    a.experts = router->experts;
+    a.hidden = router->hidden;
+    a.top_k = static_cast<int>(router->top_k);
+    a.routed_scaling_factor = router->routed_scaling_factor;
+    a.norm_topk_prob = router->norm_topk_prob;
+    a.sigmoid_out = sig;
+    a.choice_out = choice;
+    a.arrivals = arrivals;
+    a.ids_out = ids;
+    a.scores_out = scores;
+    HIP_TRY(launch_router(a, st), "router launch");
+    return GLM53_OK;
+  }
+  float* xf = static_cast<float*>(workspace);
+  float* logits = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                           round_up(sizeof(float) * tokens * router->hidden));
+  HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), xf, tokens * router->hidden, st), "widen launch");
+  int rc = router_logits(xf, router->weight, logits, tokens, router->hidden, router->experts, st);
+  if (rc) return rc;
+  return topk(logits, router, tokens, ids, scores, st);
+}
+
+// ------------------------------------------------------------ decode ------
+
+struct glm53_decode_plan {
+  int64_t H, I, Is, E, k;
+  float limit;
+  // fixed scratch (allocated once)
+  uint16_t* hidden = nullptr;  // [(k + 1) * max(I, Is)]
+  float* sig = nullptr;        // [E]
+  float* choice = nullptr;     // [E]
+  unsigned* arrivals = nullptr;
+  int32_t* ids = nullptr;      // [k]
+  float* scores = nullptr;     // [k]
+  int* err = nullptr;
+  // any-shape composition scratch
+  uint16_t* gate = nullptr;    // [k, I]
+  uint16_t* up = nullptr;      // [k, I]
+  uint16_t* down = nullptr;    // [k, H]
+  uint16_t* routed = nullptr;  // [H]
+  uint16_t* shared_gate = nullptr;  // [Is]
+  uint16_t* shared_up = nullptr;
+  uint16_t* shared_out = nullptr;   // [H]
+  void* arena = nullptr;
+  bool bound = false;
+  glm53_bank bank{};
+  glm53_shared_expert shared{};
+  bool has_shared = false;
+  glm53_router router{};
+  bool has_router = false;
+};
+
+int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate, int64_t experts,
+                             int64_t top_k, float swiglu_limit, glm53_decode_plan** out) {
+  CHECK_ARG(out != nullptr, "out is null");
+  *out = nullptr;
+  CHECK_ARG(hidden > 0 && intermediate > 0 && shared_intermediate >= 0, "invalid dimensions");
+  CHECK_ARG(experts > 0 && experts <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
+  CHECK_ARG(top_k > 0 && top_k <= kMaxTopK && top_k <= experts, "top_k must be in [1, %d]", kMaxTopK);
+  auto* p = new glm53_decode_plan();
+  p->H = hidden;
+  p->I = intermediate;
+  p->Is = shared_intermediate;
+  p->E = experts;
+  p->k = top_k;
+  p->limit = swiglu_limit;
+  const int64_t Imax = std::max(intermediate, shared_intermediate);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += round_up(bytes);
+    return o;
+  };
+  size_t o_hidden = take(2 * (top_k + 1) * Imax);
+  size_t o_sig = take(4 * experts), o_choice = take(4 * experts), o_arr = take(4), o_ids = take(4 * top_k);
+  size_t o_scores = take(4 * top_k), o_err = take(4);
+  size_t o_gate = take(2 * top_k * intermediate), o_up = take(2 * top_k * intermediate);
+  size_t o_down = take(2 * top_k * hidden), o_routed = take(2 * hidden);
+  size_t o_sg = take(2 * std::max<int64_t>(shared_intermediate, 1)), o_su = take(2 * std::max<int64_t>(shared_intermediate, 1));
+  size_t o_so = take(2 * hidden);
+  hipError_t e = hipMalloc(&p->arena, off);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "decode plan hipMalloc");
+  }
+  e = hipMemset(p->arena, 0, off);
+  if (e != hipSuccess) {
+    (void)hipFree(p->arena);
+    delete p;
+    return hip_fail(e, "decode plan hipMemset");
+  }
+  uint8_t* b = static_cast<uint8_t*>(p->arena);
+  p->hidden = reinterpret_cast<uint16_t*>(b + o_hidden);
+  p->sig = reinterpret_cast<float*>(b + o_sig);
+  p->choice = reinterpret_cast<float*>(b + o_choice);
+  p->arrivals = reinterpret_cast<unsigned*>(b + o_arr);
+  p->ids = reinterpret_cast<int32_t*>(b + o_ids);
+  p->scores = reinterpret_cast<float*>(b + o_scores);
+  p->err = reinterpret_cast<int*>(b + o_err);
+  p->gate = reinterpret_cast<uint16_t*>(b + o_gate);
+  p->up = reinterpret_cast<uint16_t*>(b + o_up);
+  p->down = reinterpret_cast<uint16_t*>(b + o_down);
+  p->routed = reinterpret_cast<uint16_t*>(b + o_routed);
+  p->shared_gate = reinterpret_cast<uint16_t*>(b + o_sg);
+  p->shared_up = reinterpret_cast<uint16_t*>(b + o_su);
+  p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
+  *out = p;
+  return GLM53_OK;
+}
+
+void glm53_decode_plan_destroy(glm53_decode_plan* plan) {
+  if (plan == nullptr) return;
+  if (plan->arena) (void)hipFree(plan->arena);
+  delete plan;
+}
+
+namespace {
+
+int check_decode_inputs(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared) {
+  CHECK_ARG(p != nullptr, "plan is null");
+  int rc = check_bank(bank, p->H, p->I, p->E);
+  if (rc) return rc;
+  if (shared != nullptr) {
+    CHECK_ARG(p->Is > 0, "plan was created without a shared expert");
+    if ((rc = check_linear(shared->gate, p->Is, p->H, "shared gate"))) return rc;
+    if ((rc = check_linear(shared->up, p->Is, p->H, "shared up"))) return rc;
+    if ((rc = check_linear(shared->down, p->H, p->Is, "shared down"))) return rc;
+  }
+  return GLM53_OK;
+}
+
+bool decode_fast_ok(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                    const void* x) {
+  if (!fast_width_supported(p->H) || !fast_width_supported(p->I)) return false;
+  if (p->H / 128 * 128 != p->H) return false;
+  if (shared != nullptr && p->Is != p->I) return false;
+  if (!aligned(x, 16) || !aligned(bank->gate_up_weight, 16) || !aligned(bank->down_weight, 16)) return false;
+  if (shared != nullptr && (!aligned(shared->gate.weight, 16) || !aligned(shared->up.weight, 16) ||
+                            !aligned(shared->down.weight, 16)))
+    return false;
+  return true;
+}
+
+int generic_linear(const void* x, int64_t x_group_stride, int64_t M, int64_t G, const uint8_t* w,
+                   int64_t w_expert_stride, int64_t w_row_offset, const float* s, int64_t s_expert_stride,
+                   int64_t s_row_offset, int64_t s_cols, const int32_t* ids, int64_t experts, int64_t N, int64_t K,
+                   uint16_t* y, int64_t y_group_stride, int* err, hipStream_t st) {
+  CHECK_ARG(K <= 16384, "generic path supports K <= 16384");
+  GenericLinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_row_stride = K;
+  a.x_group_stride = x_group_stride;
+  a.weight = w;
+  a.w_expert_stride = w_expert_stride;
+  a.w_row_offset = w_row_offset;
+  a.scale = s;
+  a.s_expert_stride = s_expert_stride;
+  a.s_row_offset = s_row_offset;
+  a.s_cols = s_cols;
+  a.expert_ids = ids;
+  a.experts = experts;
+  a.M = M;
+  a.G = G;
+  a.N = N;
+  a.K = K;
+  a.rows_per_wave = 4;
+  a.tile_rows = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kGenericRows, 16384 / K)));
+  a.y = y;
+  a.y_row_stride = N;
+  a.y_group_stride = y_group_stride;
+  a.error_flag = err;
+  HIP_TRY(launch_linear_generic(a, st), "generic linear launch");
+  return GLM53_OK;
+}
+
+int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared, const void* x,
+               const int32_t* ids, const float* scores, void* out, hipStream_t st) {
+  const int64_t H = p->H, I = p->I, Is = p->Is, k = p->k;
+  if (decode_fast_ok(p, bank, shared, x)) {
+    GateUpArgs g{};
+    g.x = static_cast<const uint16_t*>(x);
+    g.expert_ids = ids;
+    g.top_k = static_cast<int>(k);
+    g.experts = p->E;
+    g.gate_up_weight = bank->gate_up_weight;
+    g.gate_up_scale = bank->gate_up_scale_inv;
+    if (shared != nullptr) {
+      g.shared_gate_weight = shared->gate.weight;
+      g.shared_gate_scale = shared->gate.scale_inv;
+      g.shared_up_weight = shared->up.weight;
+      g.shared_up_scale = shared->up.scale_inv;
+    }
+    g.hidden = H;
+    g.intermediate = I;
+    g.shared_intermediate = shared != nullptr ? Is : 0;
+    g.limit = p->limit;
+    g.rows_per_wave = 4;
+    g.wgs_per_slot = cdiv(I, 4 * g.rows_per_wave);
+    g.hidden_out = p->hidden;
+    g.error_flag = p->err;
+    HIP_TRY(launch_gate_up(g, st), "gate/up launch");
+    DownArgs d{};
+    d.hidden_in = p->hidden;
+    d.expert_ids = ids;
+    d.scores = scores;
+    d.top_k = static_cast<int>(k);
+    d.experts = p->E;
+    d.down_weight = bank->down_weight;
+    d.down_scale = bank->down_scale_inv;
+    if (shared != nullptr) {
+      d.shared_down_weight = shared->down.weight;
+      d.shared_down_scale = shared->down.scale_inv;
+    }
+    d.hidden = H;
+    d.intermediate = I;
+    d.rows_per_wg = 8;
+    d.out = static_cast<uint16_t*>(out);
+    d.error_flag = p->err;
+    HIP_TRY(launch_down(d, st), "down launch");
+    return GLM53_OK;
+  }
+  // Any-shape composition of the reference's separate stages
+  // (packed.py:473-655): gate, up, SwiGLU, down, weighted reduction, shared.
+  const int64_t SR = cdiv(I, 128), SC = cdiv(H, 128), SH = cdiv(H, 128), SI = cdiv(I, 128);
+  int rc;
+  if ((rc = generic_linear(x, 0, 1, k, bank->gate_up_weight, 2 * I * H, 0, bank->gate_up_scale_inv, 2 * SR * SC, 0,
+                           SC, ids, p->E, I, H, p->gate, I, p->err, st)))
+    return rc;
+  if ((rc = generic_linear(x, 0, 1, k, bank->gate_up_weight, 2 * I * H, I, bank->gate_up_scale_inv, 2 * SR * SC, SR,
+                           SC, ids, p->E, I, H, p->up, I, p->err, st)))
+    return rc;
+  SwigluArgs sw{};
+  sw.gate = p->gate;
+  sw.up = p->up;
+  sw.gate_row_stride = I;
+  sw.up_row_stride = I;
+  sw.rows = k;
+  sw.cols = I;
+  sw.limit = p->limit;
+  sw.out = p->hidden;
+  sw.out_row_stride = I;
+  HIP_TRY(launch_swiglu(sw, st), "swiglu launch");
+  if ((rc = generic_linear(p->hidden, I, 1, k, bank->down_weight, H * I, 0, bank->down_scale_inv, SH * SI, 0, SI, ids,
+                           p->E, H, I, p->down, H, p->err, st)))
+    return rc;
+  WeightedReductionArgs wr{};
+  wr.down = p->down;
+  wr.scores = scores;
+  wr.top_k = static_cast<int>(k);
+  wr.H = H;
+  if (shared == nullptr) {
+    wr.out = static_cast<uint16_t*>(out);
+    HIP_TRY(launch_weighted_reduction(wr, st), "reduction launch");
+    return GLM53_OK;
+  }
+  wr.out = p->routed;
+  HIP_TRY(launch_weighted_reduction(wr, st), "reduction launch");
+  const int64_t SIs = cdiv(Is, 128);
+  if ((rc = generic_linear(x, 0, 1, 1, shared->gate.weight, 0, 0, shared->gate.scale_inv, 0, 0, SC, nullptr, 1, Is, H,
+                           p->shared_gate, 0, p->err, st)))
+    return rc;
+  if ((rc = generic_linear(x, 0, 1, 1, shared->up.weight, 0, 0, shared->up.scale_inv, 0, 0, SC, nullptr, 1, Is, H,
+                           p->shared_up, 0, p->err, st)))
+    return rc;
+  uint16_t* shared_hidden = p->hidden + k * std::max(I, Is);
+  sw.gate = p->shared_gate;
+  sw.up = p->shared_up;
+  sw.gate_row_stride = Is;
+  sw.up_row_stride = Is;
+  sw.rows = 1;
+  sw.cols = Is;
+  sw.out = shared_hidden;
+  sw.out_row_stride = Is;
+  HIP_TRY(launch_swiglu(sw, st), "swiglu launch");
+  if ((rc = generic_linear(shared_hidden, 0, 1, 1, shared->down.weight, 0, 0, shared->down.scale_inv, 0, 0, SIs,
+                           nullptr, 1, H, Is, p->shared_out, 0, p->err, st)))
+    return rc;
+  HIP_TRY(launch_add_bf16(p->routed, p->shared_out, static_cast<uint16_t*>(out), H, st), "add launch");
+  return GLM53_OK;
+}
+
+int run_router_decode(glm53_decode_plan* p, const glm53_router* r, const void* x, hipStream_t st) {
+  RouterArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.weight = r->weight;
+  a.bias = r->bias;
+  a.experts = r->experts;
+  a.hidden = r->hidden;
+  a.top_k = static_cast<int>(r->top_k);
+  a.routed_scaling_factor = r->routed_scaling_factor;
+  a.norm_topk_prob = r->norm_topk_prob;
+  a.sigmoid_out = p->sig;
+  a.choice_out = p->choice;
+  a.arrivals = p->arrivals;
+  a.ids_out = p->ids;
+  a.scores_out = p->scores;
+  HIP_TRY(launch_router(a, st), "router launch");
+  return GLM53_OK;
+}
+
+}  // namespace
+
+int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
+                            const void* x, const int32_t* expert_ids, const float* scores, void* out, void* stream) {
+  int rc = check_decode_inputs(plan, bank, shared);
+  if (rc) return rc;
+  CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
+  return run_decode(plan, bank, shared, x, expert_ids, scores, out, S(stream));
+}
+
+int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
+                     const glm53_router* router, const void* x, void* out, int32_t* ids_out, float* scores_out,
+                     void* stream) {
+  int rc = check_decode_inputs(plan, bank, shared);
+  if (rc) return rc;
+  if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  CHECK_ARG(x && out, "null pointer argument");
+  hipStream_t st = S(stream);
+  if ((rc = run_router_decode(plan, router, x, st))) return rc;
+  if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, out, st))) return rc;
+  if (ids_out) HIP_TRY(hipMemcpyAsync(ids_out, plan->ids, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy ids");
+  if (scores_out)
+    HIP_TRY(hipMemcpyAsync(scores_out, plan->scores, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy scores");
+  return GLM53_OK;
+}
+
+int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
+                           const glm53_router* router) {
+  CHECK_ARG(plan != nullptr, "plan is null");
+  if (plan->bound) return fail(GLM53_BAD_STATE, "decode plan weights are already bound");
+  int rc = check_decode_inputs(plan, bank, shared);
+  if (rc) return rc;
+  if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  plan->bank = *bank;
+  plan->has_shared = shared != nullptr;
+  if (shared) plan->shared = *shared;
+  plan->router = *router;
+  plan->has_router = true;
+  plan->bound = true;
+  return GLM53_OK;
+}
+
+int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, void* stream) {
+  CHECK_ARG(plan != nullptr, "plan is null");
+  if (!plan->bound) return fail(GLM53_BAD_STATE, "decode plan has no bound weights");
+  CHECK_ARG(x && out, "null pointer argument");
+  hipStream_t st = S(stream);
+  int rc = run_router_decode(plan, &plan->router, x, st);
+  if (rc) return rc;
+  return run_decode(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, x, plan->ids, plan->scores, out,
+                    st);
+}
+
+int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes) {
+  CHECK_ARG(plan && ptr && bytes, "null pointer argument");
+  switch (which) {
+    case 0:
+      *ptr = plan->hidden;
+      *bytes = 2 * (plan->k + 1) * std::max(plan->I, plan->Is);
+      return GLM53_OK;
+    case 1:
+      *ptr = plan->ids;
+      *bytes = 4 * plan->k;
+      return GLM53_OK;
+    case 2:
+      *ptr = plan->scores;
+      *bytes = 4 * plan->k;
+      return GLM53_OK;
+    default:
+      return fail(GLM53_INVALID_ARGUMENT, "unknown scratch id %d", which);
+  }
+}
+
+int glm53_decode_plan_error_flag(glm53_decode_plan* plan, int32_t* host_value) {
+  CHECK_ARG(plan && host_value, "null pointer argument");
+  HIP_TRY(hipMemcpy(host_value, plan->err, sizeof(int32_t), hipMemcpyDeviceToHost), "read error flag");
+  HIP_TRY(hipMemset(plan->err, 0, sizeof(int32_t)), "clear error flag");
+  return GLM53_OK;
+}
+
+// ---------------------------------------------------- prefill pieces ------
+
+size_t glm53_route_plan_workspace_bytes(int64_t routes, int64_t experts) {
+  const int64_t blocks = std::max<int64_t>(cdiv(routes, 256), 1);
+  return round_up(sizeof(unsigned) * blocks * experts) + round_up(sizeof(unsigned) * blocks);
+}
+
+namespace {
+
+int route_plan_impl(const int32_t* expert_ids, const float* scores, int64_t routes, int64_t top_k, int64_t experts,
+                    int64_t tile_rows, int32_t* sorted_route, int32_t* inverse, int32_t* sorted_expert,
+                    int32_t* sorted_token, float* sorted_score, uint32_t* route_offsets, uint32_t* tile_offsets,
+                    int32_t* tile_expert, int32_t* tile_start, int32_t* tile_len, int64_t capacity, uint32_t* status,
+                    void* workspace, hipStream_t st) {
+  RoutePlanArgs a{};
+  a.expert_ids = expert_ids;
+  a.scores = scores;
+  a.routes = routes;
+  a.top_k = static_cast<int>(top_k);
+  a.experts = static_cast<int>(experts);
+  a.tile_rows = static_cast<int>(tile_rows);
+  a.blocks = cdiv(routes, 256);
+  a.capacity = capacity;
+  a.block_counts = static_cast<unsigned*>(workspace);
+  a.block_invalid = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(workspace) +
+                                                round_up(sizeof(unsigned) * std::max<int64_t>(a.blocks, 1) * experts));
+  a.sorted_route = sorted_route;
+  a.inverse = inverse;
+  a.sorted_expert = sorted_expert;
+  a.sorted_token = sorted_token;
+  a.sorted_score = sorted_score;
+  a.route_offsets = route_offsets;
+  a.tile_offsets = tile_offsets;
+  a.tile_expert = tile_expert;
+  a.tile_start = tile_start;
+  a.tile_len = tile_len;
+  a.status = status;
+  HIP_TRY(launch_route_plan(a, st), "route plan launch");
+  return GLM53_OK;
+}
+
+}  // namespace
+
+int glm53_route_plan(const int32_t* expert_ids, const float* scores, int64_t routes, int64_t top_k, int64_t experts,
+                     int64_t tile_rows, int32_t* sorted_route, int32_t* inverse, int32_t* sorted_expert,
+                     int32_t* sorted_token, float* sorted_score, uint32_t* route_offsets, uint32_t* tile_offsets,
+                     int32_t* tile_expert, int32_t* tile_start, int32_t* tile_len, int64_t capacity, uint32_t* status,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  CHECK_ARG(routes >= 0 && top_k > 0 && experts > 0 && experts <= kPlanMaxExperts && tile_rows > 0,
+            "invalid route plan dimensions");
+  CHECK_ARG(routes < (int64_t(1) << 31), "too many routes");
+  CHECK_ARG(capacity >= cdiv(routes, tile_rows) + experts, "descriptor capacity %lld < ceil(routes/tile)+experts",
+            (long long)capacity);
+  CHECK_ARG(workspace && workspace_bytes >= glm53_route_plan_workspace_bytes(routes, experts),
+            "route plan workspace too small");
+  CHECK_ARG(sorted_route && inverse && sorted_expert && sorted_token && route_offsets && tile_offsets && tile_expert &&
+                tile_start && tile_len && status && (routes == 0 || expert_ids),
+            "null pointer argument");
+  CHECK_ARG(scores == nullptr || sorted_score != nullptr, "sorted_score is null");
+  return route_plan_impl(expert_ids, scores, routes, top_k, experts, tile_rows, sorted_route, inverse, sorted_expert,
+                         sorted_token, sorted_score, route_offsets, tile_offsets, tile_expert, tile_start, tile_len,
+                         capacity, status, workspace, S(stream));
+}
+
+size_t glm53_grouped_linear_workspace_bytes(int64_t act_rows, int64_t K) {
+  if (K % 128 != 0) return 0;
+  return split_bytes(act_rows, K) + 256;
+}
+
+int glm53_grouped_linear(const void* x, int64_t act_rows, const int32_t* row_index, int64_t routes, int64_t K,
+                         const int32_t* tile_expert, const int32_t* tile_start, const int32_t* tile_len,
+                         int64_t descriptors, const uint8_t* weight, const float* scale_inv,
+                         const int32_t* code_flags, int64_t experts, int64_t N, void* y, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0,
+            "grouped path requires block-aligned projection dimensions; got out=%lld, in=%lld", (long long)N,
+            (long long)K);
+  CHECK_ARG(routes >= 0 && act_rows >= 0 && descriptors >= 0 && experts > 0, "invalid dimensions");
+  if (routes == 0) return GLM53_OK;
+  CHECK_ARG(x && weight && scale_inv && y && tile_expert && tile_start && tile_len, "null pointer argument");
+  CHECK_ARG(aligned(weight, 16), "weight must be 16-byte aligned");
+  CHECK_ARG(workspace && workspace_bytes >= glm53_grouped_linear_workspace_bytes(act_rows, K),
+            "grouped linear workspace too small");
+  hipStream_t st = S(stream);
+  SplitBuf b = carve_split(workspace, act_rows, K);
+  if (code_flags == nullptr) {
+    int32_t* flag = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + split_bytes(act_rows, K));
+    HIP_TRY(launch_scan_480(weight, experts * N * K, flag, true, st), "scan launch");
+    code_flags = flag;
+  }
+  HIP_TRY(split(x, act_rows, K, b, st), "split launch");
+  GroupedGemmArgs g{};
+  g.fixup = code_flags;
+  g.a_hi = b.hi;
+  g.a_lo = b.lo;
+  g.a_scale = b.scale;
+  g.a_row_index = row_index;
+  g.K = K;
+  g.routes = routes;
+  g.tile_expert = tile_expert;
+  g.tile_start = tile_start;
+  g.tile_len = tile_len;
+  g.experts = experts;
+  g.weight = weight;
+  g.w_expert_stride = N * K;
+  g.scale = scale_inv;
+  g.s_expert_stride = cdiv(N, 128) * (K / 128);
+  g.s_cols = K / 128;
+  g.N = N;
+  g.out = static_cast<uint16_t*>(y);
+  g.out_row_stride = N;
+  HIP_TRY(launch_grouped_gemm(g, GEMM_PLAIN, descriptors, st), "grouped gemm launch");
+  return GLM53_OK;
+}
+
+int glm53_activate_gate_up(const void* gate_up, int64_t rows, int64_t intermediate, float limit, void* out,
+                           void* stream) {
+  CHECK_ARG(rows >= 0 && intermediate > 0, "invalid dimensions");
+  if (rows == 0) return GLM53_OK;
+  CHECK_ARG(gate_up && out, "null pointer argument");
+  SwigluArgs a{};
+  a.gate = static_cast<const uint16_t*>(gate_up);
+  a.up = static_cast<const uint16_t*>(gate_up) + intermediate;
+  a.gate_row_stride = 2 * intermediate;
+  a.up_row_stride = 2 * intermediate;
+  a.rows = rows;
+  a.cols = intermediate;
+  a.limit = limit;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_row_stride = intermediate;
+  HIP_TRY(launch_swiglu(a, S(stream)), "swiglu launch");
+  return GLM53_OK;
+}
+
+int glm53_restore_and_reduce(const void* sorted_out, const float* sorted_score, const int32_t* inverse, int64_t tokens,
+                             int64_t top_k, int64_t H, const void* shared, void* out, void* stream) {
+  CHECK_ARG(tokens >= 0 && top_k > 0 && top_k <= kMaxReduceTopK && H > 0, "invalid dimensions");
+  if (tokens == 0) return GLM53_OK;
+  CHECK_ARG(sorted_out && sorted_score && inverse && out, "null pointer argument");
+  ReduceArgs a{};
+  a.route_out = static_cast<const uint16_t*>(sorted_out);
+  a.inverse = inverse;
+  a.sorted_score = sorted_score;
+  a.shared = static_cast<const uint16_t*>(shared);
+  a.tokens = tokens;
+  a.H = H;
+  a.top_k = static_cast<int>(top_k);
+  a.out = static_cast<uint16_t*>(out);
+  HIP_TRY(launch_reduce(a, false, S(stream)), "reduce launch");
+  return GLM53_OK;
+}
+
+int glm53_direct_order_reduce(const void* sorted_out, const int32_t* inverse, const int32_t* expert_ids,
+                              const float* scores, int64_t tokens, int64_t top_k, int64_t H, const void* shared,
+                              void* out, void* stream) {
+  CHECK_ARG(tokens >= 0 && top_k > 0 && top_k <= kMaxReduceTopK && H > 0, "invalid dimensions");
+  if (tokens == 0) return GLM53_OK;
+  CHECK_ARG(sorted_out && inverse && expert_ids && scores && out, "null pointer argument");
+  ReduceArgs a{};
+  a.route_out = static_cast<const uint16_t*>(sorted_out);
+  a.inverse = inverse;
+  a.route_score = scores;
+  a.expert_ids = expert_ids;
+  a.shared = static_cast<const uint16_t*>(shared);
+  a.tokens = tokens;
+  a.H = H;
+  a.top_k = static_cast<int>(top_k);
+  a.out = static_cast<uint16_t*>(out);
+  HIP_TRY(launch_reduce(a, true, S(stream)), "reduce launch");
+  return GLM53_OK;
+}
+
+// ------------------------------------------------------- prefill plan ------
+
+struct glm53_prefill_plan {
+  int64_t H, I, Is, E, k, max_tokens;
+  float limit;
+  int64_t capacity_max;
+  void* arena = nullptr;
+  // router
+  float* xf = nullptr;
+  float* logits = nullptr;
+  int32_t* ids = nullptr;
+  float* scores = nullptr;
+  // activations
+  SplitBuf xq{};
+  SplitBuf hq{};
+  SplitBuf sq{};
+  // route plan
+  void* plan_ws = nullptr;
+  int32_t *sorted_route = nullptr, *inverse = nullptr, *sorted_expert = nullptr, *sorted_token = nullptr;
+  float* sorted_score = nullptr;
+  uint32_t *route_offsets = nullptr, *tile_offsets = nullptr, *status = nullptr;
+  int32_t *tile_expert = nullptr, *tile_start = nullptr, *tile_len = nullptr;
+  // intermediates
+  uint16_t* h = nullptr;         // [R, I]
+  uint16_t* down = nullptr;      // [R, H]
+  uint16_t* hs = nullptr;        // [T, Is]
+  uint16_t* shared_out = nullptr;  // [T, H]
+  int32_t* flags = nullptr;        // [4] scanned code flags: bank, shared gate/up/down
+  int64_t last_tokens = 0;
+};
+
+int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate, int64_t experts,
+                              int64_t top_k, int64_t max_tokens, float swiglu_limit, glm53_prefill_plan** out) {
+  CHECK_ARG(out != nullptr, "out is null");
+  *out = nullptr;
+  CHECK_ARG(hidden > 0 && hidden % 128 == 0 && intermediate > 0 && intermediate % 128 == 0,
+            "grouped path requires block-aligned projection dimensions; got hidden=%lld, intermediate=%lld",
+            (long long)hidden, (long long)intermediate);
+  CHECK_ARG(shared_intermediate >= 0 && shared_intermediate % 128 == 0, "shared intermediate must be a multiple of 128");
+  CHECK_ARG(experts > 0 && experts <= kPlanMaxExperts, "experts must be in [1, %d]", kPlanMaxExperts);
+  CHECK_ARG(top_k > 0 && top_k <= kMaxTopK && top_k <= experts, "top_k must be in [1, %d]", kMaxTopK);
+  CHECK_ARG(max_tokens > 0 && max_tokens * top_k < (int64_t(1) << 31), "invalid max_tokens");
+  auto* p = new glm53_prefill_plan();
+  p->H = hidden;
+  p->I = intermediate;
+  p->Is = shared_intermediate;
+  p->E = experts;
+  p->k = top_k;
+  p->max_tokens = max_tokens;
+  p->limit = swiglu_limit;
+  const int64_t T = max_tokens, R = T * top_k, Ism = std::max<int64_t>(shared_intermediate, 128);
+  p->capacity_max = cdiv(R, kGroupedTileRows) + experts;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += round_up(bytes);
+    return o;
+  };
+  size_t o_xf = take(4 * T * hidden), o_logits = take(4 * T * experts), o_ids = take(4 * R), o_scores = take(4 * R);
+  size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(R, intermediate)), o_sq = take(split_bytes(T, Ism));
+  size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
+  size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
+  size_t o_ro = take(4 * (experts + 1)), o_to = take(4 * (experts + 1)), o_status = take(8);
+  size_t o_te = take(4 * p->capacity_max), o_ts = take(4 * p->capacity_max), o_tl = take(4 * p->capacity_max);
+  size_t o_h = take(2 * R * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
+  size_t o_so = take(2 * T * hidden), o_flags = take(16);
+  hipError_t e = hipMalloc(&p->arena, off);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "prefill plan hipMalloc");
+  }
+  e = hipMemset(p->arena, 0, off);
+  if (e != hipSuccess) {
+    (void)hipFree(p->arena);
+    delete p;
+    return hip_fail(e, "prefill plan hipMemset");
+  }
+  uint8_t* b = static_cast<uint8_t*>(p->arena);
+  p->xf = reinterpret_cast<float*>(b + o_xf);
+  p->logits = reinterpret_cast<float*>(b + o_logits);
+  p->ids = reinterpret_cast<int32_t*>(b + o_ids);
+  p->scores = reinterpret_cast<float*>(b + o_scores);
+  p->xq = carve_split(b + o_xq, T, hidden);
+  p->hq = carve_split(b + o_hq, R, intermediate);
+  p->sq = carve_split(b + o_sq, T, Ism);
+  p->plan_ws = b + o_pws;
+  p->sorted_route = reinterpret_cast<int32_t*>(b + o_sr);
+  p->inverse = reinterpret_cast<int32_t*>(b + o_inv);
+  p->sorted_expert = reinterpret_cast<int32_t*>(b + o_se);
+  p->sorted_token = reinterpret_cast<int32_t*>(b + o_st);
+  p->sorted_score = reinterpret_cast<float*>(b + o_ss);
+  p->route_offsets = reinterpret_cast<uint32_t*>(b + o_ro);
+  p->tile_offsets = reinterpret_cast<uint32_t*>(b + o_to);
+  p->status = reinterpret_cast<uint32_t*>(b + o_status);
+  p->tile_expert = reinterpret_cast<int32_t*>(b + o_te);
+  p->tile_start = reinterpret_cast<int32_t*>(b + o_ts);
+  p->tile_len = reinterpret_cast<int32_t*>(b + o_tl);
+  p->h = reinterpret_cast<uint16_t*>(b + o_h);
+  p->down = reinterpret_cast<uint16_t*>(b + o_down);
+  p->hs = reinterpret_cast<uint16_t*>(b + o_hs);
+  p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
+  p->flags = reinterpret_cast<int32_t*>(b + o_flags);
+  *out = p;
+  return GLM53_OK;
+}
+
+void glm53_prefill_plan_destroy(glm53_prefill_plan* plan) {
+  if (plan == nullptr) return;
+  if (plan->arena) (void)hipFree(plan->arena);
+  delete plan;
+}
+
+int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                      const glm53_router* router, const void* x, int64_t tokens, const int32_t* expert_ids,
+                      const float* scores, int32_t reduction, void* out, void* stream) {
+  CHECK_ARG(p != nullptr, "plan is null");
+  CHECK_ARG(tokens >= 0 && tokens <= p->max_tokens, "tokens %lld outside [0, %lld]", (long long)tokens,
+            (long long)p->max_tokens);
+  CHECK_ARG(reduction == GLM53_REDUCE_GROUPED || reduction == GLM53_REDUCE_DIRECT, "unknown reduction %d", reduction);
+  int rc = check_bank(bank, p->H, p->I, p->E);
+  if (rc) return rc;
+  if (shared != nullptr) {
+    CHECK_ARG(p->Is > 0, "plan was created without a shared expert");
+    if ((rc = check_linear(shared->gate, p->Is, p->H, "shared gate"))) return rc;
+    if ((rc = check_linear(shared->up, p->Is, p->H, "shared up"))) return rc;
+    if ((rc = check_linear(shared->down, p->H, p->Is, "shared down"))) return rc;
+    CHECK_ARG(aligned(shared->gate.weight, 16) && aligned(shared->up.weight, 16) && aligned(shared->down.weight, 16),
+              "shared weights must be 16-byte aligned");
+  }
+  CHECK_ARG(aligned(bank->gate_up_weight, 16) && aligned(bank->down_weight, 16), "bank weights must be 16-byte aligned");
+  if (expert_ids == nullptr) {
+    if ((rc = check_router(router, p->H, p->E, p->k))) return rc;
+  } else {
+    CHECK_ARG(scores != nullptr, "scores are required with expert_ids");
+  }
+  p->last_tokens = tokens;
+  if (tokens == 0) return GLM53_OK;
+  CHECK_ARG(x && out, "null pointer argument");
+  hipStream_t st = S(stream);
+  const int64_t T = tokens, k = p->k, R = T * k, H = p->H, I = p->I, Is = p->Is, E = p->E;
+  const int64_t SC = H / 128, SR = I / 128, SI = I / 128;
+  const int32_t* ids = expert_ids;
+  const float* sc = scores;
+  if (ids == nullptr) {
+    HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), p->xf, T * H, st), "widen launch");
+    if ((rc = router_logits(p->xf, router->weight, p->logits, T, H, E, st))) return rc;
+    if ((rc = topk(p->logits, router, T, p->ids, p->scores, st))) return rc;
+    ids = p->ids;
+    sc = p->scores;
+  } else {
+    HIP_TRY(hipMemcpyAsync(p->ids, expert_ids, 4 * R, hipMemcpyDeviceToDevice, st), "copy ids");
+    HIP_TRY(hipMemcpyAsync(p->scores, scores, 4 * R, hipMemcpyDeviceToDevice, st), "copy scores");
+  }
+  // 0. 0x7F/0xFF code flags of every weight the MFMA reads (scan when absent)
+  const int32_t* bank_flag = bank->code_flags;
+  if (bank_flag == nullptr) {
+    HIP_TRY(launch_scan_480(bank->gate_up_weight, E * 2 * I * H, p->flags, true, st), "scan bank");
+    HIP_TRY(launch_scan_480(bank->down_weight, E * H * I, p->flags + 1, true, st), "scan bank");
+    bank_flag = p->flags;
+  }
+  // shared gate and up share one MFMA call, so their flags are OR-ed
+  const int32_t* shared_gu_flag = nullptr;
+  const int32_t* shared_down_flag = nullptr;
+  if (shared != nullptr) {
+    int32_t* fgu = p->flags + 2;
+    if (shared->gate.code_flags != nullptr && shared->up.code_flags != nullptr) {
+      HIP_TRY(launch_or_flags(fgu, shared->gate.code_flags, shared->up.code_flags, st), "or flags");
+    } else {
+      HIP_TRY(launch_scan_480(shared->gate.weight, Is * H, fgu, true, st), "scan shared gate");
+      HIP_TRY(launch_scan_480(shared->up.weight, Is * H, fgu, false, st), "scan shared up");
+    }
+    shared_gu_flag = fgu;
+    shared_down_flag = shared->down.code_flags;
+    if (shared_down_flag == nullptr) {
+      HIP_TRY(launch_scan_480(shared->down.weight, H * Is, p->flags + 3, true, st), "scan shared down");
+      shared_down_flag = p->flags + 3;
+    }
+  }
+  // 1. activations -> exact hi/lo E4M3 split
+  HIP_TRY(split(x, T, H, p->xq, st), "split x");
+  // 2. expert-sorted route plan
+  const int64_t cap = cdiv(R, kGroupedTileRows) + E;
+  if ((rc = route_plan_impl(ids, sc, R, k, E, kGroupedTileRows, p->sorted_route, p->inverse, p->sorted_expert,
+                            p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,
+                            p->tile_start, p->tile_len, cap, p->status, p->plan_ws, st)))
+    return rc;
+  // 3. grouped gate/up + SwiGLU (token rows gathered through sorted_token)
+  GroupedGemmArgs g{};
+  g.a_hi = p->xq.hi;
+  g.a_lo = p->xq.lo;
+  g.a_scale = p->xq.scale;
+  g.a_row_index = p->sorted_token;
+  g.K = H;
+  g.routes = R;
+  g.tile_expert = p->tile_expert;
+  g.tile_start = p->tile_start;
+  g.tile_len = p->tile_len;
+  g.experts = E;
+  g.weight = bank->gate_up_weight;
+  g.weight_up = bank->gate_up_weight + I * H;
+  g.w_expert_stride = 2 * I * H;
+  g.scale = bank->gate_up_scale_inv;
+  g.scale_up = bank->gate_up_scale_inv + SR * SC;
+  g.s_expert_stride = 2 * SR * SC;
+  g.s_cols = SC;
+  g.N = I;
+  g.limit = p->limit;
+  g.out = p->h;
+  g.out_row_stride = I;
+  g.fixup = bank_flag;
+  HIP_TRY(launch_grouped_gemm(g, GEMM_SWIGLU, cap, st), "grouped gate/up launch");
+  // 4. hidden -> split, 5. grouped down
+  HIP_TRY(split(p->h, R, I, p->hq, st), "split hidden");
+  GroupedGemmArgs d{};
+  d.a_hi = p->hq.hi;
+  d.a_lo = p->hq.lo;
+  d.a_scale = p->hq.scale;
+  d.K = I;
+  d.routes = R;
+  d.tile_expert = p->tile_expert;
+  d.tile_start = p->tile_start;
+  d.tile_len = p->tile_len;
+  d.experts = E;
+  d.weight = bank->down_weight;
+  d.w_expert_stride = H * I;
+  d.scale = bank->down_scale_inv;
+  d.s_expert_stride = (H / 128) * SI;
+  d.s_cols = SI;
+  d.N = H;
+  d.out = p->down;
+  d.out_row_stride = H;
+  d.fixup = bank->code_flags != nullptr ? bank->code_flags : p->flags + 1;
+  HIP_TRY(launch_grouped_gemm(d, GEMM_PLAIN, cap, st), "grouped down launch");
+  // 6. shared expert as a dense M = T GEMM pair
+  const uint16_t* shared_add = nullptr;
+  if (shared != nullptr) {
+    GroupedGemmArgs sg{};
+    sg.a_hi = p->xq.hi;
+    sg.a_lo = p->xq.lo;
+    sg.a_scale = p->xq.scale;
+    sg.K = H;
+    sg.routes = T;
+    sg.experts = 1;
+    sg.weight = shared->gate.weight;
+    sg.weight_up = shared->up.weight;
+    sg.scale = shared->gate.scale_inv;
+    sg.scale_up = shared->up.scale_inv;
+    sg.s_cols = SC;
+    sg.N = Is;
+    sg.limit = p->limit;
+    sg.out = p->hs;
+    sg.out_row_stride = Is;
+    sg.fixup = shared_gu_flag;
+    HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, kGroupedTileRows), st), "shared gate/up launch");
+    HIP_TRY(split(p->hs, T, Is, p->sq, st), "split shared hidden");
+    GroupedGemmArgs sd{};
+    sd.a_hi = p->sq.hi;
+    sd.a_lo = p->sq.lo;
+    sd.a_scale = p->sq.scale;
+    sd.K = Is;
+    sd.routes = T;
+    sd.experts = 1;
+    sd.weight = shared->down.weight;
+    sd.scale = shared->down.scale_inv;
+    sd.s_cols = Is / 128;
+    sd.N = H;
+    sd.out = p->shared_out;
+    sd.out_row_stride = H;
+    sd.fixup = shared_down_flag;
+    HIP_TRY(launch_grouped_gemm(sd, GEMM_PLAIN, cdiv(T, kGroupedTileRows), st), "shared down launch");
+    shared_add = p->shared_out;
+  }
+  // 7. combine
+  ReduceArgs r{};
+  r.route_out = p->down;
+  r.inverse = p->inverse;
+  r.sorted_score = p->sorted_score;
+  r.route_score = p->scores;
+  r.expert_ids = p->ids;
+  r.shared = shared_add;
+  r.tokens = T;
+  r.H = H;
+  r.top_k = static_cast<int>(k);
+  r.out = static_cast<uint16_t*>(out);
+  HIP_TRY(launch_reduce(r, reduction == GLM53_REDUCE_DIRECT, st), "reduce launch");
+  return GLM53_OK;
+}
+
+int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes) {
+  CHECK_ARG(plan && invalid_routes, "null pointer argument");
+  if (plan->last_tokens == 0) {
+    *invalid_routes = 0;
+    return GLM53_OK;
+  }
+  HIP_TRY(hipMemcpy(invalid_routes, plan->status, sizeof(uint32_t), hipMemcpyDeviceToHost), "read status");
+  return GLM53_OK;
+}
+
+int glm53_prefill_plan_scratch(glm53_prefill_plan* plan, int32_t which, void** ptr, size_t* bytes) {
+  CHECK_ARG(plan && ptr && bytes, "null pointer argument");
+  const int64_t R = plan->last_tokens * plan->k;
+  switch (which) {
+    case 0:
+      *ptr = plan->ids;
+      *bytes = 4 * R;
+      return GLM53_OK;
+    case 1:
+      *ptr = plan->scores;
+      *bytes = 4 * R;
+      return GLM53_OK;
+    case 2:
+      *ptr = plan->sorted_route;
+      *bytes = 4 * R;
+      return GLM53_OK;
+    case 3:
+      *ptr = plan->tile_expert;
+      *bytes = 4 * 3 * plan->capacity_max;
+      return GLM53_OK;
+    default:
+      return fail(GLM53_INVALID_ARGUMENT, "unknown scratch id %d", which);
+  }
+}
+
+int glm53_sigmoid_bf16(const void* gate, int64_t n, void* out, void* stream) {
+  CHECK_ARG(n >= 0 && (n == 0 || (gate && out)), "invalid arguments");
+  HIP_TRY(launch_sigmoid_bf16(static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), n, S(stream)),
+          "sigmoid launch");
+  return GLM53_OK;
+}
+
+// --------------------------------------------------------- synthetic ------
+
+int glm53_synth_fp8(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, uint64_t seed, float std,
+                    void* stream) {
+  CHECK_ARG(rows >= 0 && cols >= 0, "invalid dimensions");
+  if (rows == 0 || cols == 0) return GLM53_OK;
+  CHECK_ARG(codes && scale_inv, "null pointer argument");
+  SynthFp8Args a{codes, scale_inv, rows, cols, seed, std};
+  HIP_TRY(launch_synth_fp8(a, S(stream)), "synth launch");
+  return GLM53_OK;
+}
+
+int glm53_synth_f32(float* out, int64_t n, uint64_t seed, float std, float lo, float hi, int32_t uniform, void* stream) {
+  CHECK_ARG(n >= 0 && (n == 0 || out), "invalid arguments");
+  HIP_TRY(launch_synth_f32(out, n, seed, std, lo, hi, uniform, S(stream)), "synth launch");
+  return GLM53_OK;
+}
+
+int glm53_synth_bf16(void* out, int64_t n, uint64_t seed, float std, void* stream) {
+  CHECK_ARG(n >= 0 && (n == 0 || out), "invalid arguments");
+  HIP_TRY(launch_synth_bf16(static_cast<uint16_t*>(out), n, seed, std, S(stream)), "synth launch");
+  return GLM53_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,146 @@
+// Device helpers shared by every kernel of the FP8 block-scaled MoE path.
+// gfx950 (CDNA4) only: 64-lane wavefronts, DPP cross-lane moves, f16 dot2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm53 {
+
+constexpr int kBlock = 128;   // FP8 scale block edge (weight_scale_inv is per 128x128)
+constexpr int kWave = 64;
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------ BF16 ---
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even FP32 -> BF16 (the Metal/MLX bfloat conversion).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ------------------------------------------------------------------ E4M3 ---
+//
+// Exact E4M3 -> FP16 decode of two bytes packed into one dword.  With the
+// E4M3 exponent field e (bias 7) and mantissa m moved into FP16's exponent
+// (bias 15) and mantissa fields, the FP16 value is exactly 2^-8 times the
+// E4M3 value for every code, subnormals included (e=0 lands on FP16
+// subnormals m*2^-17), and the 0x7F/0xFF codes decode to +-480/256 exactly as
+// the reference's LUT does (no NaN code).  The 2^8 is folded into the block
+// scale.  Three or four VALU ops per pair, no table.
+//
+// v = [b3 b2 b1 b0]:   odd pair -> (b1, b3)   even pair -> (b0, b2)
+__device__ __forceinline__ uint32_t e4m3x2_odd_to_f16x2(uint32_t v) {
+  return ((v >> 1) & 0x3F803F80u) | (v & 0x80008000u);
+}
+__device__ __forceinline__ uint32_t e4m3x2_even_to_f16x2(uint32_t v) {
+  return ((v << 7) & 0x3F803F80u) | ((v << 8) & 0x80008000u);
+}
+
+__device__ __forceinline__ float dot2(uint32_t w_f16x2, uint32_t x_f16x2, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w_f16x2),
+                                __builtin_bit_cast(half2_t, x_f16x2), acc, false);
+}
+
+// Partial dot product of 4 weight bytes with 4 activations held as the FP16
+// pairs (x0, x2) and (x1, x3) (the same byte pairing as the decode above).
+__device__ __forceinline__ float dot4_e4m3(uint32_t w4, uint32_t x02, uint32_t x13, float acc) {
+  acc = dot2(e4m3x2_even_to_f16x2(w4), x02, acc);
+  return dot2(e4m3x2_odd_to_f16x2(w4), x13, acc);
+}
+
+// Pack activations (already scaled into FP16 range) as (xa, xb) FP16 pair.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  half2_t h = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Power-of-two exponent that maps |x| <= amax into [2^14, 2^15): activations
+// divided by 2^shift are exact in FP16 (BF16 has 8 significant bits, FP16 11)
+// unless they sit more than 2^28 below the lane's maximum.
+__device__ __forceinline__ int f16_shift_for(float amax) {
+  if (!(amax > 0.0f) || !isfinite(amax)) return 0;
+  int e = ilogbf(amax);
+  return e - 14;
+}
+
+// ---------------------------------------------------------- reductions ---
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over all 64 lanes; every lane gets the total.  DPP within 16-lane
+// rows, then the four row totals through readlane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// ------------------------------------------------------------- SwiGLU ---
+//
+// MLX BF16 sigmoid as the reference evaluates it (every step rounded to
+// BF16): tail = 1 / (1 + exp(|g|)); sigma = g < 0 ? tail : 1 - tail.  MLX's
+// Metal fast::exp and the correctly rounded exponential agree, after BF16
+// rounding, on every finite BF16 g in [-10, 10] except g = -6.84375
+// (0xC0DB): exp(6.84375) = 938.0000478 lies 5e-5 above the BF16 midpoint
+// 938, and fast::exp rounds to 936, giving sigma = 0x3A8C.  That point is
+// reproduced explicitly; expf is accurate to well inside 5e-5 there.
+__device__ __forceinline__ float sigmoid_mlx_bf16(uint16_t gbits) {
+  if (gbits == 0xC0DBu) return bf16_to_f32(0x3A8Cu);
+  float g = bf16_to_f32(gbits);
+  float e = bf16_round(expf(fabsf(g)));
+  float d = bf16_round(1.0f + e);
+  float tail = bf16_round(1.0f / d);
+  return g < 0.0f ? tail : bf16_round(1.0f - tail);
+}
+
+// Clamped SwiGLU with the reference's exact rounding points:
+// g' = T(min(T(g), L)); u' = T(clip(T(u), -L, L)); h = T(T(g' * s(g')) * u').
+// Inputs are the FP32 accumulator values before the projection's BF16 store.
+__device__ __forceinline__ uint16_t swiglu_mlx(float gate_acc, float up_acc, float limit) {
+  float g = bf16_round(gate_acc);
+  float u = bf16_round(up_acc);
+  float gv = (g < limit) ? g : limit;
+  if (isnan(g)) gv = g;
+  float uv = fminf(fmaxf(u, -limit), limit);
+  if (isnan(u)) uv = u;
+  uint16_t ga = f32_to_bf16(gv);
+  float gaf = bf16_to_f32(ga);
+  float ua = bf16_round(uv);
+  float silu = bf16_round(gaf * sigmoid_mlx_bf16(ga));
+  return f32_to_bf16(silu * ua);
+}
+
+}  // namespace glm53

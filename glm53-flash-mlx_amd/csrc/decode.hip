@@ -1,0 +1,729 @@
+// Batch-1 decode kernels for the FP8 block-scaled packed MoE layer.
+//
+// Streaming GEMV design for CDNA4: one wavefront owns a run of consecutive
+// weight rows; each lane owns a fixed slice of the reduction dimension, so
+// its activations are loaded once (into registers, as exact FP16 pairs) and
+// every weight row is read with 16- or 8-byte vector loads that coalesce into
+// 1 KB / 512 B contiguous segments per wave instruction.  E4M3 bytes are
+// decoded in registers (common.h) and contracted with v_dot2_f32_f16; the
+// 128-column block scale is applied once per chunk.  Row totals come from a
+// DPP wave reduction.  Nothing is ever expanded to a BF16 weight copy.
+//
+// Reference semantics: packed.py:100-179 (fused gate/up/SwiGLU, down,
+// weighted reduction), packed.py:181-235 (shared expert), fp8.py:41-116
+// (block_fp8_linear), patch.py:131-142 (FP32 router).
+#include "common.h"
+#include "kernels.h"
+
+namespace glm53 {
+
+// ------------------------------------------------------------ helpers ----
+
+// A lane's activation slice: CH chunks of VB consecutive elements at
+// positions VB*lane + 64*VB*c, held as FP16 pairs (x0,x2),(x1,x3) per 4.
+template <int VB, int CH>
+struct XSlice {
+  uint32_t p[CH][VB / 2];
+  float factor;  // 2^(8 + shift): E4M3->FP16 bias and the activation shift
+};
+
+template <int VB, int CH>
+__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane,
+                                             XSlice<VB, CH>& xs) {
+  float v[CH][VB];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint16_t* src = x + VB * lane + 64 * VB * c;
+#pragma unroll
+    for (int i = 0; i < VB; i += 8) {
+      uint4 q = *reinterpret_cast<const uint4*>(src + i);
+      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c][i + 2 * j] = __uint_as_float(w[j] << 16);
+        v[c][i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int i = 0; i < VB; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+  int shift = f16_shift_for(amax);
+  float down = ldexpf(1.0f, -shift);
+  xs.factor = ldexpf(1.0f, 8 + shift);
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int j = 0; j < VB / 4; ++j) {
+      xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 2] * down);
+      xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 1] * down, v[c][4 * j + 3] * down);
+    }
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// One lane's VB weight bytes of a chunk.  Weights are streamed exactly once
+// per launch, so they are loaded non-temporally (no L2 / MALL retention).
+template <int VB>
+struct WChunk;
+template <>
+struct WChunk<16> {
+  u32x4 q;
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  }
+  __device__ __forceinline__ uint32_t word(int j) const { return q[j]; }
+};
+template <>
+struct WChunk<8> {
+  u32x2 q;
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  }
+  __device__ __forceinline__ uint32_t word(int j) const { return q[j]; }
+};
+
+// Unscaled partial dot of one chunk (VB weight bytes) with the lane's
+// activations of that chunk.
+template <int VB, int CH>
+__device__ __forceinline__ float chunk_dot(const WChunk<VB>& w, const XSlice<VB, CH>& xs, int c) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VB / 4; ++j) acc = dot4_e4m3(w.word(j), xs.p[c][2 * j], xs.p[c][2 * j + 1], acc);
+  return acc;
+}
+
+// Lane partial of row `row` of a [rows, K] E4M3 matrix whose block-scale
+// row is `srow` (a pointer to the row's SC scales).
+template <int VB, int CH>
+__device__ __forceinline__ float row_partial(const WChunk<VB> (&w)[CH], const float* __restrict__ srow,
+                                             const XSlice<VB, CH>& xs, int lane) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float s = srow[(VB * lane + 64 * VB * c) >> 7];
+    acc += chunk_dot<VB, CH>(w[c], xs, c) * s;
+  }
+  return acc * xs.factor;
+}
+
+template <int VB, int CH>
+__device__ __forceinline__ void load_row(WChunk<VB> (&w)[CH], const uint8_t* __restrict__ row, int lane) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) w[c].load(row + VB * lane + 64 * VB * c);
+}
+
+__device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
+  return e < 0 || static_cast<int64_t>(e) >= experts;
+}
+
+// --------------------------------------------- fused routed gate/up/SwiGLU --
+//
+// packed.py:100-166 for the top_k selected experts (slots 0..k-1) plus, as
+// slot k, packed.py:181-235 for the shared expert.  One wavefront computes
+// `rows_per_wave` consecutive intermediate rows r of one slot: it streams
+// gate row r and up row r (the bank's rows r and I + r), and lane 0 stores
+// h = SwiGLU(T(gate), T(up)) with the reference's rounding sequence.
+template <int VB, int CH>
+__global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int slots_routed = a.top_k;
+  const int bid = blockIdx.x;
+  int slot, chunk;
+  int64_t rows;
+  if (bid < slots_routed * a.wgs_per_slot) {
+    slot = bid / a.wgs_per_slot;
+    chunk = bid % a.wgs_per_slot;
+    rows = a.intermediate;
+  } else {
+    slot = slots_routed;
+    chunk = bid - slots_routed * a.wgs_per_slot;
+    rows = a.shared_intermediate;
+  }
+  const int64_t r0 = (static_cast<int64_t>(chunk) * 4 + wave) * a.rows_per_wave;
+  if (r0 >= rows) return;
+  const int64_t K = a.hidden;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+
+  const uint8_t* gate_w;
+  const uint8_t* up_w;
+  const float* gate_s;
+  const float* up_s;
+  uint16_t* out;
+  if (slot < slots_routed) {
+    int32_t e = a.expert_ids[slot];
+    out = a.hidden_out + static_cast<int64_t>(slot) * a.intermediate;
+    if (bad_expert(e, a.experts)) {
+      if (lane == 0) {
+        atomicOr(a.error_flag, 1);
+        for (int64_t r = r0; r < r0 + a.rows_per_wave && r < rows; ++r) out[r] = 0x7FC0u;
+      }
+      return;
+    }
+    const int64_t SR = (a.intermediate + kBlock - 1) / kBlock;
+    gate_w = a.gate_up_weight + static_cast<int64_t>(e) * 2 * a.intermediate * K;
+    up_w = gate_w + a.intermediate * K;
+    gate_s = a.gate_up_scale + static_cast<int64_t>(e) * 2 * SR * SC;
+    up_s = gate_s + SR * SC;
+  } else {
+    out = a.hidden_out + static_cast<int64_t>(slots_routed) * a.intermediate;
+    gate_w = a.shared_gate_weight;
+    up_w = a.shared_up_weight;
+    gate_s = a.shared_gate_scale;
+    up_s = a.shared_up_scale;
+  }
+
+  XSlice<VB, CH> xs;
+  load_x_slice<VB, CH>(a.x, lane, xs);
+
+  const int64_t r_end = (r0 + a.rows_per_wave < rows) ? r0 + a.rows_per_wave : rows;
+  int64_t r = r0;
+  for (; r + 1 < r_end; r += 2) {
+    WChunk<VB> g0[CH], u0[CH], g1[CH], u1[CH];
+    load_row<VB, CH>(g0, gate_w + r * K, lane);
+    load_row<VB, CH>(u0, up_w + r * K, lane);
+    load_row<VB, CH>(g1, gate_w + (r + 1) * K, lane);
+    load_row<VB, CH>(u1, up_w + (r + 1) * K, lane);
+    float pg0 = row_partial<VB, CH>(g0, gate_s + (r >> 7) * SC, xs, lane);
+    float pu0 = row_partial<VB, CH>(u0, up_s + (r >> 7) * SC, xs, lane);
+    float pg1 = row_partial<VB, CH>(g1, gate_s + ((r + 1) >> 7) * SC, xs, lane);
+    float pu1 = row_partial<VB, CH>(u1, up_s + ((r + 1) >> 7) * SC, xs, lane);
+    float tg0 = wave_sum(pg0), tu0 = wave_sum(pu0);
+    float tg1 = wave_sum(pg1), tu1 = wave_sum(pu1);
+    if (lane == 0) {
+      out[r] = swiglu_mlx(tg0, tu0, a.limit);
+      out[r + 1] = swiglu_mlx(tg1, tu1, a.limit);
+    }
+  }
+  if (r < r_end) {
+    WChunk<VB> g0[CH], u0[CH];
+    load_row<VB, CH>(g0, gate_w + r * K, lane);
+    load_row<VB, CH>(u0, up_w + r * K, lane);
+    float tg0 = wave_sum(row_partial<VB, CH>(g0, gate_s + (r >> 7) * SC, xs, lane));
+    float tu0 = wave_sum(row_partial<VB, CH>(u0, up_s + (r >> 7) * SC, xs, lane));
+    if (lane == 0) out[r] = swiglu_mlx(tg0, tu0, a.limit);
+  }
+}
+
+// ------------------------------------- fused down + reduction + shared add --
+//
+// packed.py:66-98 (down for the k slots), packed.py:168-179 (ordered FP32
+// weighted reduction), fp8.py:254-299 (shared down GEMV) and
+// native_indexer_plan.metal:525-535 (BF16 add), in one launch.  A
+// workgroup of three wavefronts owns `rows_per_wg` output rows h; wave w
+// computes the down dot products of slots w, w+3, w+6 (slot k = shared) for
+// those rows, parks T(dot) in LDS, and the first rows_per_wg lanes then do
+// out[h] = T( T(sum_s T(down[s,h]) * score[s]) + T(shared[h]) ) in slot order.
+template <int VB, int CH>
+__global__ __launch_bounds__(192) void down_reduce_kernel(DownArgs a) {
+  __shared__ float parked[9][kMaxDownRowsPerWg];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t h0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_wg;
+  const int64_t K = a.intermediate;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+  const int64_t SH = (a.hidden + kBlock - 1) / kBlock;
+  const int nslots = a.top_k + (a.shared_down_weight != nullptr ? 1 : 0);
+  const int64_t h_end = (h0 + a.rows_per_wg < a.hidden) ? h0 + a.rows_per_wg : a.hidden;
+
+  for (int slot = wave; slot < nslots; slot += 3) {
+    const uint8_t* w;
+    const float* s;
+    if (slot < a.top_k) {
+      int32_t e = a.expert_ids[slot];
+      if (bad_expert(e, a.experts)) {
+        if (lane == 0) atomicOr(a.error_flag, 1);
+        for (int64_t h = h0; h < h_end; ++h) parked[slot][h - h0] = __builtin_nanf("");
+        continue;
+      }
+      w = a.down_weight + static_cast<int64_t>(e) * a.hidden * K;
+      s = a.down_scale + static_cast<int64_t>(e) * SH * SC;
+    } else {
+      w = a.shared_down_weight;
+      s = a.shared_down_scale;
+    }
+    XSlice<VB, CH> xs;
+    load_x_slice<VB, CH>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, xs);
+    int64_t h = h0;
+    for (; h + 1 < h_end; h += 2) {
+      WChunk<VB> w0[CH], w1[CH];
+      load_row<VB, CH>(w0, w + h * K, lane);
+      load_row<VB, CH>(w1, w + (h + 1) * K, lane);
+      float t0 = wave_sum(row_partial<VB, CH>(w0, s + (h >> 7) * SC, xs, lane));
+      float t1 = wave_sum(row_partial<VB, CH>(w1, s + ((h + 1) >> 7) * SC, xs, lane));
+      if (lane == 0) {
+        parked[slot][h - h0] = bf16_round(t0);
+        parked[slot][h + 1 - h0] = bf16_round(t1);
+      }
+    }
+    if (h < h_end) {
+      WChunk<VB> w0[CH];
+      load_row<VB, CH>(w0, w + h * K, lane);
+      float t0 = wave_sum(row_partial<VB, CH>(w0, s + (h >> 7) * SC, xs, lane));
+      if (lane == 0) parked[slot][h - h0] = bf16_round(t0);
+    }
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < h_end - h0) {
+    float total = 0.0f;
+    for (int slot = 0; slot < a.top_k; ++slot) {
+      total = __fadd_rn(total, __fmul_rn(parked[slot][t], a.scores[slot]));
+    }
+    float routed = bf16_round(total);
+    float result = routed;
+    if (a.shared_down_weight != nullptr) result = __fadd_rn(routed, parked[a.top_k][t]);
+    a.out[h0 + t] = f32_to_bf16(result);
+  }
+}
+
+// ----------------------------------------------------------------- router --
+//
+// patch.py:131-142: logits = x_f32 . W_f32^T (FP32), sigmoid, +bias for the
+// choice, top-k ordered by (choice desc, expert id asc), weights =
+// sigmoid[ids] normalised and scaled (scripts/sweep_grouped_fp8_suffix.py:
+// 84-91).  One workgroup per expert row; the last workgroup to finish (a
+// self-resetting arrival counter) selects the top-k with one wavefront.
+__global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
+  __shared__ float partial[4];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t e = blockIdx.x;
+  const float* w = a.weight + e * a.hidden;
+  float acc = 0.0f;
+  if ((a.hidden & 3) == 0) {
+    for (int64_t k = 4 * static_cast<int64_t>(threadIdx.x); k < a.hidden; k += 1024) {
+      float4 wv = *reinterpret_cast<const float4*>(w + k);
+      uint2 xv = *reinterpret_cast<const uint2*>(a.x + k);
+      acc = fmaf(__uint_as_float(xv.x << 16), wv.x, acc);
+      acc = fmaf(__uint_as_float(xv.x & 0xffff0000u), wv.y, acc);
+      acc = fmaf(__uint_as_float(xv.y << 16), wv.z, acc);
+      acc = fmaf(__uint_as_float(xv.y & 0xffff0000u), wv.w, acc);
+    }
+  } else {
+    for (int64_t k = threadIdx.x; k < a.hidden; k += 256) acc = fmaf(bf16_to_f32(a.x[k]), w[k], acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) partial[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float logit = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    float sig = 1.0f / (1.0f + expf(-logit));
+    a.sigmoid_out[e] = sig;
+    a.choice_out[e] = __fadd_rn(sig, a.bias[e]);
+    __threadfence();
+    unsigned prev = atomicAdd(a.arrivals, 1u);
+    last = (prev == gridDim.x - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!last || wave != 0) return;
+  __threadfence();
+  // One wavefront: top_k rounds of a 64-lane argmax over (choice, -id).
+  // Lane l holds candidates l, l+64, ... in registers; NaN choices rank as
+  // -inf so they are only ever picked after every finite score.
+  const volatile float* choice = a.choice_out;
+  const volatile float* sig = a.sigmoid_out;
+  constexpr int kPerLane = kMaxExperts / 64;
+  float vals[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    int64_t c = lane + 64 * i;
+    float v = c < a.experts ? choice[c] : -__builtin_inff();
+    vals[i] = (v != v) ? -__builtin_inff() : v;
+  }
+  uint32_t taken = 0;
+  float total = 0.0f;
+  float picked[kMaxTopK];
+  int32_t picked_id[kMaxTopK];
+  for (int slot = 0; slot < a.top_k; ++slot) {
+    float best = -__builtin_inff();
+    int32_t best_id = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      int32_t c = lane + 64 * i;
+      bool ok = c < a.experts && !((taken >> i) & 1u);
+      if (ok && (best_id == 0x7fffffff || vals[i] > best || (vals[i] == best && c < best_id))) {
+        best = vals[i];
+        best_id = c;
+      }
+    }
+    // wave argmax: larger value wins, ties go to the smaller id
+    for (int off = 32; off >= 1; off >>= 1) {
+      float ov = __shfl_xor(best, off);
+      int32_t oid = __shfl_xor(best_id, off);
+      if (oid != 0x7fffffff && (best_id == 0x7fffffff || ov > best || (ov == best && oid < best_id))) {
+        best = ov;
+        best_id = oid;
+      }
+    }
+    if (best_id == 0x7fffffff) best_id = 0;
+    if ((best_id & 63) == lane) taken |= 1u << (best_id >> 6);
+    picked_id[slot] = best_id;
+    picked[slot] = sig[best_id];
+    total = __fadd_rn(total, picked[slot]);
+  }
+  if (lane == 0) {
+    for (int slot = 0; slot < a.top_k; ++slot) {
+      float v = picked[slot];
+      if (a.top_k > 1 && a.norm_topk_prob) v = v / total;
+      a.ids_out[slot] = picked_id[slot];
+      a.scores_out[slot] = __fmul_rn(v, a.routed_scaling_factor);
+    }
+    *a.arrivals = 0u;  // self-reset for the next launch on this plan
+  }
+}
+
+// ---------------------------------------------------------- plain GEMV ----
+//
+// fp8.py:41-72 `block_fp8_linear` for one activation row: y[n] = T(sum_k
+// x[k] * LUT[w[n,k]] * s[n/128, k/128]).  Wave w of a workgroup streams
+// rows [rows_per_wave * (4 * block + w), ...).
+template <int VB, int CH>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * a.rows_per_wave;
+  if (n0 >= a.N) return;
+  const int64_t K = a.K;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+  XSlice<VB, CH> xs;
+  load_x_slice<VB, CH>(a.x, lane, xs);
+  const int64_t n_end = (n0 + a.rows_per_wave < a.N) ? n0 + a.rows_per_wave : a.N;
+  int64_t n = n0;
+  for (; n + 3 < n_end; n += 4) {
+    WChunk<VB> w0[CH], w1[CH], w2[CH], w3[CH];
+    load_row<VB, CH>(w0, a.weight + n * K, lane);
+    load_row<VB, CH>(w1, a.weight + (n + 1) * K, lane);
+    load_row<VB, CH>(w2, a.weight + (n + 2) * K, lane);
+    load_row<VB, CH>(w3, a.weight + (n + 3) * K, lane);
+    float t0 = wave_sum(row_partial<VB, CH>(w0, a.scale + (n >> 7) * SC, xs, lane));
+    float t1 = wave_sum(row_partial<VB, CH>(w1, a.scale + ((n + 1) >> 7) * SC, xs, lane));
+    float t2 = wave_sum(row_partial<VB, CH>(w2, a.scale + ((n + 2) >> 7) * SC, xs, lane));
+    float t3 = wave_sum(row_partial<VB, CH>(w3, a.scale + ((n + 3) >> 7) * SC, xs, lane));
+    if (lane == 0) {
+      a.y[n] = f32_to_bf16(t0);
+      a.y[n + 1] = f32_to_bf16(t1);
+      a.y[n + 2] = f32_to_bf16(t2);
+      a.y[n + 3] = f32_to_bf16(t3);
+    }
+  }
+  for (; n < n_end; ++n) {
+    WChunk<VB> w0[CH];
+    load_row<VB, CH>(w0, a.weight + n * K, lane);
+    float t0 = wave_sum(row_partial<VB, CH>(w0, a.scale + (n >> 7) * SC, xs, lane));
+    if (lane == 0) a.y[n] = f32_to_bf16(t0);
+  }
+}
+
+// ------------------------------------------------------ per-token top-k ----
+//
+// Selection half of the router for many tokens (prefill): one wavefront per
+// token reads its FP32 logits row, forms sigmoid and the biased choice, and
+// runs the same (choice desc, id asc) top-k as the decode router.
+__global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= a.tokens) return;
+  const float* row = a.logits + t * a.experts;
+  constexpr int kPerLane = kMaxExperts / 64;
+  float vals[kPerLane];
+  float sigs[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    int64_t c = lane + 64 * i;
+    float sg = 0.0f, v = -__builtin_inff();
+    if (c < a.experts) {
+      sg = 1.0f / (1.0f + expf(-row[c]));
+      v = __fadd_rn(sg, a.bias[c]);
+      if (v != v) v = -__builtin_inff();
+    }
+    sigs[i] = sg;
+    vals[i] = v;
+  }
+  uint32_t taken = 0;
+  float total = 0.0f;
+  float picked[kMaxTopK];
+  int32_t picked_id[kMaxTopK];
+  for (int slot = 0; slot < a.top_k; ++slot) {
+    float best = -__builtin_inff();
+    float best_sig = 0.0f;
+    int32_t best_id = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      int32_t c = lane + 64 * i;
+      bool ok = c < a.experts && !((taken >> i) & 1u);
+      if (ok && (best_id == 0x7fffffff || vals[i] > best || (vals[i] == best && c < best_id))) {
+        best = vals[i];
+        best_id = c;
+        best_sig = sigs[i];
+      }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      float ov = __shfl_xor(best, off);
+      float os = __shfl_xor(best_sig, off);
+      int32_t oid = __shfl_xor(best_id, off);
+      if (oid != 0x7fffffff && (best_id == 0x7fffffff || ov > best || (ov == best && oid < best_id))) {
+        best = ov;
+        best_id = oid;
+        best_sig = os;
+      }
+    }
+    if (best_id == 0x7fffffff) best_id = 0;
+    if ((best_id & 63) == lane) taken |= 1u << (best_id >> 6);
+    picked_id[slot] = best_id;
+    picked[slot] = best_sig;
+    total = __fadd_rn(total, best_sig);
+  }
+  if (lane == 0) {
+    for (int slot = 0; slot < a.top_k; ++slot) {
+      float v = picked[slot];
+      if (a.top_k > 1 && a.norm_topk_prob) v = v / total;
+      a.ids_out[t * a.top_k + slot] = picked_id[slot];
+      a.scores_out[t * a.top_k + slot] = __fmul_rn(v, a.routed_scaling_factor);
+    }
+  }
+}
+
+// BF16 -> FP32 widening of the router input (patch.py:133 x.astype(float32)).
+__global__ void bf16_to_f32_kernel(const uint16_t* x, float* y, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = bf16_to_f32(x[i]);
+}
+
+// ------------------------------------------------------- generic path ----
+//
+// Any-shape block-FP8 linear (fp8.py:41-116 / packed.py:304-387 semantics)
+// for odd widths that the vector fast path cannot tile: groups g select an
+// expert (optional), the activation rows of the group are staged in LDS as
+// FP32, and each wavefront reduces one output row per step with byte loads.
+__global__ __launch_bounds__(256) void linear_generic_kernel(GenericLinearArgs a) {
+  extern __shared__ float xs[];  // [tile_rows][K], tile_rows <= kGenericRows
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t g = blockIdx.y;
+  const int64_t n_base = static_cast<int64_t>(blockIdx.x) * 4 * a.rows_per_wave;
+  const int64_t K = a.K;
+  const uint8_t* w = a.weight;
+  const float* s = a.scale;
+  if (a.expert_ids != nullptr) {
+    int32_t e = a.expert_ids[g];
+    if (bad_expert(e, a.experts)) {
+      if (threadIdx.x == 0) atomicOr(a.error_flag, 1);
+      for (int64_t m = 0; m < a.M; ++m)
+        for (int64_t n = n_base + threadIdx.x; n < n_base + 4 * a.rows_per_wave && n < a.N; n += 256)
+          a.y[g * a.y_group_stride + m * a.y_row_stride + n] = 0x7FC0u;
+      return;
+    }
+    w += static_cast<int64_t>(e) * a.w_expert_stride;
+    s += static_cast<int64_t>(e) * a.s_expert_stride;
+  }
+  w += a.w_row_offset * K;
+  s += a.s_row_offset * a.s_cols;
+  const uint16_t* xg = a.x + g * a.x_group_stride;
+  for (int64_t m0 = 0; m0 < a.M; m0 += a.tile_rows) {
+    const int mt = static_cast<int>((a.M - m0) < a.tile_rows ? (a.M - m0) : a.tile_rows);
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < mt * K; i += 256) {
+      int64_t m = i / K, k = i % K;
+      xs[i] = bf16_to_f32(xg[(m0 + m) * a.x_row_stride + k]);
+    }
+    __syncthreads();
+    for (int rr = 0; rr < a.rows_per_wave; ++rr) {
+      const int64_t n = n_base + static_cast<int64_t>(wave) * a.rows_per_wave + rr;
+      if (n >= a.N) break;
+      float acc[kGenericRows];
+#pragma unroll
+      for (int m = 0; m < kGenericRows; ++m) acc[m] = 0.0f;
+      const uint8_t* wr = w + n * K;
+      const float* sr = s + (n >> 7) * a.s_cols;
+      for (int64_t k = lane; k < K; k += 64) {
+        uint32_t b = wr[k];
+        float wv = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(
+                       ((b & 0x7Fu) << 7) | ((b & 0x80u) << 8)))) * 256.0f * sr[k >> 7];
+#pragma unroll
+        for (int m = 0; m < kGenericRows; ++m)
+          if (m < mt) acc[m] = fmaf(xs[m * K + k], wv, acc[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < kGenericRows; ++m) {
+        float t = wave_sum(acc[m]);
+        if (lane == 0 && m < mt) a.y[g * a.y_group_stride + (m0 + m) * a.y_row_stride + n] = f32_to_bf16(t);
+      }
+    }
+  }
+}
+
+// packed.py:146-163 / grouped_fp8.py:265-270 elementwise SwiGLU on BF16
+// projections (gate row-block / up row-block with independent strides).
+__global__ void swiglu_kernel(SwigluArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= a.rows * a.cols) return;
+  const int64_t r = i / a.cols, c = i % a.cols;
+  float g = bf16_to_f32(a.gate[r * a.gate_row_stride + c]);
+  float u = bf16_to_f32(a.up[r * a.up_row_stride + c]);
+  a.out[r * a.out_row_stride + c] = swiglu_mlx(g, u, a.limit);
+}
+
+// packed.py:168-179: out[h] = T(sum_s float(down[s,h]) * score[s]), FP32
+// products summed in slot order; optional BF16 add of `addend`.
+__global__ void weighted_reduction_kernel(WeightedReductionArgs a) {
+  const int64_t h = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (h >= a.H) return;
+  float total = 0.0f;
+  for (int s = 0; s < a.top_k; ++s)
+    total = __fadd_rn(total, __fmul_rn(bf16_to_f32(a.down[static_cast<int64_t>(s) * a.H + h]), a.scores[s]));
+  float r = bf16_round(total);
+  if (a.addend != nullptr) r = __fadd_rn(r, bf16_to_f32(a.addend[h]));
+  a.out[h] = f32_to_bf16(r);
+}
+
+// The MLX BF16 sigmoid of the SwiGLU epilogue on its own (diagnostic entry
+// point; lets a test pin the device arithmetic against the reference's
+// exhaustive sweep).
+__global__ void sigmoid_bf16_kernel(const uint16_t* g, uint16_t* out, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f32_to_bf16(sigmoid_mlx_bf16(g[i]));
+}
+
+__global__ void add_bf16_kernel(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f32_to_bf16(__fadd_rn(bf16_to_f32(a[i]), bf16_to_f32(b[i])));
+}
+
+// --------------------------------------------------------------- launch ---
+
+template <int VB, int CH>
+static hipError_t launch_gate_up_t(const GateUpArgs& a, hipStream_t st) {
+  int64_t rows_per_wg = 4 * static_cast<int64_t>(a.rows_per_wave);
+  int64_t blocks = static_cast<int64_t>(a.top_k) * a.wgs_per_slot;
+  if (a.shared_gate_weight != nullptr) blocks += (a.shared_intermediate + rows_per_wg - 1) / rows_per_wg;
+  hipLaunchKernelGGL((gate_up_swiglu_kernel<VB, CH>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int VB, int CH>
+static hipError_t launch_down_t(const DownArgs& a, hipStream_t st) {
+  int64_t blocks = (a.hidden + a.rows_per_wg - 1) / a.rows_per_wg;
+  hipLaunchKernelGGL((down_reduce_kernel<VB, CH>), dim3(static_cast<unsigned>(blocks)), dim3(192), 0, st, a);
+  return hipGetLastError();
+}
+
+// Reduction widths the vector fast path is instantiated for: K = 64*VB*CH.
+bool fast_width_supported(int64_t K) {
+  return K == 1024 || K == 2048 || K == 3072 || K == 4096 || K == 5120 || K == 6144 || K == 7168 ||
+         K == 8192 || K == 512 || K == 1536;
+}
+
+hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st) {
+  switch (a.hidden) {
+    case 512: return launch_gate_up_t<8, 1>(a, st);
+    case 1024: return launch_gate_up_t<16, 1>(a, st);
+    case 1536: return launch_gate_up_t<8, 3>(a, st);
+    case 2048: return launch_gate_up_t<16, 2>(a, st);
+    case 3072: return launch_gate_up_t<16, 3>(a, st);
+    case 4096: return launch_gate_up_t<16, 4>(a, st);
+    case 5120: return launch_gate_up_t<16, 5>(a, st);
+    case 6144: return launch_gate_up_t<16, 6>(a, st);
+    case 7168: return launch_gate_up_t<16, 7>(a, st);
+    case 8192: return launch_gate_up_t<16, 8>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_down(const DownArgs& a, hipStream_t st) {
+  switch (a.intermediate) {
+    case 512: return launch_down_t<8, 1>(a, st);
+    case 1024: return launch_down_t<16, 1>(a, st);
+    case 1536: return launch_down_t<8, 3>(a, st);
+    case 2048: return launch_down_t<16, 2>(a, st);
+    case 3072: return launch_down_t<16, 3>(a, st);
+    case 4096: return launch_down_t<16, 4>(a, st);
+    case 5120: return launch_down_t<16, 5>(a, st);
+    case 6144: return launch_down_t<16, 6>(a, st);
+    case 7168: return launch_down_t<16, 7>(a, st);
+    case 8192: return launch_down_t<16, 8>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int VB, int CH>
+static hipError_t launch_gemv_t(const GemvArgs& a, hipStream_t st) {
+  int64_t rows_per_wg = 4 * static_cast<int64_t>(a.rows_per_wave);
+  hipLaunchKernelGGL((gemv_kernel<VB, CH>), dim3(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg)),
+                     dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
+  switch (a.K) {
+    case 512: return launch_gemv_t<8, 1>(a, st);
+    case 1024: return launch_gemv_t<16, 1>(a, st);
+    case 1536: return launch_gemv_t<8, 3>(a, st);
+    case 2048: return launch_gemv_t<16, 2>(a, st);
+    case 3072: return launch_gemv_t<16, 3>(a, st);
+    case 4096: return launch_gemv_t<16, 4>(a, st);
+    case 5120: return launch_gemv_t<16, 5>(a, st);
+    case 6144: return launch_gemv_t<16, 6>(a, st);
+    case 7168: return launch_gemv_t<16, 7>(a, st);
+    case 8192: return launch_gemv_t<16, 8>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_topk(const TopkArgs& a, hipStream_t st) {
+  if (a.tokens == 0) return hipSuccess;
+  hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>((a.tokens + 3) / 4)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_router(const RouterArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(router_kernel, dim3(static_cast<unsigned>(a.experts)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st) {
+  int64_t rows_per_wg = 4 * static_cast<int64_t>(a.rows_per_wave);
+  dim3 grid(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(a.G));
+  size_t lds = sizeof(float) * static_cast<size_t>(a.tile_rows) * static_cast<size_t>(a.K);
+  hipLaunchKernelGGL(linear_generic_kernel, grid, dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st) {
+  int64_t n = a.rows * a.cols;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_weighted_reduction(const WeightedReductionArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(weighted_reduction_kernel, dim3(static_cast<unsigned>((a.H + 255) / 256)), dim3(256), 0,
+                     st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sigmoid_bf16(const uint16_t* g, uint16_t* out, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(sigmoid_bf16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, g, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, a, b, out,
+                     n);
+  return hipGetLastError();
+}
+
+}  // namespace glm53

@@ -1,0 +1,91 @@
+// Prefill (grouped-expert) kernel argument blocks and launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm53 {
+
+constexpr int kPlanMaxExperts = 1024;
+constexpr int kGroupedTileRows = 32;   // routes per descriptor (grouped_fp8.py:20)
+constexpr int kMaxReduceTopK = 16;
+enum { GEMM_PLAIN = 0, GEMM_SWIGLU = 1 };
+
+struct RoutePlanArgs {
+  const int32_t* expert_ids;  // [routes] flat (token-major, slot-minor)
+  const float* scores;        // [routes] or null
+  int64_t routes;
+  int top_k;
+  int experts;
+  int tile_rows;
+  int64_t blocks;             // ceil(routes / 256)
+  int64_t capacity;           // ceil(routes / tile_rows) + experts
+  unsigned* block_counts;     // [blocks, experts] scratch
+  unsigned* block_invalid;    // [blocks] scratch
+  int32_t* sorted_route;      // [routes] order
+  int32_t* inverse;           // [routes]
+  int32_t* sorted_expert;     // [routes]
+  int32_t* sorted_token;      // [routes]
+  float* sorted_score;        // [routes]
+  unsigned* route_offsets;    // [experts + 1]
+  unsigned* tile_offsets;     // [experts + 1]
+  int32_t* tile_expert;       // [capacity]
+  int32_t* tile_start;        // [capacity]
+  int32_t* tile_len;          // [capacity]
+  unsigned* status;           // [2]: invalid routes, valid descriptors
+};
+
+struct SplitArgs {
+  const uint16_t* x;          // [rows, cols] bf16
+  int64_t x_row_stride;
+  int64_t rows, cols;         // cols % 128 == 0
+  uint8_t* hi;                // [rows, cols] E4M3
+  uint8_t* lo;                // [rows, cols] E4M3 (residual * 16)
+  float* scale;               // [rows, cols / 128] power of two
+};
+
+struct GroupedGemmArgs {
+  const uint8_t* a_hi;
+  const uint8_t* a_lo;
+  const float* a_scale;       // [act_rows, K / 128]
+  const int32_t* a_row_index; // [routes] -> activation row, or null (identity)
+  int64_t K;                  // % 128 == 0
+  int64_t routes;
+  const int32_t* tile_expert; // descriptors, or null: implicit expert 0, 32-route tiles
+  const int32_t* tile_start;
+  const int32_t* tile_len;
+  int64_t experts;
+  const uint8_t* weight;      // expert e rows at weight + e * w_expert_stride, [rows, K]
+  const uint8_t* weight_up;   // SwiGLU mode: up rows, same strides
+  int64_t w_expert_stride;
+  const float* scale;         // expert e block scales, [ceil(rows/128), s_cols]
+  const float* scale_up;
+  int64_t s_expert_stride;
+  int64_t s_cols;
+  int64_t N;                  // output columns (PLAIN) / intermediate columns (SWIGLU)
+  float limit;
+  uint16_t* out;              // [routes, out_row_stride] bf16
+  int64_t out_row_stride;
+  const int32_t* fixup;       // device flag: weights hold 0x7F/0xFF codes (or null)
+};
+
+struct ReduceArgs {
+  const uint16_t* route_out;  // [routes, H] in sorted order
+  const int32_t* inverse;     // [tokens * top_k] -> sorted position
+  const float* sorted_score;  // [routes] (grouped order)
+  const float* route_score;   // [tokens * top_k] (Direct order)
+  const int32_t* expert_ids;  // [tokens * top_k] (Direct order)
+  const uint16_t* shared;     // [tokens, H] or null
+  int64_t tokens, H;
+  int top_k;
+  uint16_t* out;              // [tokens, H]
+};
+
+hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t st);
+hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st);
+hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st);
+hipError_t launch_reduce(const ReduceArgs& a, bool direct_order, hipStream_t st);
+hipError_t launch_scan_480(const uint8_t* codes, int64_t n, int32_t* flag, bool clear, hipStream_t st);
+hipError_t launch_or_flags(int32_t* dst, const int32_t* a, const int32_t* b, hipStream_t st);
+
+}  // namespace glm53

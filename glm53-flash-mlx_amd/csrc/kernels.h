@@ -1,0 +1,136 @@
+// Kernel argument blocks and host launchers (internal to libglm53_moe.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm53 {
+
+constexpr int kMaxTopK = 8;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxDownRowsPerWg = 64;
+
+// ---------------------------------------------------------------- decode --
+
+struct GateUpArgs {
+  const uint16_t* x;              // [H] bf16
+  const int32_t* expert_ids;      // [top_k]
+  int top_k;
+  int64_t experts;
+  const uint8_t* gate_up_weight;  // [E, 2I, H]
+  const float* gate_up_scale;     // [E, 2*ceil(I/128), ceil(H/128)]
+  const uint8_t* shared_gate_weight;  // [Is, H] or null
+  const float* shared_gate_scale;
+  const uint8_t* shared_up_weight;
+  const float* shared_up_scale;
+  int64_t hidden, intermediate, shared_intermediate;
+  float limit;
+  int rows_per_wave;
+  int64_t wgs_per_slot;
+  uint16_t* hidden_out;           // [top_k, I] then [Is]
+  int* error_flag;
+};
+
+struct DownArgs {
+  const uint16_t* hidden_in;      // [top_k, I] then shared [I]
+  const int32_t* expert_ids;
+  const float* scores;            // [top_k]
+  int top_k;
+  int64_t experts;
+  const uint8_t* down_weight;     // [E, H, I]
+  const float* down_scale;        // [E, ceil(H/128), ceil(I/128)]
+  const uint8_t* shared_down_weight;  // [H, I] or null
+  const float* shared_down_scale;
+  int64_t hidden, intermediate;
+  int64_t rows_per_wg;
+  uint16_t* out;                  // [H] bf16
+  int* error_flag;
+};
+
+struct RouterArgs {
+  const uint16_t* x;       // [H] bf16
+  const float* weight;     // [E, H]
+  const float* bias;       // [E]
+  int64_t experts, hidden;
+  int top_k;
+  float routed_scaling_factor;
+  int norm_topk_prob;
+  float* sigmoid_out;      // [E] scratch
+  float* choice_out;       // [E] scratch
+  unsigned* arrivals;      // zero-initialised, self-resetting
+  int32_t* ids_out;        // [top_k]
+  float* scores_out;       // [top_k]
+};
+
+struct GenericLinearArgs {
+  const uint16_t* x;
+  int64_t x_row_stride, x_group_stride;
+  const uint8_t* weight;
+  int64_t w_expert_stride, w_row_offset;
+  const float* scale;
+  int64_t s_expert_stride, s_row_offset, s_cols;
+  const int32_t* expert_ids;  // [G] or null
+  int64_t experts;
+  int64_t M, G, N, K;
+  int rows_per_wave;
+  int tile_rows;              // activation rows staged in LDS per pass
+  uint16_t* y;
+  int64_t y_row_stride, y_group_stride;
+  int* error_flag;
+};
+
+struct SwigluArgs {
+  const uint16_t* gate;
+  const uint16_t* up;
+  int64_t gate_row_stride, up_row_stride;
+  int64_t rows, cols;
+  float limit;
+  uint16_t* out;
+  int64_t out_row_stride;
+};
+
+struct WeightedReductionArgs {
+  const uint16_t* down;    // [top_k, H]
+  const float* scores;     // [top_k]
+  const uint16_t* addend;  // [H] or null
+  int top_k;
+  int64_t H;
+  uint16_t* out;
+};
+
+struct GemvArgs {
+  const uint16_t* x;      // [K] bf16
+  const uint8_t* weight;  // [N, K]
+  const float* scale;     // [ceil(N/128), ceil(K/128)]
+  int64_t N, K;
+  int rows_per_wave;
+  uint16_t* y;            // [N] bf16
+};
+
+struct TopkArgs {
+  const float* logits;    // [tokens, experts] FP32
+  const float* bias;      // [experts]
+  int64_t tokens, experts;
+  int top_k;
+  float routed_scaling_factor;
+  int norm_topk_prob;
+  int32_t* ids_out;       // [tokens, top_k]
+  float* scores_out;      // [tokens, top_k]
+};
+
+constexpr int kGenericRows = 8;
+
+bool fast_width_supported(int64_t K);
+hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st);
+hipError_t launch_down(const DownArgs& a, hipStream_t st);
+hipError_t launch_router(const RouterArgs& a, hipStream_t st);
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
+hipError_t launch_topk(const TopkArgs& a, hipStream_t st);
+hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st);
+hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st);
+hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st);
+hipError_t launch_weighted_reduction(const WeightedReductionArgs& a, hipStream_t st);
+hipError_t launch_sigmoid_bf16(const uint16_t* g, uint16_t* out, int64_t n, hipStream_t st);
+hipError_t launch_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n, hipStream_t st);
+
+}  // namespace glm53

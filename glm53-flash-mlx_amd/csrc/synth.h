@@ -1,0 +1,22 @@
+// Synthetic weight generation (benchmarks and device-side test inputs).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glm53 {
+
+struct SynthFp8Args {
+  uint8_t* codes;   // [rows, cols] E4M3
+  float* scale;     // [ceil(rows/128), ceil(cols/128)]
+  int64_t rows, cols;
+  uint64_t seed;
+  float std;
+};
+
+hipError_t launch_synth_fp8(const SynthFp8Args& a, hipStream_t st);
+hipError_t launch_synth_f32(float* out, int64_t n, uint64_t seed, float std, float lo, float hi, int uniform,
+                            hipStream_t st);
+hipError_t launch_synth_bf16(uint16_t* out, int64_t n, uint64_t seed, float std, hipStream_t st);
+
+}  // namespace glm53

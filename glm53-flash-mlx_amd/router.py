@@ -1,0 +1,66 @@
+"""FP32 top-k router (patch.py:131-142 ``Float32Gate`` of the reference).
+
+logits = x_f32 @ W_f32^T, sigma = sigmoid(logits), choice = sigma + bias
+(``e_score_correction_bias``), ids = top_k(choice) ordered by (choice desc,
+expert id asc), weights = sigma[ids] normalised when ``norm_topk_prob`` and
+multiplied by ``routed_scaling_factor``.  The selection rule is the
+DeepSeek-V3 auxiliary-loss-free rule that mlx-vlm's
+``dsv32.group_expert_select`` implements, with n_group = 1; the slot order
+(MLX leaves argpartition order unspecified) is this build's documented tie
+policy.  Decode (one token) runs a fused GEMV + top-k kernel; prefill runs an
+FP32 rocBLAS GEMM for the logits and a wavefront-per-token top-k.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+
+class Float32Gate(torch.nn.Module):
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor, *, top_k: int = 8,
+                 routed_scaling_factor: float = 1.0, norm_topk_prob: bool = True, n_group: int = 1,
+                 topk_group: int = 1):
+        super().__init__()
+        if weight.dtype != torch.float32 or weight.dim() != 2:
+            raise ValueError("router weight must be a 2-D float32 [experts, hidden] tensor")
+        if bias.dtype != torch.float32 or bias.shape != (weight.shape[0],):
+            raise ValueError("e_score_correction_bias must be float32 [experts]")
+        if n_group != 1 or topk_group != 1:
+            raise ValueError("grouped expert selection (n_group > 1) is not part of this path")
+        self.register_buffer("weight", weight.contiguous())
+        self.register_buffer("e_score_correction_bias", bias.contiguous())
+        self.top_k = int(top_k)
+        self.routed_scaling_factor = float(routed_scaling_factor)
+        self.norm_topk_prob = bool(norm_topk_prob)
+        self.n_group = n_group
+        self.topk_group = topk_group
+
+    @property
+    def n_routed_experts(self) -> int:
+        return int(self.weight.shape[0])
+
+    def as_c_struct(self) -> N.Router:
+        return N.Router(self.weight.data_ptr(), self.e_score_correction_bias.data_ptr(), self.weight.shape[0],
+                        self.weight.shape[1], self.top_k, self.routed_scaling_factor, int(self.norm_topk_prob))
+
+    def forward(self, x):
+        N.require_device(x, self.weight)
+        if x.dtype != torch.bfloat16:
+            raise ValueError(f"router input must be bfloat16, got {x.dtype}")
+        hidden = self.weight.shape[1]
+        if x.shape[-1] != hidden:
+            raise ValueError(f"input width {x.shape[-1]} != router width {hidden}")
+        flat = x.reshape(-1, hidden).contiguous()
+        tokens = flat.shape[0]
+        ids = torch.empty((tokens, self.top_k), dtype=torch.int32, device=x.device)
+        scores = torch.empty((tokens, self.top_k), dtype=torch.float32, device=x.device)
+        lib = N.lib()
+        ws_bytes = lib.glm53_router_workspace_bytes(tokens, hidden, self.weight.shape[0])
+        ws = N.workspace(ws_bytes, x.device)
+        router = self.as_c_struct()
+        N.check(lib.glm53_router_topk(N.ctypes.byref(router), N.ptr(flat), tokens, N.ptr(ids), N.ptr(scores),
+                                      N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
+        lead = x.shape[:-1]
+        return ids.reshape(*lead, self.top_k), scores.reshape(*lead, self.top_k)

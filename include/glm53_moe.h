@@ -1,0 +1,270 @@
+/*
+ * glm53_moe.h -- C ABI of libglm53_moe.so, the MI355X (gfx950) implementation
+ * of the FP8 block-scaled packed mixture-of-experts path of
+ * kiojuvr/glm53-flash-mlx.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  Every pointer argument is a device
+ *     pointer unless the comment says "host".  BF16 tensors are passed as
+ *     `void*` (2 bytes per element, row-major), E4M3 weights as `uint8_t*`,
+ *     block scales (`weight_scale_inv`) as `float*` over 128x128 blocks.
+ *   - `stream` is a hipStream_t (NULL = default stream).  All work is
+ *     enqueued on it; no call synchronises the host except the *_status /
+ *     *_error_flag readbacks, which say so.
+ *   - Return value: GLM53_OK, or an error code with a message retrievable by
+ *     glm53_last_error() (thread-local).  The Python layer maps
+ *     GLM53_INVALID_ARGUMENT to ValueError and the others to RuntimeError,
+ *     as the reference does (fp8.py:256-273; native_packed_moe_plan.cpp:
+ *     127-149).
+ *   - Plans own fixed device scratch allocated once at creation and are not
+ *     safe for concurrent use (one plan per layer and stream), as the
+ *     reference's native plans (native_packed_moe_plan.h:22-146).
+ *
+ * Reference paths are relative to the kiojuvr/glm53-flash-mlx repository.
+ */
+#ifndef GLM53_MOE_H
+#define GLM53_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLM53_ABI_VERSION 1
+
+#define GLM53_OK 0
+#define GLM53_INVALID_ARGUMENT 1
+#define GLM53_BAD_STATE 2
+#define GLM53_DEVICE_ERROR 3
+
+/* Reduction order of the prefill combine step. */
+#define GLM53_REDUCE_GROUPED 0 /* FP32 slot order, grouped_fp8.py:273-276 */
+#define GLM53_REDUCE_DIRECT 1  /* BF16 ascending expert, fp8.py:384-397 */
+
+/* Packed per-layer expert bank, reference layout (packed.py:782-850):
+ *   gate_up_weight    u8  [E, 2I, H]  rows 0..I-1 gate, I..2I-1 up
+ *   gate_up_scale_inv f32 [E, 2*ceil(I/128), ceil(H/128)]  (up from row ceil(I/128))
+ *   down_weight       u8  [E, H, I]
+ *   down_scale_inv    f32 [E, ceil(H/128), ceil(I/128)]                      */
+typedef struct glm53_bank {
+  const uint8_t* gate_up_weight;
+  const float* gate_up_scale_inv;
+  const uint8_t* down_weight;
+  const float* down_scale_inv;
+  int64_t experts;
+  int64_t hidden;
+  int64_t intermediate;
+  /* device int32, nonzero when the weights hold E4M3 codes 0x7F / 0xFF
+   * (glm53_e4m3_scan_codes); NULL makes every prefill call scan the bank */
+  const int32_t* code_flags;
+} glm53_bank;
+
+/* One BlockFP8Linear (fp8.py:302-326): weight u8 [out, in], scale
+ * f32 [ceil(out/128), ceil(in/128)]. */
+typedef struct glm53_linear {
+  const uint8_t* weight;
+  const float* scale_inv;
+  int64_t out_features;
+  int64_t in_features;
+  const int32_t* code_flags; /* as glm53_bank.code_flags; may be NULL */
+} glm53_linear;
+
+/* Shared expert = ClampedMLP over block-FP8 linears (patch.py:114-129). */
+typedef struct glm53_shared_expert {
+  glm53_linear gate;
+  glm53_linear up;
+  glm53_linear down;
+} glm53_shared_expert;
+
+/* FP32 router (patch.py:131-142): weight f32 [E, H], bias f32 [E]
+ * (e_score_correction_bias); selection = top_k of sigmoid(logits) + bias
+ * ordered (biased score desc, expert id asc); weights = sigmoid of the
+ * selected logits, normalised if norm_topk_prob, times
+ * routed_scaling_factor. */
+typedef struct glm53_router {
+  const float* weight;
+  const float* bias;
+  int64_t experts;
+  int64_t hidden;
+  int64_t top_k;
+  float routed_scaling_factor;
+  int32_t norm_topk_prob;
+} glm53_router;
+
+const char* glm53_last_error(void);
+int glm53_abi_version(void);
+
+/* Writes 1 to the device int32 *flag when any of the n E4M3 codes is 0x7F
+ * or 0xFF, else 0.  The reference's table (fp8.py:22-27) decodes those codes
+ * to +-480; OCP E4M3 (the MFMA operand format) reads them as NaN, so the
+ * MFMA paths use the flag to switch on an exact fix-up.  The streaming
+ * decode kernels decode them exactly without a flag. */
+int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * block_fp8_linear -- replaces fp8.py:254-299 `block_fp8_linear`
+ * (kernels fp8.py:41-116).  y[m, n] = T(sum_k x[m,k] * E4M3(w[n,k]) *
+ * s[n/128, k/128]).  x bf16 [M, K], y bf16 [M, N].  M == 1 runs the
+ * streaming GEMV; M > 1 with K % 128 == 0 runs the FP8 MFMA GEMM and needs
+ * `workspace` of glm53_fp8_linear_workspace_bytes(M, N, K) bytes (may be
+ * NULL when that is 0).
+ * ---------------------------------------------------------------------- */
+size_t glm53_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N,
+                     const float* scale_inv, void* y, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* ------------------------------------------------------------------------
+ * Router -- replaces patch.py:131-142 `Float32Gate.__call__` (with the
+ * selection half of mlx-vlm dsv32.group_expert_select, n_group = 1).
+ * x bf16 [tokens, H] -> ids int32 [tokens, top_k], scores f32 [tokens, top_k].
+ * ---------------------------------------------------------------------- */
+size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts);
+int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids,
+                      float* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Batch-1 decode plan -- replaces native_packed_moe_plan.h:22-146
+ * `NativePackedMoEDecodePlan` (bindings.cpp:562-632) and the Python
+ * composition packed.py:896-923 `PackedFP8MoE.__call__` for one token.
+ * ---------------------------------------------------------------------- */
+typedef struct glm53_decode_plan glm53_decode_plan;
+
+int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate,
+                             int64_t experts, int64_t top_k, float swiglu_limit,
+                             glm53_decode_plan** out);
+void glm53_decode_plan_destroy(glm53_decode_plan* plan);
+
+/* Routed experts + shared expert for given expert ids / scores (the
+ * reference's execute(x, ids, scores, weights...), .cpp:151-173).
+ * x bf16 [H]; expert_ids int32 [top_k]; scores f32 [top_k]; out bf16 [H].
+ * shared may be NULL. */
+int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank,
+                            const glm53_shared_expert* shared, const void* x,
+                            const int32_t* expert_ids, const float* scores, void* out,
+                            void* stream);
+
+/* Router + routed + shared in one call (PackedFP8MoE.__call__ for L = 1).
+ * ids_out / scores_out (device, [top_k]) may be NULL. */
+int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank,
+                     const glm53_shared_expert* shared, const glm53_router* router,
+                     const void* x, void* out, int32_t* ids_out, float* scores_out, void* stream);
+
+/* bind_weights / execute_bound (native_packed_moe_plan.cpp:231-280): bind
+ * once, then run with only the activation.  Binding twice is GLM53_BAD_STATE. */
+int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank,
+                           const glm53_shared_expert* shared, const glm53_router* router);
+int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, void* stream);
+
+/* Device scratch of the last call (read-only diagnostics): which = 0 hidden
+ * bf16 [top_k + 1, I] (routed rows, then shared), 1 expert ids int32
+ * [top_k], 2 scores f32 [top_k]. */
+int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes);
+
+/* Synchronous: copies the plan's device error flag to *host_value (nonzero
+ * when an expert id was out of range) and clears it. */
+int glm53_decode_plan_error_flag(glm53_decode_plan* plan, int32_t* host_value);
+
+/* ------------------------------------------------------------------------
+ * Prefill building blocks -- replace grouped_fp8.py:157-276.
+ * ---------------------------------------------------------------------- */
+
+/* build_route_plan + build_grouped_tile_plan (grouped_fp8.py:157-203;
+ * native_indexer_plan.metal:1878-1982).  expert_ids int32 [routes] (flat,
+ * token-major), scores f32 [routes] (may be NULL).  Outputs (device):
+ * sorted_route/inverse/sorted_expert/sorted_token int32 [routes],
+ * sorted_score f32 [routes] (ignored when scores is NULL),
+ * route_offsets/tile_offsets u32 [experts + 1], tile_expert/tile_start/
+ * tile_len int32 [capacity] with capacity = ceil(routes / tile_rows) +
+ * experts, status u32 [2] = {invalid route count, valid descriptors}. */
+size_t glm53_route_plan_workspace_bytes(int64_t routes, int64_t experts);
+int glm53_route_plan(const int32_t* expert_ids, const float* scores, int64_t routes, int64_t top_k,
+                     int64_t experts, int64_t tile_rows, int32_t* sorted_route, int32_t* inverse,
+                     int32_t* sorted_expert, int32_t* sorted_token, float* sorted_score,
+                     uint32_t* route_offsets, uint32_t* tile_offsets, int32_t* tile_expert,
+                     int32_t* tile_start, int32_t* tile_len, int64_t capacity, uint32_t* status,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* grouped_fp8_linear (grouped_fp8.py:206-262): y[r] = T(x[row(r)] .
+ * W[e(r)]^T) for sorted routes r, where row(r) = row_index[r] (NULL:
+ * identity) and e(r) comes from the 32-route descriptors.  x bf16
+ * [act_rows, K], weight u8 [E, N, K], scale f32 [E, ceil(N/128), K/128],
+ * y bf16 [routes, N].  Requires K % 128 == 0 and N % 16 == 0.  code_flags
+ * (device int32, may be NULL = scan the weight first) as in glm53_bank. */
+size_t glm53_grouped_linear_workspace_bytes(int64_t act_rows, int64_t K);
+int glm53_grouped_linear(const void* x, int64_t act_rows, const int32_t* row_index, int64_t routes,
+                         int64_t K, const int32_t* tile_expert, const int32_t* tile_start,
+                         const int32_t* tile_len, int64_t descriptors, const uint8_t* weight,
+                         const float* scale_inv, const int32_t* code_flags, int64_t experts,
+                         int64_t N, void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/* activate_gate_up (grouped_fp8.py:265-270): gate_up bf16 [rows, 2I] ->
+ * h bf16 [rows, I] = T(T(g' * sigmoid(g')) * u'), g' = min(g, L),
+ * u' = clip(u, -L, L), MLX BF16 rounding. */
+int glm53_activate_gate_up(const void* gate_up, int64_t rows, int64_t intermediate, float limit,
+                           void* out, void* stream);
+
+/* restore_and_reduce (grouped_fp8.py:273-276) plus optional BF16 add of
+ * `shared` bf16 [tokens, H]: out[t] = T(T(sum_s sorted_out[inverse[t*k+s]]
+ * * sorted_score[...]) + shared[t]). */
+int glm53_restore_and_reduce(const void* sorted_out, const float* sorted_score,
+                             const int32_t* inverse, int64_t tokens, int64_t top_k, int64_t H,
+                             const void* shared, void* out, void* stream);
+
+/* Exact Direct accumulation (fp8.py:384-397; native_indexer_plan.metal:
+ * 2174-2207): per token, ascending expert id, total = T(total + T(out *
+ * score)); expert_ids / scores are the unsorted flat routes. */
+int glm53_direct_order_reduce(const void* sorted_out, const int32_t* inverse,
+                              const int32_t* expert_ids, const float* scores, int64_t tokens,
+                              int64_t top_k, int64_t H, const void* shared, void* out,
+                              void* stream);
+
+/* MLX BF16 sigmoid used inside the SwiGLU epilogue (packed.py:155-160),
+ * elementwise over n BF16 values.  Diagnostic: pins the device arithmetic
+ * against the reference's exhaustive sweep. */
+int glm53_sigmoid_bf16(const void* gate, int64_t n, void* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill plan -- replaces native_prefill_moe_plan.h:18-96
+ * `NativePrefillMoEPlan` and grouped_fp8.py:279-328
+ * `SortedGroupedFP8MoE.grouped_from_routes` (+ the shared expert).
+ * ---------------------------------------------------------------------- */
+typedef struct glm53_prefill_plan glm53_prefill_plan;
+
+int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate,
+                              int64_t experts, int64_t top_k, int64_t max_tokens,
+                              float swiglu_limit, glm53_prefill_plan** out);
+void glm53_prefill_plan_destroy(glm53_prefill_plan* plan);
+
+/* x bf16 [tokens, H] -> out bf16 [tokens, H].  Routes come from `router`
+ * when expert_ids is NULL, otherwise from expert_ids int32 [tokens, top_k]
+ * and scores f32 [tokens, top_k].  reduction: GLM53_REDUCE_*. */
+int glm53_prefill_moe(glm53_prefill_plan* plan, const glm53_bank* bank,
+                      const glm53_shared_expert* shared, const glm53_router* router, const void* x,
+                      int64_t tokens, const int32_t* expert_ids, const float* scores,
+                      int32_t reduction, void* out, void* stream);
+
+/* Synchronous: invalid route count of the last glm53_prefill_moe. */
+int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes);
+
+/* Device scratch of the last call: which = 0 ids int32 [tokens, top_k],
+ * 1 scores f32 [tokens, top_k], 2 sorted route order int32 [routes],
+ * 3 descriptors int32 [3, capacity]. */
+int glm53_prefill_plan_scratch(glm53_prefill_plan* plan, int32_t which, void** ptr, size_t* bytes);
+
+/* ------------------------------------------------------------------------
+ * Seeded synthetic inputs (no reference counterpart: the reference loads a
+ * checkpoint).  Element i of stream `seed` is N(0, std) (or U(lo, hi)). */
+int glm53_synth_fp8(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, uint64_t seed,
+                    float std, void* stream);
+int glm53_synth_f32(float* out, int64_t n, uint64_t seed, float std, float lo, float hi,
+                    int32_t uniform, void* stream);
+int glm53_synth_bf16(void* out, int64_t n, uint64_t seed, float std, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM53_MOE_H */
