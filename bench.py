@@ -1,0 +1,409 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FP8 block-scaled MoE path (one JSON line).
+
+Headline workload (made of config-2 layers): steady
+batch-1 decode through 42 independent MoE layers (H=4096, I=1536, 288 routed
+experts, top-8, one shared expert, FP32 router; 229 GB of E4M3 banks
+resident in HBM), one BF16 token per step with a residual add, a fresh
+seeded input every step.  One step (42 x 3 launches + the input draw) is
+captured once as a HIP graph and replayed; `value` = microseconds per MoE
+layer = step time / 42.
+
+Also reported: the dominant kernel (fused routed+shared gate/up/SwiGLU)
+timed with HIP events on its stream against the HBM roofline, the grouped
+prefill configs 4 (256 tokens, near-uniform) and 5 (2,048 tokens, Zipf
+router bias) as routes/s with HBM and FP8-MFMA roofline fractions, a parity
+sample against the CPU oracle, and the CPU oracle's own decode time on the
+host cores (the reference has no CPU FP8 path; MLX is not installable).
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+from types import SimpleNamespace
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP8_TFLOPS = 5000.0   # dense FP8 MFMA
+SEED = 20260901
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=512)
+    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--layers", type=int, default=42)
+    p.add_argument("--kernel-steps", type=int, default=8, help="stage-graph replays (x8) for per-launch timing")
+    p.add_argument("--prefill-iters", type=int, default=10)
+    p.add_argument("--cpu-samples", type=int, default=7, help="CPU oracle layer evaluations (2 warmup + rest timed)")
+    p.add_argument("--parity-layers", type=int, default=3)
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--json-out", type=str, default="")
+    return p.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_layer_bytes(H, I, Is, E, k):
+    """Algorithmic bytes of one decode layer: every weight byte touched once."""
+    sr, sh, srs = math.ceil(I / 128), math.ceil(H / 128), math.ceil(Is / 128)
+    router = E * H * 4 + E * 4
+    gate_up = k * (2 * I * H + 2 * sr * sh * 4)
+    down = k * (H * I + sh * sr * 4)
+    shared = 3 * Is * H + (2 * srs * sh + sh * srs) * 4
+    return {"router": router, "routed_gate_up": gate_up, "routed_down": down, "shared": shared,
+            "activations": 2 * H * 2, "total": router + gate_up + down + shared + 2 * H * 2}
+
+
+def gate_up_launch_bytes(H, I, Is, k):
+    sr, sh, srs = math.ceil(I / 128), math.ceil(H / 128), math.ceil(Is / 128)
+    weights = k * (2 * I * H + 2 * sr * sh * 4) + 2 * Is * H + 2 * srs * sh * 4
+    return weights + H * 2 + (k * I + Is) * 2
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported on this single-GPU build "
+              "(the multi-GPU sharding is described, not run)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    pkg = importlib.import_module("glm53-flash-mlx_amd")
+    syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
+    N = importlib.import_module("glm53-flash-mlx_amd._native")
+    packed = importlib.import_module("glm53-flash-mlx_amd.packed")
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = syn.layer_config()
+    H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    Is = I * cfg.n_shared_experts
+    L = args.layers
+
+    # ------------------------------------------------------------ weights ---
+    t0 = time.perf_counter()
+    layers = []
+    for layer in range(L):
+        bank, shared, gate = syn.synth_layer(cfg, SEED, layer, dev)
+        plan = packed.DecodePlan(H, I, Is, E, k, cfg.swiglu_limit)
+        bank.code_flags()
+        layers.append(SimpleNamespace(bank=bank, shared=shared, gate=gate, plan=plan))
+    torch.cuda.synchronize()
+    gen_s = time.perf_counter() - t0
+    resident = sum(l.bank.nbytes for l in layers) + L * (3 * Is * H + E * H * 4)
+    log(f"generated {L} layers, {resident / 1e9:.1f} GB resident, in {gen_s:.1f} s")
+
+    # ------------------------------------------------------- decode graph ---
+    x = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = N.lib()
+
+    def step():
+        N.check(lib.glm53_synth_step_input(N.ptr(x), H, SEED, 1.0, N.ptr(counter), N.stream_handle(dev)))
+        for l in layers:
+            l.plan.step(l.bank, l.shared, l.gate, x, x, x, N.STAGE_ALL, dev)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = start.elapsed_time(end) / args.steps
+    us_layer = ms_step * 1000.0 / L
+    finite = bool(torch.isfinite(x.float()).all().item())
+    log(f"decode: {ms_step:.3f} ms/step, {us_layer:.2f} us/layer (wall {wall:.2f} s, finite={finite})")
+
+    bytes_layer = decode_layer_bytes(H, I, Is, E, k)
+    layer_gbs = bytes_layer["total"] / (us_layer * 1e-6) / 1e9
+
+    # ------------------------------------------- per-launch HIP-event timing --
+    # Per-launch durations: one graph per stage holds that stage's launch for
+    # all L layers back to back (each layer's own weights, so no launch is
+    # served from L2 / MALL), replayed between two HIP events on the launch
+    # stream.  Event pairs around single eager launches would time host
+    # enqueue latency and the events' own cache flushes instead.
+    stage_us = {}
+    for name, mask in (("router", N.STAGE_ROUTER), ("gate_up", N.STAGE_GATE_UP), ("down", N.STAGE_DOWN)):
+        def run(mask=mask):
+            for l in layers:
+                l.plan.step(l.bank, l.shared, l.gate, x, x, x, mask, dev)
+        stage_us[name] = time_graph(run, args.kernel_steps * 8, torch) / L
+    router_us, gate_up_us, down_us = stage_us["router"], stage_us["gate_up"], stage_us["down"]
+    probe = read_probe(lib, N, layers[-1].bank, dev, torch)
+    gu_bytes = gate_up_launch_bytes(H, I, Is, k)
+    gu_gbs = gu_bytes / (gate_up_us * 1e-6) / 1e9
+    down_bytes = (bytes_layer["routed_down"] + Is * H + math.ceil(H / 128) * math.ceil(Is / 128) * 4
+                  + (k + 1) * I * 2 + 2 * H * 2)
+    log(f"launches: router {router_us:.2f} us, gate/up {gate_up_us:.2f} us ({gu_gbs:.0f} GB/s), "
+        f"down {down_us:.2f} us ({down_bytes / (down_us * 1e-6) / 1e9:.0f} GB/s)")
+
+    # -------------------------------------------------------------- parity ---
+    parity = parity_sample(args, layers, cfg, dev, torch, np)
+
+    # ------------------------------------------------------------- prefill ---
+    prefill = {}
+    if not args.no_prefill:
+        prefill = bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn)
+
+    # --------------------------------------------------------- CPU baseline ---
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args, layers, cfg, dev, torch, np)
+
+    result = {
+        "metric": "µs per MoE layer @ batch-1 decode (HBM GB/s %peak); prefill routes/s (%FP8 MFMA)",
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3xbf16->f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantised per 128x128 block, N(0,1) bf16 tokens)",
+        "config": {
+            "workload": f"BASELINE config 3: steady batch-1 decode, {L} independent config-2 MoE layers "
+                        f"(H={H}, I={I}, {E} experts top-{k} + 1 shared, FP32 router, swiglu_limit=10), "
+                        "BF16 residual, fresh seeded token per step, HIP-graph replay",
+            "layers": L, "hidden": H, "intermediate": I, "experts": E, "top_k": k, "shared_experts": 1,
+            "resident_bytes": resident, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gate_up_swiglu_kernel<16,4> (8 routed + shared gate/up rows, fused SwiGLU)",
+            "achieved": round(gu_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": gu_bytes,
+            "avg_launch_us": round(gate_up_us, 3),
+        },
+        "decode": {
+            "us_per_layer": round(us_layer, 3),
+            "tokens_per_s": round(1000.0 / ms_step, 1),
+            "layer_bytes": bytes_layer["total"],
+            "layer_GBps": round(layer_gbs, 1),
+            "layer_hbm_frac": round(layer_gbs / PEAK_HBM_GBS, 4),
+            "launch_us": {"router": round(router_us, 3), "gate_up": round(gate_up_us, 3),
+                          "down_reduce": round(down_us, 3)},
+            "launch_GBps": {"gate_up": round(gu_gbs, 1), "down_reduce": round(down_bytes / (down_us * 1e-6) / 1e9, 1)},
+            "achievable_read_GBps": probe,
+            "weights_generated_s": round(gen_s, 1),
+            "final_state_finite": finite,
+        },
+        "prefill": prefill,
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.json_out:
+        Path(args.json_out).write_text(line + "\n")
+
+
+def time_graph(fn, reps, torch):
+    """Mean microseconds per replay of a graph holding fn's launches."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1000.0 / reps
+
+
+def read_probe(lib, N, bank, dev, torch):
+    """Achievable streaming-read rate: a read-only kernel over regions of the
+    size of one gate/up launch (and 4 GiB), taken from a resident bank."""
+    out = {}
+    blocks = 4096
+    sink = torch.empty(4 * blocks, dtype=torch.int32, device=dev)
+    base = bank.gate_up_weight
+    span = base.numel()
+    for label, size in (("113MB", 113309696 // 256 * 256), ("1GiB", 1 << 30), ("4GiB", min(4 << 30, span))):
+        regions = max(1, min(16, span // size))
+
+        def run(size=size, regions=regions):
+            for r in range(regions):
+                N.check(lib.glm53_probe_read(N.ctypes.c_void_p(base.data_ptr() + r * size), size, N.ptr(sink), blocks,
+                                             N.stream_handle(dev)))
+        us = time_graph(run, 4, torch) / regions
+        out[label] = round(size / (us * 1e-6) / 1e9, 1)
+    return out
+
+
+def host_layer_subset(layer, ids, torch, np):
+    idx = torch.as_tensor(np.asarray(ids, dtype=np.int64), device=layer.bank.gate_up_weight.device)
+    b = layer.bank
+    bank = SimpleNamespace(
+        gate_up_weight=b.gate_up_weight.index_select(0, idx).cpu().numpy(),
+        gate_up_scale_inv=b.gate_up_scale_inv.index_select(0, idx).cpu().numpy(),
+        down_weight=b.down_weight.index_select(0, idx).cpu().numpy(),
+        down_scale_inv=b.down_scale_inv.index_select(0, idx).cpu().numpy(),
+        intermediate_size=b.intermediate_size)
+    s = layer.shared
+    shared = SimpleNamespace(gate=(s.gate_proj.weight.cpu().numpy(), s.gate_proj.weight_scale_inv.cpu().numpy()),
+                             up=(s.up_proj.weight.cpu().numpy(), s.up_proj.weight_scale_inv.cpu().numpy()),
+                             down=(s.down_proj.weight.cpu().numpy(), s.down_proj.weight_scale_inv.cpu().numpy()))
+    return bank, shared
+
+
+def bits(t, torch, np):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def parity_sample(args, layers, cfg, dev, torch, np):
+    """One eager step; the first `parity_layers` layers are checked against the
+    CPU oracle on the device's own expert selection."""
+    from oracle import oracle as O
+
+    syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
+    x = syn.normal_bf16((cfg.hidden_size,), syn.key(SEED, "parity"), device=dev)
+    worst = {"cosine": 1.0, "max_abs_rel": 0.0, "bit_exact_fraction": 1.0}
+    router_mismatch = 0
+    for l in layers[:args.parity_layers]:
+        ids, scores = l.gate(x.reshape(1, -1))
+        out = torch.empty_like(x)
+        l.plan.step(l.bank, l.shared, l.gate, x, None, out, 7, dev)
+        xb = bits(x, torch, np)
+        ids_o, _ = O.router(xb[None], l.gate.weight.cpu().numpy(), l.gate.e_score_correction_bias.cpu().numpy())
+        router_mismatch += int(set(ids_o[0].tolist()) != set(ids.cpu().numpy()[0].tolist()))
+        hb, hs = host_layer_subset(l, ids.cpu().numpy()[0], torch, np)
+        want = O.decode_moe(xb, hb, np.arange(8), scores.cpu().numpy()[0], cfg.swiglu_limit, hs)
+        st = O.compare(bits(out, torch, np), want)
+        worst["cosine"] = min(worst["cosine"], st["cosine"])
+        worst["max_abs_rel"] = max(worst["max_abs_rel"], st["max_abs_rel"])
+        worst["bit_exact_fraction"] = min(worst["bit_exact_fraction"], st["bit_exact_fraction"])
+        x = (x.float() + out.float()).to(torch.bfloat16)
+    worst["layers_checked"] = args.parity_layers
+    worst["router_set_mismatches"] = router_mismatch
+    worst["gates"] = "cosine >= 0.9999 and max_abs_rel <= 2e-2 vs CPU oracle (Direct semantics)"
+    worst["pass"] = worst["cosine"] >= 0.9999 and worst["max_abs_rel"] <= 2e-2
+    return {k: (round(v, 7) if isinstance(v, float) else v) for k, v in worst.items()}
+
+
+def bench_prefill(args, layer, cfg, dev, torch, np, pkg, syn):
+    H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    Is = I
+    out = {}
+    zipf_gate = pkg.Float32Gate(layer.gate.weight, syn.zipf_bias(E).to(dev), top_k=k)
+    for name, tokens, gate in (("config4_256_tokens", 256, layer.gate), ("config5_2048_tokens_zipf", 2048, zipf_gate)):
+        moe = pkg.SortedGroupedFP8MoE(layer.bank, cfg, gate, layer.shared)
+        x = syn.normal_bf16((1, tokens, H), syn.key(SEED, name), device=dev)
+        ids, _ = gate(x.reshape(tokens, H))
+        counts = torch.bincount(ids.reshape(-1).long(), minlength=E).cpu().numpy()
+        for _ in range(2):
+            moe(x)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(args.prefill_iters):
+            y = moe(x)
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) * 1000.0 / args.prefill_iters
+        routes = tokens * k
+        touched = int((counts > 0).sum())
+        expert_bytes = 3 * I * H + (2 * math.ceil(I / 128) * (H // 128) + (H // 128) * math.ceil(I / 128)) * 4
+        weight_bytes = touched * expert_bytes + 3 * Is * H + E * H * 4
+        act_bytes = 2 * tokens * H * 2
+        flops = 2 * routes * 3 * I * H + 2 * tokens * 3 * Is * H
+        gbs = (weight_bytes + act_bytes) / (us * 1e-6) / 1e9
+        tflops = flops / (us * 1e-6) / 1e12
+        out[name] = {
+            "tokens": tokens, "routes": routes, "us": round(us, 1), "routes_per_s": round(routes / (us * 1e-6), 1),
+            "tokens_per_s": round(tokens / (us * 1e-6), 1), "touched_experts": touched,
+            "max_expert_share": round(float(counts.max()) / routes, 4),
+            "experts_under_10_routes": int((counts < 10).sum()),
+            "algorithmic_bytes": weight_bytes + act_bytes, "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_tflops": round(tflops, 1),
+            "mfma_fp8_frac": round(tflops / PEAK_FP8_TFLOPS, 4),
+            "binding_roofline": "hbm" if (weight_bytes + act_bytes) / (PEAK_HBM_GBS * 1e9) > flops / (PEAK_FP8_TFLOPS * 1e12) else "mfma",
+            "finite": bool(torch.isfinite(y.float()).all().item()),
+        }
+        log(f"prefill {name}: {us:.1f} us, {gbs:.0f} GB/s, {tflops:.1f} TFLOP/s")
+    return out
+
+
+def cpu_baseline(args, layers, cfg, dev, torch, np):
+    """CPU oracle (C + OpenMP restatement of Direct decode) on the host cores,
+    timed on touched experts already copied to host memory."""
+    from oracle import oracle as O
+
+    syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
+    samples = []
+    warm = 2
+    for i in range(args.cpu_samples):
+        l = layers[i % len(layers)]
+        x = syn.normal_bf16((cfg.hidden_size,), syn.key(SEED, "cpu", i), device=dev)
+        xb = bits(x, torch, np)
+        w = l.gate.weight.cpu().numpy()
+        b = l.gate.e_score_correction_bias.cpu().numpy()
+        ids, _ = O.router(xb[None], w, b)
+        hb, hs = host_layer_subset(l, ids[0], torch, np)
+        t0 = time.perf_counter()
+        ids2, sc2 = O.router(xb[None], w, b)
+        O.decode_moe(xb, hb, np.arange(8), sc2[0], cfg.swiglu_limit, hs)
+        dt = time.perf_counter() - t0
+        if i >= warm:
+            samples.append(dt)
+    us = statistics.median(samples) * 1e6
+    cores = O.num_threads()
+    return {"value": round(us, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"median of {len(samples)} single-layer decodes (config-2 layer: router + 8 routed + shared) "
+                      f"after {warm} warmups; touched experts pre-copied to host; OpenMP threads={cores}; "
+                      f"CPU {cpu_model()}"}
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

@@ -21,6 +21,7 @@ LIB_PATH = Path(os.environ.get("GLM53_MOE_LIB", _PKG / "libglm53_moe.so"))
 
 OK, INVALID_ARGUMENT, BAD_STATE, DEVICE_ERROR = 0, 1, 2, 3
 REDUCE_GROUPED, REDUCE_DIRECT = 0, 1
+STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 4, 7
 
 _lib = None
 
@@ -69,15 +70,17 @@ _SIGNATURES = {
     "glm53_abi_version": (ctypes.c_int, []),
     "glm53_e4m3_scan_codes": (ctypes.c_int, [P, I64, P, P]),
     "glm53_fp8_linear_workspace_bytes": (SZ, [I64, I64, I64]),
-    "glm53_fp8_linear": (ctypes.c_int, [P, I64, I64, P, I64, P, P, P, SZ, P]),
+    "glm53_fp8_linear": (ctypes.c_int, [P, I64, I64, P, I64, P, P, P, P, SZ, P]),
     "glm53_router_workspace_bytes": (SZ, [I64, I64, I64]),
     "glm53_router_topk": (ctypes.c_int, [P, P, I64, P, P, P, SZ, P]),
     "glm53_decode_plan_create": (ctypes.c_int, [I64, I64, I64, I64, I64, F32, P]),
     "glm53_decode_plan_destroy": (None, [P]),
     "glm53_decode_moe_routed": (ctypes.c_int, [P, P, P, P, P, P, P, P]),
     "glm53_decode_moe": (ctypes.c_int, [P, P, P, P, P, P, P, P, P]),
+    "glm53_decode_moe_ex": (ctypes.c_int, [P, P, P, P, P, P, P, I32, P]),
     "glm53_decode_plan_bind": (ctypes.c_int, [P, P, P, P]),
     "glm53_decode_moe_bound": (ctypes.c_int, [P, P, P, P]),
+    "glm53_decode_plan_tune": (ctypes.c_int, [P, I32, I32]),
     "glm53_decode_plan_scratch": (ctypes.c_int, [P, I32, P, P]),
     "glm53_decode_plan_error_flag": (ctypes.c_int, [P, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),
@@ -96,6 +99,9 @@ _SIGNATURES = {
     "glm53_synth_fp8": (ctypes.c_int, [P, P, I64, I64, ctypes.c_uint64, F32, P]),
     "glm53_synth_f32": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, F32, F32, I32, P]),
     "glm53_synth_bf16": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, P]),
+    "glm53_synth_fp8_batched": (ctypes.c_int, [P, P, I64, I64, I64, I64, I64, ctypes.c_uint64, F32, P]),
+    "glm53_synth_step_input": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, P, P]),
+    "glm53_probe_read": (ctypes.c_int, [P, I64, P, I32, P]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -107,6 +107,7 @@ int check_bank(const glm53_bank* b, int64_t H, int64_t I, int64_t E) {
 
 int check_router(const glm53_router* r, int64_t H, int64_t E, int64_t k) {
   CHECK_ARG(r != nullptr && r->weight != nullptr && r->bias != nullptr, "router weight/bias is null");
+  CHECK_ARG(E <= kMaxRouterExperts, "router experts must be at most %d", kMaxRouterExperts);
   CHECK_ARG(r->hidden == H && r->experts == E, "router shape [%lld, %lld] != [%lld, %lld]", (long long)r->experts,
             (long long)r->hidden, (long long)E, (long long)H);
   CHECK_ARG(r->top_k == k, "router top_k %lld != plan top_k %lld", (long long)r->top_k, (long long)k);
@@ -178,7 +179,7 @@ int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* 
 }
 
 int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N, const float* scale_inv,
-                     void* y, void* workspace, size_t workspace_bytes, void* stream) {
+                     const int32_t* code_flags, void* y, void* workspace, size_t workspace_bytes, void* stream) {
   CHECK_ARG(M >= 0 && K > 0 && N > 0, "invalid shape M=%lld K=%lld N=%lld", (long long)M, (long long)K, (long long)N);
   if (M == 0) return GLM53_OK;
   CHECK_ARG(x && weight && scale_inv && y, "null pointer argument");
@@ -192,14 +193,19 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
     a.K = K;
     a.rows_per_wave = 4;
     a.y = static_cast<uint16_t*>(y);
+    a.flags = code_flags;
     HIP_TRY(launch_gemv(a, st), "gemv launch");
     return GLM53_OK;
   }
   const size_t need = glm53_fp8_linear_workspace_bytes(M, N, K);
   if (need > 0 && aligned(weight, 16) && workspace != nullptr && workspace_bytes >= need) {
     SplitBuf b = carve_split(workspace, M, K);
-    int32_t* flag = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + split_bytes(M, K));
-    HIP_TRY(launch_scan_480(weight, N * K, flag, true, st), "scan launch");
+    const int32_t* flag = code_flags;
+    if (flag == nullptr) {
+      int32_t* f = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + split_bytes(M, K));
+      HIP_TRY(launch_scan_480(weight, N * K, f, true, st), "scan launch");
+      flag = f;
+    }
     HIP_TRY(split(x, M, K, b, st), "split launch");
     GroupedGemmArgs g{};
     g.fixup = flag;
@@ -240,14 +246,15 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
 // ------------------------------------------------------------ router ------
 
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
-  if (tokens <= 1) return round_up(sizeof(float) * 2 * experts) + 256;
+  if (tokens <= 1) return round_up(sizeof(float) * experts);
   return round_up(sizeof(float) * tokens * hidden) + round_up(sizeof(float) * tokens * experts);
 }
 
 int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids, float* scores,
                       void* workspace, size_t workspace_bytes, void* stream) {
   CHECK_ARG(router && router->weight && router->bias, "router is null");
-  CHECK_ARG(router->experts > 0 && router->experts <= kMaxExperts, "experts must be in [1, %d]", kMaxExperts);
+  CHECK_ARG(router->experts > 0 && router->experts <= kMaxRouterExperts, "router experts must be in [1, %d]",
+            kMaxRouterExperts);
   CHECK_ARG(router->top_k > 0 && router->top_k <= kMaxTopK && router->top_k <= router->experts,
             "top_k must be in [1, %d]", kMaxTopK);
   CHECK_ARG(tokens >= 0, "tokens < 0");
@@ -257,27 +264,15 @@ int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens,
             "router workspace too small");
   hipStream_t st = S(stream);
   if (tokens == 1) {
-    float* sig = static_cast<float*>(workspace);
-    float* choice = sig + router->experts;
-    unsigned* arrivals = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(workspace) +
-                                                     round_up(sizeof(float) * 2 * router->experts));
-    HIP_TRY(hipMemsetAsync(arrivals, 0, sizeof(unsigned), st), "memset");
+    float* logits = static_cast<float*>(workspace);
     RouterArgs a{};
     a.x = static_cast<const uint16_t*>(x);
     a.weight = router->weight;
-    a.bias = router->bias;
     a.experts = router->experts;
     a.hidden = router->hidden;
-    a.top_k = static_cast<int>(router->top_k);
-    a.routed_scaling_factor = router->routed_scaling_factor;
-    a.norm_topk_prob = router->norm_topk_prob;
-    a.sigmoid_out = sig;
-    a.choice_out = choice;
-    a.arrivals = arrivals;
-    a.ids_out = ids;
-    a.scores_out = scores;
+    a.logits_out = logits;
     HIP_TRY(launch_router(a, st), "router launch");
-    return GLM53_OK;
+    return topk(logits, router, 1, ids, scores, st);
   }
   float* xf = static_cast<float*>(workspace);
   float* logits = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
@@ -295,9 +290,7 @@ struct glm53_decode_plan {
   float limit;
   // fixed scratch (allocated once)
   uint16_t* hidden = nullptr;  // [(k + 1) * max(I, Is)]
-  float* sig = nullptr;        // [E]
-  float* choice = nullptr;     // [E]
-  unsigned* arrivals = nullptr;
+  float* sig = nullptr;        // [E] router logits
   int32_t* ids = nullptr;      // [k]
   float* scores = nullptr;     // [k]
   int* err = nullptr;
@@ -309,8 +302,11 @@ struct glm53_decode_plan {
   uint16_t* shared_gate = nullptr;  // [Is]
   uint16_t* shared_up = nullptr;
   uint16_t* shared_out = nullptr;   // [H]
+  uint16_t* moe_out = nullptr;      // [H] before a residual add
   void* arena = nullptr;
   bool bound = false;
+  int gate_up_rows_per_wave = 8;   // launch shape (glm53_decode_plan_tune), swept on MI355X
+  int down_rows_per_wg = 16;
   glm53_bank bank{};
   glm53_shared_expert shared{};
   bool has_shared = false;
@@ -345,7 +341,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   size_t o_gate = take(2 * top_k * intermediate), o_up = take(2 * top_k * intermediate);
   size_t o_down = take(2 * top_k * hidden), o_routed = take(2 * hidden);
   size_t o_sg = take(2 * std::max<int64_t>(shared_intermediate, 1)), o_su = take(2 * std::max<int64_t>(shared_intermediate, 1));
-  size_t o_so = take(2 * hidden);
+  size_t o_so = take(2 * hidden), o_mo = take(2 * hidden);
   hipError_t e = hipMalloc(&p->arena, off);
   if (e != hipSuccess) {
     delete p;
@@ -360,8 +356,6 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   uint8_t* b = static_cast<uint8_t*>(p->arena);
   p->hidden = reinterpret_cast<uint16_t*>(b + o_hidden);
   p->sig = reinterpret_cast<float*>(b + o_sig);
-  p->choice = reinterpret_cast<float*>(b + o_choice);
-  p->arrivals = reinterpret_cast<unsigned*>(b + o_arr);
   p->ids = reinterpret_cast<int32_t*>(b + o_ids);
   p->scores = reinterpret_cast<float*>(b + o_scores);
   p->err = reinterpret_cast<int*>(b + o_err);
@@ -372,6 +366,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   p->shared_gate = reinterpret_cast<uint16_t*>(b + o_sg);
   p->shared_up = reinterpret_cast<uint16_t*>(b + o_su);
   p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
+  p->moe_out = reinterpret_cast<uint16_t*>(b + o_mo);
   *out = p;
   return GLM53_OK;
 }
@@ -441,13 +436,30 @@ int generic_linear(const void* x, int64_t x_group_stride, int64_t M, int64_t G, 
   return GLM53_OK;
 }
 
+// stages: bit 1 = routed + shared gate/up/SwiGLU, bit 2 = down + reduction
+// (+ shared, + residual).  The any-shape composition runs only whole.
+// With topk_router the selection runs from the plan's router logits (fused
+// into the gate/up launch on the fast path) and ids / scores are the plan's.
 int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared, const void* x,
-               const int32_t* ids, const float* scores, void* out, hipStream_t st) {
+               const int32_t* ids, const float* scores, const glm53_router* topk_router, const void* residual,
+               void* out, int stages, hipStream_t st) {
   const int64_t H = p->H, I = p->I, Is = p->Is, k = p->k;
+  if (topk_router != nullptr) {
+    ids = p->ids;
+    scores = p->scores;
+  }
   if (decode_fast_ok(p, bank, shared, x)) {
     GateUpArgs g{};
     g.x = static_cast<const uint16_t*>(x);
     g.expert_ids = ids;
+    if (topk_router != nullptr) {
+      g.router_logits = p->sig;
+      g.router_bias = topk_router->bias;
+      g.routed_scaling_factor = topk_router->routed_scaling_factor;
+      g.norm_topk_prob = topk_router->norm_topk_prob;
+      g.ids_out = p->ids;
+      g.scores_out = p->scores;
+    }
     g.top_k = static_cast<int>(k);
     g.experts = p->E;
     g.gate_up_weight = bank->gate_up_weight;
@@ -462,11 +474,16 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
     g.intermediate = I;
     g.shared_intermediate = shared != nullptr ? Is : 0;
     g.limit = p->limit;
-    g.rows_per_wave = 4;
+    g.rows_per_wave = p->gate_up_rows_per_wave;
     g.wgs_per_slot = cdiv(I, 4 * g.rows_per_wave);
     g.hidden_out = p->hidden;
     g.error_flag = p->err;
-    HIP_TRY(launch_gate_up(g, st), "gate/up launch");
+    g.routed_flags = bank->code_flags;
+    if (shared != nullptr) {
+      g.shared_flags = shared->gate.code_flags;
+      g.shared_flags2 = shared->up.code_flags;
+    }
+    if (stages & GLM53_STAGE_GATE_UP) HIP_TRY(launch_gate_up(g, st), "gate/up launch");
     DownArgs d{};
     d.hidden_in = p->hidden;
     d.expert_ids = ids;
@@ -481,12 +498,23 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
     }
     d.hidden = H;
     d.intermediate = I;
-    d.rows_per_wg = 8;
+    d.rows_per_wg = p->down_rows_per_wg;
+    d.residual = static_cast<const uint16_t*>(residual);
+    d.routed_flags = bank->code_flags;
+    if (shared != nullptr) d.shared_flags = shared->down.code_flags;
     d.out = static_cast<uint16_t*>(out);
     d.error_flag = p->err;
-    HIP_TRY(launch_down(d, st), "down launch");
+    if (stages & GLM53_STAGE_DOWN) HIP_TRY(launch_down(d, st), "down launch");
     return GLM53_OK;
   }
+  CHECK_ARG((stages & (GLM53_STAGE_GATE_UP | GLM53_STAGE_DOWN)) == (GLM53_STAGE_GATE_UP | GLM53_STAGE_DOWN),
+            "partial stages need the fused fast path (aligned pointers, supported widths)");
+  if (topk_router != nullptr) {
+    int rc0 = topk(p->sig, topk_router, 1, p->ids, p->scores, st);
+    if (rc0) return rc0;
+  }
+  uint16_t* final_out = static_cast<uint16_t*>(out);
+  if (residual != nullptr) out = p->moe_out;
   // Any-shape composition of the reference's separate stages
   // (packed.py:473-655): gate, up, SwiGLU, down, weighted reduction, shared.
   const int64_t SR = cdiv(I, 128), SC = cdiv(H, 128), SH = cdiv(H, 128), SI = cdiv(I, 128);
@@ -519,6 +547,8 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
   if (shared == nullptr) {
     wr.out = static_cast<uint16_t*>(out);
     HIP_TRY(launch_weighted_reduction(wr, st), "reduction launch");
+    if (residual != nullptr)
+      HIP_TRY(launch_add_bf16(static_cast<const uint16_t*>(residual), p->moe_out, final_out, H, st), "add launch");
     return GLM53_OK;
   }
   wr.out = p->routed;
@@ -544,6 +574,8 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
                            nullptr, 1, H, Is, p->shared_out, 0, p->err, st)))
     return rc;
   HIP_TRY(launch_add_bf16(p->routed, p->shared_out, static_cast<uint16_t*>(out), H, st), "add launch");
+  if (residual != nullptr)
+    HIP_TRY(launch_add_bf16(static_cast<const uint16_t*>(residual), p->moe_out, final_out, H, st), "add launch");
   return GLM53_OK;
 }
 
@@ -551,17 +583,9 @@ int run_router_decode(glm53_decode_plan* p, const glm53_router* r, const void* x
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.weight = r->weight;
-  a.bias = r->bias;
   a.experts = r->experts;
   a.hidden = r->hidden;
-  a.top_k = static_cast<int>(r->top_k);
-  a.routed_scaling_factor = r->routed_scaling_factor;
-  a.norm_topk_prob = r->norm_topk_prob;
-  a.sigmoid_out = p->sig;
-  a.choice_out = p->choice;
-  a.arrivals = p->arrivals;
-  a.ids_out = p->ids;
-  a.scores_out = p->scores;
+  a.logits_out = p->sig;  // the plan's [E] FP32 logits
   HIP_TRY(launch_router(a, st), "router launch");
   return GLM53_OK;
 }
@@ -573,7 +597,7 @@ int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank, con
   int rc = check_decode_inputs(plan, bank, shared);
   if (rc) return rc;
   CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
-  return run_decode(plan, bank, shared, x, expert_ids, scores, out, S(stream));
+  return run_decode(plan, bank, shared, x, expert_ids, scores, nullptr, nullptr, out, GLM53_STAGE_ALL, S(stream));
 }
 
 int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
@@ -585,7 +609,8 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm5
   CHECK_ARG(x && out, "null pointer argument");
   hipStream_t st = S(stream);
   if ((rc = run_router_decode(plan, router, x, st))) return rc;
-  if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, out, st))) return rc;
+  if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, nullptr, out, GLM53_STAGE_ALL, st)))
+    return rc;
   if (ids_out) HIP_TRY(hipMemcpyAsync(ids_out, plan->ids, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy ids");
   if (scores_out)
     HIP_TRY(hipMemcpyAsync(scores_out, plan->scores, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy scores");
@@ -615,8 +640,37 @@ int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, vo
   hipStream_t st = S(stream);
   int rc = run_router_decode(plan, &plan->router, x, st);
   if (rc) return rc;
-  return run_decode(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, x, plan->ids, plan->scores, out,
-                    st);
+  return run_decode(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, x, plan->ids, plan->scores,
+                    &plan->router, nullptr, out, GLM53_STAGE_ALL, st);
+}
+
+int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
+                        const glm53_router* router, const void* x, const void* residual, void* out, int32_t stages,
+                        void* stream) {
+  int rc = check_decode_inputs(plan, bank, shared);
+  if (rc) return rc;
+  CHECK_ARG(x && out, "null pointer argument");
+  CHECK_ARG(stages > 0 && (stages & ~GLM53_STAGE_ALL) == 0, "invalid stage mask %d", stages);
+  hipStream_t st = S(stream);
+  if (stages & (GLM53_STAGE_ROUTER | GLM53_STAGE_GATE_UP)) {
+    if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  }
+  if (stages & GLM53_STAGE_ROUTER) {
+    if ((rc = run_router_decode(plan, router, x, st))) return rc;
+  }
+  if (stages & (GLM53_STAGE_GATE_UP | GLM53_STAGE_DOWN))
+    return run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, residual, out, stages, st);
+  return GLM53_OK;
+}
+
+int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wave, int32_t down_rows_per_wg) {
+  CHECK_ARG(plan != nullptr, "plan is null");
+  CHECK_ARG(gate_up_rows_per_wave >= 1 && gate_up_rows_per_wave <= 64, "gate_up_rows_per_wave must be in [1, 64]");
+  CHECK_ARG(down_rows_per_wg >= 1 && down_rows_per_wg <= kMaxDownRowsPerWg, "down_rows_per_wg must be in [1, %d]",
+            kMaxDownRowsPerWg);
+  plan->gate_up_rows_per_wave = gate_up_rows_per_wave;
+  plan->down_rows_per_wg = down_rows_per_wg;
+  return GLM53_OK;
 }
 
 int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes) {
@@ -1152,11 +1206,29 @@ int glm53_sigmoid_bf16(const void* gate, int64_t n, void* out, void* stream) {
 
 int glm53_synth_fp8(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, uint64_t seed, float std,
                     void* stream) {
-  CHECK_ARG(rows >= 0 && cols >= 0, "invalid dimensions");
-  if (rows == 0 || cols == 0) return GLM53_OK;
+  return glm53_synth_fp8_batched(codes, scale_inv, rows, cols, 1, 0, 0, seed, std, stream);
+}
+
+int glm53_synth_fp8_batched(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, int64_t batch,
+                            int64_t codes_stride, int64_t scale_stride, uint64_t seed, float std, void* stream) {
+  CHECK_ARG(rows >= 0 && cols >= 0 && batch >= 0 && batch < 65536, "invalid dimensions");
+  if (rows == 0 || cols == 0 || batch == 0) return GLM53_OK;
   CHECK_ARG(codes && scale_inv, "null pointer argument");
-  SynthFp8Args a{codes, scale_inv, rows, cols, seed, std};
+  SynthFp8Args a{codes, scale_inv, rows, cols, seed, std, batch, codes_stride, scale_stride};
   HIP_TRY(launch_synth_fp8(a, S(stream)), "synth launch");
+  return GLM53_OK;
+}
+
+int glm53_probe_read(const void* buf, int64_t bytes, uint32_t* sink, int32_t blocks, void* stream) {
+  CHECK_ARG(buf && sink && bytes >= 0 && blocks > 0 && blocks <= (1 << 20), "invalid arguments");
+  CHECK_ARG(aligned(buf, 16), "buffer must be 16-byte aligned");
+  HIP_TRY(launch_probe_read(static_cast<const uint8_t*>(buf), bytes, sink, blocks, S(stream)), "probe launch");
+  return GLM53_OK;
+}
+
+int glm53_synth_step_input(void* out, int64_t n, uint64_t seed, float std, uint32_t* counter, void* stream) {
+  CHECK_ARG(n >= 0 && out && counter, "invalid arguments");
+  HIP_TRY(launch_synth_step_input(static_cast<uint16_t*>(out), n, seed, std, counter, S(stream)), "synth launch");
   return GLM53_OK;
 }
 

@@ -20,16 +20,17 @@ namespace glm53 {
 // ------------------------------------------------------------ helpers ----
 
 // A lane's activation slice: CH chunks of VB consecutive elements at
-// positions VB*lane + 64*VB*c, held as FP16 pairs (x0,x2),(x1,x3) per 4.
-template <int VB, int CH>
+// positions VB*lane + 64*VB*c, held as FP16 pairs.  HW = true pairs them
+// (x0,x1),(x2,x3) for the gfx950 E4M3->FP16 converter; HW = false pairs
+// them (x0,x2),(x1,x3) for the exact SWAR decode in common.h.
+template <int VB, int CH, bool HW>
 struct XSlice {
   uint32_t p[CH][VB / 2];
-  float factor;  // 2^(8 + shift): E4M3->FP16 bias and the activation shift
+  float factor;  // 2^shift (HW) or 2^(8 + shift) (SWAR bias of 2^-8)
 };
 
-template <int VB, int CH>
-__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane,
-                                             XSlice<VB, CH>& xs) {
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane, XSlice<VB, CH, HW>& xs) {
   float v[CH][VB];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -50,15 +51,20 @@ __device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int
   for (int c = 0; c < CH; ++c)
 #pragma unroll
     for (int i = 0; i < VB; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
-  int shift = f16_shift_for(amax);
-  float down = ldexpf(1.0f, -shift);
-  xs.factor = ldexpf(1.0f, 8 + shift);
+  const int shift = f16_shift_for(amax);
+  const float down = ldexpf(1.0f, -shift);
+  xs.factor = ldexpf(1.0f, (HW ? 0 : 8) + shift);
 #pragma unroll
   for (int c = 0; c < CH; ++c)
 #pragma unroll
     for (int j = 0; j < VB / 4; ++j) {
-      xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 2] * down);
-      xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 1] * down, v[c][4 * j + 3] * down);
+      if (HW) {
+        xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 1] * down);
+        xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 2] * down, v[c][4 * j + 3] * down);
+      } else {
+        xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 2] * down);
+        xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 1] * down, v[c][4 * j + 3] * down);
+      }
     }
 }
 
@@ -88,27 +94,41 @@ struct WChunk<8> {
 
 // Unscaled partial dot of one chunk (VB weight bytes) with the lane's
 // activations of that chunk.
-template <int VB, int CH>
-__device__ __forceinline__ float chunk_dot(const WChunk<VB>& w, const XSlice<VB, CH>& xs, int c) {
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ float chunk_dot(const WChunk<VB>& w, const XSlice<VB, CH, HW>& xs, int c) {
   float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < VB / 4; ++j) acc = dot4_e4m3(w.word(j), xs.p[c][2 * j], xs.p[c][2 * j + 1], acc);
+  for (int j = 0; j < VB / 4; ++j) {
+    if (HW) {
+      // v_cvt_scalef32_pk_f16_fp8: two E4M3 bytes -> two exact FP16 (OCP;
+      // only used when the weights hold no 0x7F / 0xFF code)
+      const half2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.word(j), 1.0f, false);
+      const half2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.word(j), 1.0f, true);
+      acc = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(half2_t, xs.p[c][2 * j]), acc, false);
+      acc = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(half2_t, xs.p[c][2 * j + 1]), acc, false);
+    } else {
+      acc = dot4_e4m3(w.word(j), xs.p[c][2 * j], xs.p[c][2 * j + 1], acc);
+    }
+  }
   return acc;
 }
 
-// Lane partial of row `row` of a [rows, K] E4M3 matrix whose block-scale
-// row is `srow` (a pointer to the row's SC scales).
-template <int VB, int CH>
+// Lane partial of one row whose block-scale row is `srow` (SC scales).
+template <int VB, int CH, bool HW>
 __device__ __forceinline__ float row_partial(const WChunk<VB> (&w)[CH], const float* __restrict__ srow,
-                                             const XSlice<VB, CH>& xs, int lane) {
+                                             const XSlice<VB, CH, HW>& xs, int lane) {
   float acc = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float s = srow[(VB * lane + 64 * VB * c) >> 7];
-    acc += chunk_dot<VB, CH>(w[c], xs, c) * s;
+    acc += chunk_dot<VB, CH, HW>(w[c], xs, c) * s;
   }
   return acc * xs.factor;
 }
+
+// The register decode is usable unless a (device) scan flagged 0x7F / 0xFF
+// codes; a null flag means "not scanned" and keeps the exact SWAR decode.
+__device__ __forceinline__ bool hw_decode_ok(const int32_t* flag) { return flag != nullptr && *flag == 0; }
 
 template <int VB, int CH>
 __device__ __forceinline__ void load_row(WChunk<VB> (&w)[CH], const uint8_t* __restrict__ row, int lane) {
@@ -120,6 +140,96 @@ __device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
   return e < 0 || static_cast<int64_t>(e) >= experts;
 }
 
+// 64-bit top-k key: order-preserving bits of the choice score above the
+// complemented expert id, so max(key) = max score, then min id.  NaN -> -inf.
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t id) {
+  if (v != v) v = -__builtin_inff();
+  uint32_t u = __float_as_uint(v);
+  u ^= (u & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u;
+  return (static_cast<uint64_t>(u) << 32) | (0xFFFFFFFFu - id);
+}
+
+// ------------------------------------------------------------------ top-k --
+//
+// Selection half of the router (patch.py:131-142 with the DeepSeek-V3
+// aux-loss-free rule): one wavefront reads the FP32 logits of one token,
+// forms sigma = sigmoid(logit) and choice = sigma + bias, and picks top_k by
+// (choice desc, expert id asc).  Lane l holds candidates l, l+64, ... as
+// 64-bit keys, so each round is one max-reduction.  Weights = sigma of the
+// picks, normalised in slot order when norm, times the scaling factor.
+// Emits ids[slot] / weights[slot] (lane 0 stores; dst may be LDS or global).
+// PER_LANE = candidates per lane, a compile-time bound (experts <= 64 *
+// PER_LANE) that keeps the selection in a handful of registers.
+template <int PER_LANE>
+__device__ __forceinline__ void wave_topk_emit(const float* __restrict__ logits, const float* __restrict__ bias,
+                                               int64_t experts, int top_k, float scaling, int norm, int lane,
+                                               int32_t* ids_dst, float* w_dst) {
+  uint64_t keys[PER_LANE];
+  float sigs[PER_LANE];
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    const int64_t c = lane + 64 * i;
+    float sg = 0.0f;
+    keys[i] = 0ull;
+    if (c < experts) {
+      sg = 1.0f / (1.0f + expf(-logits[c]));
+      keys[i] = topk_key(__fadd_rn(sg, bias[c]), static_cast<uint32_t>(c));
+    }
+    sigs[i] = sg;
+  }
+  float total = 0.0f;
+#pragma unroll 1
+  for (int slot = 0; slot < top_k; ++slot) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) best = keys[i] > best ? keys[i] : best;
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint64_t other = __shfl_xor(best, off);
+      best = other > best ? other : best;
+    }
+    const int32_t best_id = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) {
+      if (keys[i] == best) {
+        mine = sigs[i];
+        keys[i] = 0ull;  // taken
+      }
+    }
+    const float w = __shfl(mine, best_id & 63);
+    total = __fadd_rn(total, w);
+    if (lane == 0) {
+      ids_dst[slot] = best_id;
+      w_dst[slot] = w;
+    }
+  }
+  if (lane == 0) {
+    for (int slot = 0; slot < top_k; ++slot) {
+      float v = w_dst[slot];
+      if (top_k > 1 && norm) v = v / total;
+      w_dst[slot] = __fmul_rn(v, scaling);
+    }
+  }
+}
+
+__device__ __forceinline__ void wave_topk(const float* __restrict__ logits, const float* __restrict__ bias,
+                                          int64_t experts, int top_k, float scaling, int norm, int lane,
+                                          int32_t* ids_dst, float* w_dst) {
+  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+  else if (experts <= 320) wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+  else wave_topk_emit<kMaxRouterExperts / 64>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+}
+
+// Narrow form for the gate/up prologue (experts <= 320; wider routers select
+// in topk_kernel first), so the selection never raises the streaming kernel's
+// register count.
+__device__ __forceinline__ void wave_topk_narrow(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                 int64_t experts, int top_k, float scaling, int norm, int lane,
+                                                 int32_t* ids_dst, float* w_dst) {
+  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+  else wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+}
+
 // --------------------------------------------- fused routed gate/up/SwiGLU --
 //
 // packed.py:100-166 for the top_k selected experts (slots 0..k-1) plus, as
@@ -127,8 +237,52 @@ __device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
 // `rows_per_wave` consecutive intermediate rows r of one slot: it streams
 // gate row r and up row r (the bank's rows r and I + r), and lane 0 stores
 // h = SwiGLU(T(gate), T(up)) with the reference's rounding sequence.
+//
+// With router logits given, wavefront 0 of every routed workgroup runs the
+// top-k itself (288 logits from L2), so the router launch needs no
+// cross-workgroup reduction; workgroup 0 also publishes ids and weights for
+// the down kernel.
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const uint8_t* __restrict__ gate_w,
+                                             const uint8_t* __restrict__ up_w, const float* __restrict__ gate_s,
+                                             const float* __restrict__ up_s, uint16_t* __restrict__ out,
+                                             int64_t r0, int64_t r_end, int lane) {
+  const int64_t K = a.hidden;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+  XSlice<VB, CH, HW> xs;
+  load_x_slice<VB, CH, HW>(a.x, lane, xs);
+  int64_t r = r0;
+  for (; r + 1 < r_end; r += 2) {
+    WChunk<VB> g0[CH], u0[CH], g1[CH], u1[CH];
+    load_row<VB, CH>(g0, gate_w + r * K, lane);
+    load_row<VB, CH>(u0, up_w + r * K, lane);
+    load_row<VB, CH>(g1, gate_w + (r + 1) * K, lane);
+    load_row<VB, CH>(u1, up_w + (r + 1) * K, lane);
+    float pg0 = row_partial<VB, CH, HW>(g0, gate_s + (r >> 7) * SC, xs, lane);
+    float pu0 = row_partial<VB, CH, HW>(u0, up_s + (r >> 7) * SC, xs, lane);
+    float pg1 = row_partial<VB, CH, HW>(g1, gate_s + ((r + 1) >> 7) * SC, xs, lane);
+    float pu1 = row_partial<VB, CH, HW>(u1, up_s + ((r + 1) >> 7) * SC, xs, lane);
+    float tg0 = wave_sum(pg0), tu0 = wave_sum(pu0);
+    float tg1 = wave_sum(pg1), tu1 = wave_sum(pu1);
+    if (lane == 0) {
+      out[r] = swiglu_mlx(tg0, tu0, a.limit);
+      out[r + 1] = swiglu_mlx(tg1, tu1, a.limit);
+    }
+  }
+  if (r < r_end) {
+    WChunk<VB> g0[CH], u0[CH];
+    load_row<VB, CH>(g0, gate_w + r * K, lane);
+    load_row<VB, CH>(u0, up_w + r * K, lane);
+    float tg0 = wave_sum(row_partial<VB, CH, HW>(g0, gate_s + (r >> 7) * SC, xs, lane));
+    float tu0 = wave_sum(row_partial<VB, CH, HW>(u0, up_s + (r >> 7) * SC, xs, lane));
+    if (lane == 0) out[r] = swiglu_mlx(tg0, tu0, a.limit);
+  }
+}
+
 template <int VB, int CH>
 __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
+  __shared__ int32_t s_ids[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slots_routed = a.top_k;
@@ -144,6 +298,25 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
     chunk = bid - slots_routed * a.wgs_per_slot;
     rows = a.shared_intermediate;
   }
+  int32_t e = 0;
+  if (slot < slots_routed) {
+    if (a.router_logits != nullptr) {  // uniform per workgroup
+      if (wave == 0) {
+        wave_topk_narrow(a.router_logits, a.router_bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
+                  lane, s_ids, s_w);
+        if (lane == 0 && bid == 0) {
+          for (int s = 0; s < a.top_k; ++s) {
+            a.ids_out[s] = s_ids[s];
+            a.scores_out[s] = s_w[s];
+          }
+        }
+      }
+      __syncthreads();
+      e = s_ids[slot];
+    } else {
+      e = a.expert_ids[slot];
+    }
+  }
   const int64_t r0 = (static_cast<int64_t>(chunk) * 4 + wave) * a.rows_per_wave;
   if (r0 >= rows) return;
   const int64_t K = a.hidden;
@@ -155,7 +328,6 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
   const float* up_s;
   uint16_t* out;
   if (slot < slots_routed) {
-    int32_t e = a.expert_ids[slot];
     out = a.hidden_out + static_cast<int64_t>(slot) * a.intermediate;
     if (bad_expert(e, a.experts)) {
       if (lane == 0) {
@@ -177,120 +349,107 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
     up_s = a.shared_up_scale;
   }
 
-  XSlice<VB, CH> xs;
-  load_x_slice<VB, CH>(a.x, lane, xs);
-
   const int64_t r_end = (r0 + a.rows_per_wave < rows) ? r0 + a.rows_per_wave : rows;
-  int64_t r = r0;
-  for (; r + 1 < r_end; r += 2) {
-    WChunk<VB> g0[CH], u0[CH], g1[CH], u1[CH];
-    load_row<VB, CH>(g0, gate_w + r * K, lane);
-    load_row<VB, CH>(u0, up_w + r * K, lane);
-    load_row<VB, CH>(g1, gate_w + (r + 1) * K, lane);
-    load_row<VB, CH>(u1, up_w + (r + 1) * K, lane);
-    float pg0 = row_partial<VB, CH>(g0, gate_s + (r >> 7) * SC, xs, lane);
-    float pu0 = row_partial<VB, CH>(u0, up_s + (r >> 7) * SC, xs, lane);
-    float pg1 = row_partial<VB, CH>(g1, gate_s + ((r + 1) >> 7) * SC, xs, lane);
-    float pu1 = row_partial<VB, CH>(u1, up_s + ((r + 1) >> 7) * SC, xs, lane);
-    float tg0 = wave_sum(pg0), tu0 = wave_sum(pu0);
-    float tg1 = wave_sum(pg1), tu1 = wave_sum(pu1);
-    if (lane == 0) {
-      out[r] = swiglu_mlx(tg0, tu0, a.limit);
-      out[r + 1] = swiglu_mlx(tg1, tu1, a.limit);
-    }
-  }
-  if (r < r_end) {
-    WChunk<VB> g0[CH], u0[CH];
-    load_row<VB, CH>(g0, gate_w + r * K, lane);
-    load_row<VB, CH>(u0, up_w + r * K, lane);
-    float tg0 = wave_sum(row_partial<VB, CH>(g0, gate_s + (r >> 7) * SC, xs, lane));
-    float tu0 = wave_sum(row_partial<VB, CH>(u0, up_s + (r >> 7) * SC, xs, lane));
-    if (lane == 0) out[r] = swiglu_mlx(tg0, tu0, a.limit);
-  }
+  if (slot < slots_routed ? hw_decode_ok(a.routed_flags)
+                           : (hw_decode_ok(a.shared_flags) && hw_decode_ok(a.shared_flags2)))
+    gate_up_rows<VB, CH, true>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, lane);
+  else
+    gate_up_rows<VB, CH, false>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, lane);
 }
 
 // ------------------------------------- fused down + reduction + shared add --
 //
 // packed.py:66-98 (down for the k slots), packed.py:168-179 (ordered FP32
 // weighted reduction), fp8.py:254-299 (shared down GEMV) and
-// native_indexer_plan.metal:525-535 (BF16 add), in one launch.  A
-// workgroup of three wavefronts owns `rows_per_wg` output rows h; wave w
-// computes the down dot products of slots w, w+3, w+6 (slot k = shared) for
-// those rows, parks T(dot) in LDS, and the first rows_per_wg lanes then do
-// out[h] = T( T(sum_s T(down[s,h]) * score[s]) + T(shared[h]) ) in slot order.
+// native_indexer_plan.metal:525-535 (BF16 add), in one launch.  A workgroup
+// has one wavefront per slot (the k routed slots, then the shared expert)
+// and owns `rows_per_wg` output rows h: each wavefront loads its slot's
+// hidden vector once and issues the loads of all its rows in batches of 8
+// before reducing any, parks T(dot) in LDS, and the first rows_per_wg lanes
+// then form out[h] = T( T(sum_s T(down[s,h]) * score[s]) + T(shared[h]) ),
+// summed in slot order (and T(residual[h] + that) with a residual).
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ void down_rows(const DownArgs& a, const uint8_t* __restrict__ w,
+                                          const float* __restrict__ s, float* parked_row, int slot, int64_t h0,
+                                          int64_t h_end, int lane) {
+  const int64_t K = a.intermediate;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+  XSlice<VB, CH, HW> xs;
+  load_x_slice<VB, CH, HW>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, xs);
+  for (int64_t hb = h0; hb < h_end; hb += 8) {
+    WChunk<VB> rowsv[8][CH];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (hb + j < h_end) load_row<VB, CH>(rowsv[j], w + (hb + j) * K, lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (hb + j < h_end) {
+        const float t = wave_sum(row_partial<VB, CH, HW>(rowsv[j], s + ((hb + j) >> 7) * SC, xs, lane));
+        if (lane == 0) parked_row[hb + j - h0] = bf16_round(t);
+      }
+    }
+  }
+}
+
 template <int VB, int CH>
-__global__ __launch_bounds__(192) void down_reduce_kernel(DownArgs a) {
-  __shared__ float parked[9][kMaxDownRowsPerWg];
+__global__ __launch_bounds__(64 * (kMaxTopK + 1)) void down_reduce_kernel(DownArgs a) {
+  __shared__ float parked[kMaxTopK + 1][kMaxDownRowsPerWg];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int slot = threadIdx.x >> 6;
   const int64_t h0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_wg;
   const int64_t K = a.intermediate;
   const int64_t SC = (K + kBlock - 1) / kBlock;
   const int64_t SH = (a.hidden + kBlock - 1) / kBlock;
-  const int nslots = a.top_k + (a.shared_down_weight != nullptr ? 1 : 0);
   const int64_t h_end = (h0 + a.rows_per_wg < a.hidden) ? h0 + a.rows_per_wg : a.hidden;
 
-  for (int slot = wave; slot < nslots; slot += 3) {
-    const uint8_t* w;
-    const float* s;
-    if (slot < a.top_k) {
-      int32_t e = a.expert_ids[slot];
-      if (bad_expert(e, a.experts)) {
-        if (lane == 0) atomicOr(a.error_flag, 1);
-        for (int64_t h = h0; h < h_end; ++h) parked[slot][h - h0] = __builtin_nanf("");
-        continue;
-      }
+  const uint8_t* w = nullptr;
+  const float* s = nullptr;
+  bool ok = true;
+  if (slot < a.top_k) {
+    const int32_t e = a.expert_ids[slot];
+    if (bad_expert(e, a.experts)) {
+      ok = false;
+      if (lane == 0) atomicOr(a.error_flag, 1);
+    } else {
       w = a.down_weight + static_cast<int64_t>(e) * a.hidden * K;
       s = a.down_scale + static_cast<int64_t>(e) * SH * SC;
-    } else {
-      w = a.shared_down_weight;
-      s = a.shared_down_scale;
     }
-    XSlice<VB, CH> xs;
-    load_x_slice<VB, CH>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, xs);
-    int64_t h = h0;
-    for (; h + 1 < h_end; h += 2) {
-      WChunk<VB> w0[CH], w1[CH];
-      load_row<VB, CH>(w0, w + h * K, lane);
-      load_row<VB, CH>(w1, w + (h + 1) * K, lane);
-      float t0 = wave_sum(row_partial<VB, CH>(w0, s + (h >> 7) * SC, xs, lane));
-      float t1 = wave_sum(row_partial<VB, CH>(w1, s + ((h + 1) >> 7) * SC, xs, lane));
-      if (lane == 0) {
-        parked[slot][h - h0] = bf16_round(t0);
-        parked[slot][h + 1 - h0] = bf16_round(t1);
-      }
-    }
-    if (h < h_end) {
-      WChunk<VB> w0[CH];
-      load_row<VB, CH>(w0, w + h * K, lane);
-      float t0 = wave_sum(row_partial<VB, CH>(w0, s + (h >> 7) * SC, xs, lane));
-      if (lane == 0) parked[slot][h - h0] = bf16_round(t0);
-    }
+  } else {
+    w = a.shared_down_weight;
+    s = a.shared_down_scale;
+  }
+  if (ok) {
+    const int32_t* flag = slot < a.top_k ? a.routed_flags : a.shared_flags;
+    if (hw_decode_ok(flag))
+      down_rows<VB, CH, true>(a, w, s, parked[slot], slot, h0, h_end, lane);
+    else
+      down_rows<VB, CH, false>(a, w, s, parked[slot], slot, h0, h_end, lane);
+  } else {
+    for (int64_t h = h0 + lane; h < h_end; h += 64) parked[slot][h - h0] = __builtin_nanf("");
   }
   __syncthreads();
   const int t = threadIdx.x;
   if (t < h_end - h0) {
     float total = 0.0f;
-    for (int slot = 0; slot < a.top_k; ++slot) {
-      total = __fadd_rn(total, __fmul_rn(parked[slot][t], a.scores[slot]));
+    for (int sl = 0; sl < a.top_k; ++sl) total = __fadd_rn(total, __fmul_rn(parked[sl][t], a.scores[sl]));
+    float result = bf16_round(total);
+    if (a.shared_down_weight != nullptr) result = __fadd_rn(result, parked[a.top_k][t]);
+    if (a.residual != nullptr) {
+      // decoder residual x + T(moe(x)): the MoE output is rounded first, as
+      // it is when the decoder layer adds it outside the MoE module
+      result = __fadd_rn(bf16_to_f32(a.residual[h0 + t]), bf16_round(result));
     }
-    float routed = bf16_round(total);
-    float result = routed;
-    if (a.shared_down_weight != nullptr) result = __fadd_rn(routed, parked[a.top_k][t]);
     a.out[h0 + t] = f32_to_bf16(result);
   }
 }
 
 // ----------------------------------------------------------------- router --
 //
-// patch.py:131-142: logits = x_f32 . W_f32^T (FP32), sigmoid, +bias for the
-// choice, top-k ordered by (choice desc, expert id asc), weights =
-// sigmoid[ids] normalised and scaled (scripts/sweep_grouped_fp8_suffix.py:
-// 84-91).  One workgroup per expert row; the last workgroup to finish (a
-// self-resetting arrival counter) selects the top-k with one wavefront.
-__global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
+// patch.py:133: logits = x_f32 . W_f32^T in FP32, one workgroup per expert
+// row (16 KB for H = 4096), no cross-workgroup traffic; selection runs in the
+// consumer (gate/up prologue or topk_kernel).
+__global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
   __shared__ float partial[4];
-  __shared__ int last;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t e = blockIdx.x;
@@ -311,71 +470,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
   acc = wave_sum(acc);
   if (lane == 0) partial[wave] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float logit = (partial[0] + partial[1]) + (partial[2] + partial[3]);
-    float sig = 1.0f / (1.0f + expf(-logit));
-    a.sigmoid_out[e] = sig;
-    a.choice_out[e] = __fadd_rn(sig, a.bias[e]);
-    __threadfence();
-    unsigned prev = atomicAdd(a.arrivals, 1u);
-    last = (prev == gridDim.x - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!last || wave != 0) return;
-  __threadfence();
-  // One wavefront: top_k rounds of a 64-lane argmax over (choice, -id).
-  // Lane l holds candidates l, l+64, ... in registers; NaN choices rank as
-  // -inf so they are only ever picked after every finite score.
-  const volatile float* choice = a.choice_out;
-  const volatile float* sig = a.sigmoid_out;
-  constexpr int kPerLane = kMaxExperts / 64;
-  float vals[kPerLane];
-#pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
-    int64_t c = lane + 64 * i;
-    float v = c < a.experts ? choice[c] : -__builtin_inff();
-    vals[i] = (v != v) ? -__builtin_inff() : v;
-  }
-  uint32_t taken = 0;
-  float total = 0.0f;
-  float picked[kMaxTopK];
-  int32_t picked_id[kMaxTopK];
-  for (int slot = 0; slot < a.top_k; ++slot) {
-    float best = -__builtin_inff();
-    int32_t best_id = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      int32_t c = lane + 64 * i;
-      bool ok = c < a.experts && !((taken >> i) & 1u);
-      if (ok && (best_id == 0x7fffffff || vals[i] > best || (vals[i] == best && c < best_id))) {
-        best = vals[i];
-        best_id = c;
-      }
-    }
-    // wave argmax: larger value wins, ties go to the smaller id
-    for (int off = 32; off >= 1; off >>= 1) {
-      float ov = __shfl_xor(best, off);
-      int32_t oid = __shfl_xor(best_id, off);
-      if (oid != 0x7fffffff && (best_id == 0x7fffffff || ov > best || (ov == best && oid < best_id))) {
-        best = ov;
-        best_id = oid;
-      }
-    }
-    if (best_id == 0x7fffffff) best_id = 0;
-    if ((best_id & 63) == lane) taken |= 1u << (best_id >> 6);
-    picked_id[slot] = best_id;
-    picked[slot] = sig[best_id];
-    total = __fadd_rn(total, picked[slot]);
-  }
-  if (lane == 0) {
-    for (int slot = 0; slot < a.top_k; ++slot) {
-      float v = picked[slot];
-      if (a.top_k > 1 && a.norm_topk_prob) v = v / total;
-      a.ids_out[slot] = picked_id[slot];
-      a.scores_out[slot] = __fmul_rn(v, a.routed_scaling_factor);
-    }
-    *a.arrivals = 0u;  // self-reset for the next launch on this plan
-  }
+  if (threadIdx.x == 0) a.logits_out[e] = (partial[0] + partial[1]) + (partial[2] + partial[3]);
 }
 
 // ---------------------------------------------------------- plain GEMV ----
@@ -383,17 +478,12 @@ __global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
 // fp8.py:41-72 `block_fp8_linear` for one activation row: y[n] = T(sum_k
 // x[k] * LUT[w[n,k]] * s[n/128, k/128]).  Wave w of a workgroup streams
 // rows [rows_per_wave * (4 * block + w), ...).
-template <int VB, int CH>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * a.rows_per_wave;
-  if (n0 >= a.N) return;
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ void gemv_rows(const GemvArgs& a, int64_t n0, int64_t n_end, int lane) {
   const int64_t K = a.K;
   const int64_t SC = (K + kBlock - 1) / kBlock;
-  XSlice<VB, CH> xs;
-  load_x_slice<VB, CH>(a.x, lane, xs);
-  const int64_t n_end = (n0 + a.rows_per_wave < a.N) ? n0 + a.rows_per_wave : a.N;
+  XSlice<VB, CH, HW> xs;
+  load_x_slice<VB, CH, HW>(a.x, lane, xs);
   int64_t n = n0;
   for (; n + 3 < n_end; n += 4) {
     WChunk<VB> w0[CH], w1[CH], w2[CH], w3[CH];
@@ -401,10 +491,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     load_row<VB, CH>(w1, a.weight + (n + 1) * K, lane);
     load_row<VB, CH>(w2, a.weight + (n + 2) * K, lane);
     load_row<VB, CH>(w3, a.weight + (n + 3) * K, lane);
-    float t0 = wave_sum(row_partial<VB, CH>(w0, a.scale + (n >> 7) * SC, xs, lane));
-    float t1 = wave_sum(row_partial<VB, CH>(w1, a.scale + ((n + 1) >> 7) * SC, xs, lane));
-    float t2 = wave_sum(row_partial<VB, CH>(w2, a.scale + ((n + 2) >> 7) * SC, xs, lane));
-    float t3 = wave_sum(row_partial<VB, CH>(w3, a.scale + ((n + 3) >> 7) * SC, xs, lane));
+    float t0 = wave_sum(row_partial<VB, CH, HW>(w0, a.scale + (n >> 7) * SC, xs, lane));
+    float t1 = wave_sum(row_partial<VB, CH, HW>(w1, a.scale + ((n + 1) >> 7) * SC, xs, lane));
+    float t2 = wave_sum(row_partial<VB, CH, HW>(w2, a.scale + ((n + 2) >> 7) * SC, xs, lane));
+    float t3 = wave_sum(row_partial<VB, CH, HW>(w3, a.scale + ((n + 3) >> 7) * SC, xs, lane));
     if (lane == 0) {
       a.y[n] = f32_to_bf16(t0);
       a.y[n + 1] = f32_to_bf16(t1);
@@ -415,78 +505,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   for (; n < n_end; ++n) {
     WChunk<VB> w0[CH];
     load_row<VB, CH>(w0, a.weight + n * K, lane);
-    float t0 = wave_sum(row_partial<VB, CH>(w0, a.scale + (n >> 7) * SC, xs, lane));
+    float t0 = wave_sum(row_partial<VB, CH, HW>(w0, a.scale + (n >> 7) * SC, xs, lane));
     if (lane == 0) a.y[n] = f32_to_bf16(t0);
   }
 }
 
+template <int VB, int CH>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * a.rows_per_wave;
+  if (n0 >= a.N) return;
+  const int64_t K = a.K;
+  const int64_t SC = (K + kBlock - 1) / kBlock;
+  const int64_t n_end = (n0 + a.rows_per_wave < a.N) ? n0 + a.rows_per_wave : a.N;
+  if (hw_decode_ok(a.flags)) gemv_rows<VB, CH, true>(a, n0, n_end, lane);
+  else gemv_rows<VB, CH, false>(a, n0, n_end, lane);
+}
+
 // ------------------------------------------------------ per-token top-k ----
-//
-// Selection half of the router for many tokens (prefill): one wavefront per
-// token reads its FP32 logits row, forms sigmoid and the biased choice, and
-// runs the same (choice desc, id asc) top-k as the decode router.
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= a.tokens) return;
-  const float* row = a.logits + t * a.experts;
-  constexpr int kPerLane = kMaxExperts / 64;
-  float vals[kPerLane];
-  float sigs[kPerLane];
-#pragma unroll
-  for (int i = 0; i < kPerLane; ++i) {
-    int64_t c = lane + 64 * i;
-    float sg = 0.0f, v = -__builtin_inff();
-    if (c < a.experts) {
-      sg = 1.0f / (1.0f + expf(-row[c]));
-      v = __fadd_rn(sg, a.bias[c]);
-      if (v != v) v = -__builtin_inff();
-    }
-    sigs[i] = sg;
-    vals[i] = v;
-  }
-  uint32_t taken = 0;
-  float total = 0.0f;
-  float picked[kMaxTopK];
-  int32_t picked_id[kMaxTopK];
-  for (int slot = 0; slot < a.top_k; ++slot) {
-    float best = -__builtin_inff();
-    float best_sig = 0.0f;
-    int32_t best_id = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-      int32_t c = lane + 64 * i;
-      bool ok = c < a.experts && !((taken >> i) & 1u);
-      if (ok && (best_id == 0x7fffffff || vals[i] > best || (vals[i] == best && c < best_id))) {
-        best = vals[i];
-        best_id = c;
-        best_sig = sigs[i];
-      }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-      float ov = __shfl_xor(best, off);
-      float os = __shfl_xor(best_sig, off);
-      int32_t oid = __shfl_xor(best_id, off);
-      if (oid != 0x7fffffff && (best_id == 0x7fffffff || ov > best || (ov == best && oid < best_id))) {
-        best = ov;
-        best_id = oid;
-        best_sig = os;
-      }
-    }
-    if (best_id == 0x7fffffff) best_id = 0;
-    if ((best_id & 63) == lane) taken |= 1u << (best_id >> 6);
-    picked_id[slot] = best_id;
-    picked[slot] = best_sig;
-    total = __fadd_rn(total, best_sig);
-  }
-  if (lane == 0) {
-    for (int slot = 0; slot < a.top_k; ++slot) {
-      float v = picked[slot];
-      if (a.top_k > 1 && a.norm_topk_prob) v = v / total;
-      a.ids_out[t * a.top_k + slot] = picked_id[slot];
-      a.scores_out[t * a.top_k + slot] = __fmul_rn(v, a.routed_scaling_factor);
-    }
-  }
+  wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
+            lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
 }
 
 // BF16 -> FP32 widening of the router input (patch.py:133 x.astype(float32)).
@@ -609,7 +652,8 @@ static hipError_t launch_gate_up_t(const GateUpArgs& a, hipStream_t st) {
 template <int VB, int CH>
 static hipError_t launch_down_t(const DownArgs& a, hipStream_t st) {
   int64_t blocks = (a.hidden + a.rows_per_wg - 1) / a.rows_per_wg;
-  hipLaunchKernelGGL((down_reduce_kernel<VB, CH>), dim3(static_cast<unsigned>(blocks)), dim3(192), 0, st, a);
+  const unsigned threads = 64u * static_cast<unsigned>(a.top_k + (a.shared_down_weight != nullptr ? 1 : 0));
+  hipLaunchKernelGGL((down_reduce_kernel<VB, CH>), dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, st, a);
   return hipGetLastError();
 }
 
@@ -688,7 +732,7 @@ hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_
 }
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(router_kernel, dim3(static_cast<unsigned>(a.experts)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(router_logits_kernel, dim3(static_cast<unsigned>(a.experts)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -8,6 +8,7 @@ namespace glm53 {
 
 constexpr int kMaxTopK = 8;
 constexpr int kMaxExperts = 1024;
+constexpr int kMaxRouterExperts = 512;  // top-k selection bound (8 candidates per lane)
 constexpr int kMaxDownRowsPerWg = 64;
 
 // ---------------------------------------------------------------- decode --
@@ -29,6 +30,17 @@ struct GateUpArgs {
   int64_t wgs_per_slot;
   uint16_t* hidden_out;           // [top_k, I] then [Is]
   int* error_flag;
+  // fused top-k (router_logits non-null): selection replaces expert_ids
+  const float* router_logits;     // [E] FP32
+  const float* router_bias;       // [E]
+  float routed_scaling_factor;
+  int norm_topk_prob;
+  int32_t* ids_out;               // [top_k], written by workgroup 0
+  float* scores_out;              // [top_k]
+  // device code flags (0 = no 0x7F/0xFF code, register decode allowed)
+  const int32_t* routed_flags;
+  const int32_t* shared_flags;    // shared gate
+  const int32_t* shared_flags2;   // shared up
 };
 
 struct DownArgs {
@@ -43,23 +55,18 @@ struct DownArgs {
   const float* shared_down_scale;
   int64_t hidden, intermediate;
   int64_t rows_per_wg;
-  uint16_t* out;                  // [H] bf16
+  const uint16_t* residual;       // [H] bf16 or null: out = T(residual + T(moe))
+  uint16_t* out;                  // [H] bf16 (may alias residual)
   int* error_flag;
+  const int32_t* routed_flags;    // as GateUpArgs
+  const int32_t* shared_flags;
 };
 
 struct RouterArgs {
   const uint16_t* x;       // [H] bf16
   const float* weight;     // [E, H]
-  const float* bias;       // [E]
   int64_t experts, hidden;
-  int top_k;
-  float routed_scaling_factor;
-  int norm_topk_prob;
-  float* sigmoid_out;      // [E] scratch
-  float* choice_out;       // [E] scratch
-  unsigned* arrivals;      // zero-initialised, self-resetting
-  int32_t* ids_out;        // [top_k]
-  float* scores_out;       // [top_k]
+  float* logits_out;       // [E] FP32
 };
 
 struct GenericLinearArgs {
@@ -105,6 +112,7 @@ struct GemvArgs {
   int64_t N, K;
   int rows_per_wave;
   uint16_t* y;            // [N] bf16
+  const int32_t* flags;   // device code flag (null: exact SWAR decode)
 };
 
 struct TopkArgs {

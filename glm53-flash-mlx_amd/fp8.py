@@ -26,8 +26,13 @@ def _scale_shape(out_features: int, in_features: int) -> tuple[int, int]:
     return (math.ceil(out_features / BLOCK_SIZE), math.ceil(in_features / BLOCK_SIZE))
 
 
-def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
-    """Compute ``x @ dequant(weight, scale_inv).T`` without expanding weight."""
+def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor,
+                     code_flags: torch.Tensor | None = None) -> torch.Tensor:
+    """Compute ``x @ dequant(weight, scale_inv).T`` without expanding weight.
+
+    code_flags: optional device int32 from a scan of `weight` for the E4M3
+    codes 0x7F / 0xFF (``_native.scan_codes``); when given and clear, the
+    kernels use the hardware E4M3 decode."""
     N.require_device(x, weight, scale_inv)
     if weight.dtype != torch.uint8 or weight.dim() != 2:
         raise ValueError(f"expected 2-D uint8 E4M3 weight, got {tuple(weight.shape)} {weight.dtype}")
@@ -50,7 +55,7 @@ def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Ten
     ws_bytes = lib.glm53_fp8_linear_workspace_bytes(rows, out_features, in_features)
     ws = N.workspace(ws_bytes, x.device)
     N.check(lib.glm53_fp8_linear(N.ptr(flat), rows, in_features, N.ptr(weight), out_features, N.ptr(scale_inv),
-                                 N.ptr(y), N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
+                                 N.ptr(code_flags), N.ptr(y), N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
     return y.reshape(*x.shape[:-1], out_features)
 
 
@@ -86,12 +91,21 @@ class BlockFP8Linear(torch.nn.Module):
         out_features, in_features = linear.weight.shape
         return cls(in_features, out_features, bias=getattr(linear, "bias", None) is not None)
 
+    def code_flags(self) -> torch.Tensor:
+        """Cached device flag of the weight's 0x7F/0xFF codes (rescanned when
+        the weight tensor is replaced or modified in place)."""
+        stamp = (self.weight.data_ptr(), self.weight._version)
+        cached = getattr(self, "_code_flags", None)
+        if cached is None or cached[0] != stamp:
+            self._code_flags = (stamp, N.scan_codes(self.weight))
+        return self._code_flags[1]
+
     def as_c_struct(self) -> N.Linear:
         return N.Linear(self.weight.data_ptr(), self.weight_scale_inv.data_ptr(), self.out_features, self.in_features,
-                        None)
+                        self.code_flags().data_ptr())
 
     def forward(self, x):
-        y = block_fp8_linear(x, self.weight, self.weight_scale_inv)
+        y = block_fp8_linear(x, self.weight, self.weight_scale_inv, self.code_flags())
         return y + self.bias if self.bias is not None else y
 
 

@@ -27,7 +27,8 @@ class _PackedLinearView:
     themselves contiguous, so no copy is made."""
 
     def __init__(self, weight, scale_inv, *, expert_id: int, row_offset: int, scale_row_offset: int,
-                 out_features: int):
+                 out_features: int, bank=None):
+        self._bank = bank
         self._bank_weight = weight
         self._bank_scale_inv = scale_inv
         self.expert_id = int(expert_id)
@@ -45,7 +46,8 @@ class _PackedLinearView:
         return self._bank_scale_inv[self.expert_id, self.scale_row_offset:self.scale_row_offset + rows]
 
     def __call__(self, x):
-        return block_fp8_linear(x, self.weight, self.weight_scale_inv)
+        flags = self._bank.code_flags() if self._bank is not None else None
+        return block_fp8_linear(x, self.weight, self.weight_scale_inv, flags)
 
 
 class _PackedExpertView:
@@ -53,11 +55,13 @@ class _PackedExpertView:
         inter = bank.intermediate_size
         scale_rows = bank.intermediate_scale_rows
         self.gate_proj = _PackedLinearView(bank.gate_up_weight, bank.gate_up_scale_inv, expert_id=expert_id,
-                                           row_offset=0, scale_row_offset=0, out_features=inter)
+                                           row_offset=0, scale_row_offset=0, out_features=inter, bank=bank)
         self.up_proj = _PackedLinearView(bank.gate_up_weight, bank.gate_up_scale_inv, expert_id=expert_id,
-                                         row_offset=inter, scale_row_offset=scale_rows, out_features=inter)
+                                         row_offset=inter, scale_row_offset=scale_rows, out_features=inter,
+                                         bank=bank)
         self.down_proj = _PackedLinearView(bank.down_weight, bank.down_scale_inv, expert_id=expert_id,
-                                           row_offset=0, scale_row_offset=0, out_features=bank.down_weight.shape[1])
+                                           row_offset=0, scale_row_offset=0, out_features=bank.down_weight.shape[1],
+                                           bank=bank)
         self.limit = float(limit)
 
     def __call__(self, x):
@@ -201,6 +205,19 @@ class DecodePlan:
         N.check(self._lib.glm53_decode_moe(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
                                            ctypes.byref(r), N.ptr(x), N.ptr(out), N.ptr(ids_out), N.ptr(scores_out),
                                            N.stream_handle(device)))
+
+    def step(self, bank, shared, router, x, residual, out, stages, device):
+        """Decoder-step form: out = T(residual + T(moe(x))) (residual may be
+        None); stages is a mask of the router / gate-up / down launches."""
+        b = bank.as_c_struct()
+        s = shared.as_c_struct() if shared is not None else None
+        r = router.as_c_struct() if router is not None else None
+        N.check(self._lib.glm53_decode_moe_ex(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                              ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual), N.ptr(out),
+                                              int(stages), N.stream_handle(device)))
+
+    def tune(self, gate_up_rows_per_wave: int = 8, down_rows_per_wg: int = 16) -> None:
+        N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))
 
     def error_flag(self) -> int:
         value = ctypes.c_int32()

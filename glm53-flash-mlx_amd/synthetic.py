@@ -74,10 +74,17 @@ def synth_bank(experts: int, hidden: int, intermediate: int, seed: int, layer: i
     gus = torch.empty((experts, 2 * sr, sh), dtype=torch.float32, device=device)
     dw = torch.empty((experts, hidden, intermediate), dtype=torch.uint8, device=device)
     dws = torch.empty((experts, sh, sr), dtype=torch.float32, device=device)
-    for e in range(experts):
-        fill_fp8(gu[e, :intermediate], gus[e, :sr], key(seed, layer, e, "gate"), std)
-        fill_fp8(gu[e, intermediate:], gus[e, sr:], key(seed, layer, e, "up"), std)
-        fill_fp8(dw[e], dws[e], key(seed, layer, e, "down"), std)
+    lib = N.lib()
+    stream = N.stream_handle(gu.device)
+    # one launch per projection over all experts; expert e of a projection
+    # draws from the key derived from (projection key, e)
+    N.check(lib.glm53_synth_fp8_batched(N.ptr(gu), N.ptr(gus), intermediate, hidden, experts,
+                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "gate"), std, stream))
+    N.check(lib.glm53_synth_fp8_batched(N.ctypes.c_void_p(gu.data_ptr() + intermediate * hidden),
+                                        N.ctypes.c_void_p(gus.data_ptr() + 4 * sr * sh), intermediate, hidden, experts,
+                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "up"), std, stream))
+    N.check(lib.glm53_synth_fp8_batched(N.ptr(dw), N.ptr(dws), hidden, intermediate, experts, hidden * intermediate,
+                                        sh * sr, key(seed, layer, "down"), std, stream))
     return PackedFP8ExpertBank(gu, gus, dw, dws, intermediate_size=intermediate)
 
 

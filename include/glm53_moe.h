@@ -109,12 +109,15 @@ int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* 
  * s[n/128, k/128]).  x bf16 [M, K], y bf16 [M, N].  M == 1 runs the
  * streaming GEMV; M > 1 with K % 128 == 0 runs the FP8 MFMA GEMM and needs
  * `workspace` of glm53_fp8_linear_workspace_bytes(M, N, K) bytes (may be
- * NULL when that is 0).
+ * NULL when that is 0).  code_flags (device int32 from glm53_e4m3_scan_codes,
+ * may be NULL) lets both paths use the hardware E4M3 decode when the weight
+ * holds no 0x7F / 0xFF code; NULL keeps the exact software decode (M == 1)
+ * or scans the weight first (M > 1).
  * ---------------------------------------------------------------------- */
 size_t glm53_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N,
-                     const float* scale_inv, void* y, void* workspace, size_t workspace_bytes,
-                     void* stream);
+                     const float* scale_inv, const int32_t* code_flags, void* y, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Router -- replaces patch.py:131-142 `Float32Gate.__call__` (with the
@@ -152,11 +155,35 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank,
                      const glm53_shared_expert* shared, const glm53_router* router,
                      const void* x, void* out, int32_t* ids_out, float* scores_out, void* stream);
 
+/* Decoder-step form with optional residual and stage control:
+ * out = T(residual + T(moe(x))) when residual is not NULL (out may alias
+ * residual / x), else out = moe(x).  stages selects launches:
+ * GLM53_STAGE_ROUTER (router + top-k into the plan), GLM53_STAGE_GATE_UP
+ * (routed + shared gate/up/SwiGLU), GLM53_STAGE_DOWN (down, ordered
+ * reduction, shared add, residual).  Partial masks let a caller time each
+ * launch; they need the fused path (16-byte aligned pointers, supported
+ * widths).  A captured HIP graph of this call replays correctly: it records
+ * no memset and resets its own counters. */
+#define GLM53_STAGE_ROUTER 1
+#define GLM53_STAGE_GATE_UP 2
+#define GLM53_STAGE_DOWN 4
+#define GLM53_STAGE_ALL 7
+int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank,
+                        const glm53_shared_expert* shared, const glm53_router* router,
+                        const void* x, const void* residual, void* out, int32_t stages,
+                        void* stream);
+
 /* bind_weights / execute_bound (native_packed_moe_plan.cpp:231-280): bind
  * once, then run with only the activation.  Binding twice is GLM53_BAD_STATE. */
 int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank,
                            const glm53_shared_expert* shared, const glm53_router* router);
 int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, void* stream);
+
+/* Launch shape of the fused decode kernels: rows of one slot streamed per
+ * wavefront in the gate/up kernel (default 8) and output rows per workgroup
+ * in the down kernel (default 16, at most 64).  Results do not depend on it. */
+int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wave,
+                           int32_t down_rows_per_wg);
 
 /* Device scratch of the last call (read-only diagnostics): which = 0 hidden
  * bf16 [top_k + 1, I] (routed rows, then shared), 1 expert ids int32
@@ -262,6 +289,21 @@ int glm53_synth_fp8(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols
 int glm53_synth_f32(float* out, int64_t n, uint64_t seed, float std, float lo, float hi,
                     int32_t uniform, void* stream);
 int glm53_synth_bf16(void* out, int64_t n, uint64_t seed, float std, void* stream);
+/* batch matrices at codes + b * codes_stride / scale_inv + b * scale_stride;
+ * matrix b draws from a key derived from (seed, b), matrix 0 from seed. */
+int glm53_synth_fp8_batched(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, int64_t batch,
+                            int64_t codes_stride, int64_t scale_stride, uint64_t seed, float std,
+                            void* stream);
+/* out bf16 [n] = N(0, std) under key (seed, *counter), then ++*counter
+ * (device uint32): a fresh decode input per replay of a captured graph. */
+int glm53_synth_step_input(void* out, int64_t n, uint64_t seed, float std, uint32_t* counter,
+                           void* stream);
+
+/* Streaming-read probe (measurement only): reads every byte of buf once with
+ * 16-byte non-temporal loads from `blocks` workgroups of 256 lanes and writes
+ * 4 words per workgroup to sink ([4 * blocks] uint32).  Its rate is the
+ * achievable-HBM reference of the benchmark's roofline fractions. */
+int glm53_probe_read(const void* buf, int64_t bytes, uint32_t* sink, int32_t blocks, void* stream);
 
 #ifdef __cplusplus
 }
