@@ -1,0 +1,128 @@
+"""CPU checks of the C-ABI boundary (no device work): the shared library
+loads, exports every entry point include/glm53_moe.h declares, the Python
+binding types every one of them, struct layouts agree between the header
+and ctypes, and the product refuses to run without a GPU instead of falling
+back to a CPU path."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from conftest import ROOT, submodule
+
+HEADER = ROOT / "include" / "glm53_moe.h"
+PACKAGE_DIR = ROOT / "glm53-flash-mlx_amd"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(glm53_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def header_define(name: str) -> int:
+    m = re.search(rf"#define\s+{name}\s+(\d+)", HEADER.read_text())
+    assert m, name
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def N():
+    return submodule("_native")
+
+
+@pytest.fixture(scope="module")
+def libso(N):
+    if not N.LIB_PATH.exists():
+        pytest.fail(f"{N.LIB_PATH} not built: run __graft_entry__.build() first")
+    return N.load_library()
+
+
+def test_header_declares_the_path_entry_points():
+    names = declared_functions()
+    for required in ("glm53_fp8_linear", "glm53_router_topk", "glm53_decode_moe", "glm53_decode_moe_ex",
+                     "glm53_route_plan", "glm53_grouped_linear", "glm53_activate_gate_up",
+                     "glm53_restore_and_reduce", "glm53_direct_order_reduce", "glm53_prefill_moe"):
+        assert required in names
+    assert len(names) >= 30
+
+
+def test_library_exports_every_declared_symbol(libso):
+    for name in declared_functions():
+        assert hasattr(libso, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(submodule("_native").LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\b(glm53_\w+)$", out, flags=re.M))
+    assert set(declared_functions()) <= exported
+    # nothing glm53_* leaks out of the library that the header does not declare
+    assert exported - set(declared_functions()) == set()
+
+
+def test_binding_types_every_declared_symbol(N):
+    assert set(N.EXPORTED_SYMBOLS) == set(declared_functions())
+
+
+def test_abi_version_and_constants(N, libso):
+    assert libso.glm53_abi_version() == header_define("GLM53_ABI_VERSION")
+    assert libso.glm53_last_error() == b""
+    assert (N.OK, N.INVALID_ARGUMENT, N.BAD_STATE, N.DEVICE_ERROR) == tuple(
+        header_define(n) for n in ("GLM53_OK", "GLM53_INVALID_ARGUMENT", "GLM53_BAD_STATE", "GLM53_DEVICE_ERROR"))
+    assert (N.REDUCE_GROUPED, N.REDUCE_DIRECT) == (header_define("GLM53_REDUCE_GROUPED"),
+                                                   header_define("GLM53_REDUCE_DIRECT"))
+    assert (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN, N.STAGE_ALL) == tuple(
+        header_define(n) for n in ("GLM53_STAGE_ROUTER", "GLM53_STAGE_GATE_UP", "GLM53_STAGE_DOWN",
+                                   "GLM53_STAGE_ALL"))
+
+
+def test_struct_layouts_match_header(N, tmp_path):
+    """sizeof / offsetof of every public struct, compiled from the header with
+    the host C compiler, equal the ctypes mirrors."""
+    structs = {"glm53_bank": N.Bank, "glm53_linear": N.Linear, "glm53_shared_expert": N.SharedExpert,
+               "glm53_router": N.Router}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        cname, field, value = line.split()
+        got[(cname, field)] = int(value)
+    for cname, py in structs.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
+
+
+def test_product_refuses_cpu_tensors():
+    """No CPU fallback: a product op on host tensors raises."""
+    torch = pytest.importorskip("torch")
+    fp8 = submodule("fp8")
+    x = torch.zeros((1, 256), dtype=torch.bfloat16)
+    w = torch.zeros((128, 256), dtype=torch.uint8)
+    s = torch.ones((1, 2), dtype=torch.float32)
+    with pytest.raises((RuntimeError, ValueError)):
+        fp8.block_fp8_linear(x, w, s)
+
+
+def test_missing_library_fails_loudly(N, tmp_path):
+    with pytest.raises(RuntimeError, match="missing"):
+        N.load_library(tmp_path / "absent.so")
+
+
+def test_product_does_not_import_the_oracle():
+    for path in PACKAGE_DIR.rglob("*"):
+        if path.suffix in (".py", ".cpp", ".hip", ".h"):
+            text = path.read_text()
+            assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), path
+            assert "glm53o_" not in text, path
