@@ -8,10 +8,13 @@
 //    the sorted token index.
 //  * Activation split (this build's MFMA operand format): every (row,
 //    128-column block) gets a power-of-two scale s with amax/s <= 448, and
-//    x/s is written as hi + lo/16 with hi, lo both E4M3.  For BF16 inputs the
-//    split is exact (hi keeps 4 significant bits, the residual has at most 4
-//    more), so the FP8 MFMA below multiplies exactly the products the
-//    reference multiplies in FP32.
+//    x/s is written as hi + lo/16 with hi, lo both E4M3.  A BF16 value has 8
+//    significant bits: hi keeps 4 and lo the remaining 4, so the split is
+//    exact whenever lo stays in E4M3's normal range, i.e. for every element
+//    with |x/s| >= 2^-6 (|x| >= amax / 28672).  Smaller elements are rounded
+//    on E4M3's subnormal grid, an absolute error of at most 2^-14 * s
+//    (< 2.8e-7 * amax of the row block); the MFMA then multiplies these
+//    operands by the raw weight codes with no further rounding of products.
 //  * Grouped GEMM (grouped_fp8.py:30-140): gfx950 v_mfma_f32_16x16x128 with
 //    E4M3 weights fed raw from HBM as the B operand (no decode, no LDS) and
 //    the hi/lo activation rows as the A operand.  One MFMA covers exactly
