@@ -46,11 +46,14 @@ def parse():
     p.add_argument("--layers", type=int, default=42)
     p.add_argument("--kernel-steps", type=int, default=8, help="stage-graph replays (x8) for per-launch timing")
     p.add_argument("--prefill-iters", type=int, default=10)
-    p.add_argument("--cpu-samples", type=int, default=7, help="CPU oracle layer evaluations (2 warmup + rest timed)")
+    p.add_argument("--cpu-steps", type=int, default=24, help="tokens through all layers for the CPU oracle timing")
     p.add_argument("--parity-layers", type=int, default=3)
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--json-out", type=str, default="")
+    p.add_argument("--traffic-run", action="store_true", help="short eager program for rocprofv3 --pmc passes")
+    p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                   help="print the counter summary of two --pmc runs of --traffic-run")
     return p.parse_args()
 
 
@@ -77,10 +80,16 @@ def gate_up_launch_bytes(H, I, Is, k):
 
 def main():
     args = parse()
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported on this single-GPU build "
               "(the multi-GPU sharding is described, not run)", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_run:
+        traffic_run(args)
+        return
     import numpy as np
     import torch
 
@@ -206,7 +215,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": load_traffic("gate_up_swiglu_kernel"),
+            "traffic_source": "profiles/decode_traffic_pmc.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)",
             "bytes_per_launch": gu_bytes,
             "avg_launch_us": round(gate_up_us, 3),
         },
@@ -366,33 +376,136 @@ def bench_prefill(args, layer, cfg, dev, torch, np, pkg, syn):
 
 
 def cpu_baseline(args, layers, cfg, dev, torch, np):
-    """CPU oracle (C + OpenMP restatement of Direct decode) on the host cores,
-    timed on touched experts already copied to host memory."""
+    """CPU oracle (C + OpenMP restatement of Direct decode) on the host cores:
+    `cpu_steps` tokens through all layers (x += moe(x), as on the GPU), each
+    layer timed from router to output on its touched experts, which are
+    copied to host memory before the timer starts (the 229 GB of banks do
+    not fit host RAM)."""
     from oracle import oracle as O
 
     syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
+    host_router = [(l.gate.weight.cpu().numpy(), l.gate.e_score_correction_bias.cpu().numpy()) for l in layers]
     samples = []
     warm = 2
-    for i in range(args.cpu_samples):
-        l = layers[i % len(layers)]
-        x = syn.normal_bf16((cfg.hidden_size,), syn.key(SEED, "cpu", i), device=dev)
+    for step in range(args.cpu_steps):
+        x = syn.normal_bf16((cfg.hidden_size,), syn.key(SEED, "cpu", step), device=dev)
         xb = bits(x, torch, np)
-        w = l.gate.weight.cpu().numpy()
-        b = l.gate.e_score_correction_bias.cpu().numpy()
-        ids, _ = O.router(xb[None], w, b)
-        hb, hs = host_layer_subset(l, ids[0], torch, np)
-        t0 = time.perf_counter()
-        ids2, sc2 = O.router(xb[None], w, b)
-        O.decode_moe(xb, hb, np.arange(8), sc2[0], cfg.swiglu_limit, hs)
-        dt = time.perf_counter() - t0
-        if i >= warm:
-            samples.append(dt)
-    us = statistics.median(samples) * 1e6
+        for li, l in enumerate(layers):
+            w, b = host_router[li]
+            ids, _ = O.router(xb[None], w, b)
+            hb, hs = host_layer_subset(l, ids[0], torch, np)
+            t0 = time.perf_counter()
+            ids2, sc2 = O.router(xb[None], w, b)
+            y = O.decode_moe(xb, hb, np.arange(8), sc2[0], cfg.swiglu_limit, hs)
+            samples.append(time.perf_counter() - t0)
+            xb = O.add_bf16(xb, y)
+    timed = samples[warm:]
+    us = statistics.median(timed) * 1e6
     cores = O.num_threads()
     return {"value": round(us, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"median of {len(samples)} single-layer decodes (config-2 layer: router + 8 routed + shared) "
-                      f"after {warm} warmups; touched experts pre-copied to host; OpenMP threads={cores}; "
-                      f"CPU {cpu_model()}"}
+            "sample": f"{args.cpu_steps} tokens x {len(layers)} config-2 layers of batch-1 decode with residual "
+                      f"(router + 8 routed + shared per layer), {len(timed)} layer evaluations timed "
+                      f"({sum(timed):.1f} s of CPU work), median per layer; touched experts copied to host "
+                      f"before each timer; OpenMP threads={cores}; CPU {cpu_model()}"}
+
+
+def traffic_run(args):
+    """Short eager program for `rocprofv3 --pmc` passes: each decode launch on
+    4 layers (4 times), the read probe over 113,309,696 B and a 64 MiB torch
+    device copy, whose counter readings calibrate FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
+    N = importlib.import_module("glm53-flash-mlx_amd._native")
+    packed = importlib.import_module("glm53-flash-mlx_amd.packed")
+    dev = torch.device("cuda:0")
+    cfg = syn.layer_config()
+    H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    layers = []
+    for layer in range(4):
+        bank, shared, gate = syn.synth_layer(cfg, SEED, layer, dev)
+        bank.code_flags()
+        layers.append(SimpleNamespace(bank=bank, shared=shared, gate=gate,
+                                      plan=packed.DecodePlan(H, I, I, E, k, cfg.swiglu_limit)))
+    x = syn.normal_bf16((H,), syn.key(SEED, "traffic"), device=dev)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        for l in layers:
+            for mask in (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN):
+                l.plan.step(l.bank, l.shared, l.gate, x, None, x, mask, dev)
+    lib = N.lib()
+    sink = torch.empty(4 * 4096, dtype=torch.int32, device=dev)
+    probe_bytes = 113309696 // 256 * 256
+    for r in range(4):
+        N.check(lib.glm53_probe_read(N.ctypes.c_void_p(layers[r].bank.gate_up_weight.data_ptr()), probe_bytes,
+                                     N.ptr(sink), 4096, N.stream_handle(dev)))
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"traffic run done: probe {probe_bytes} B, copy {64 << 20} B")
+
+
+def summarize_traffic(fetch_csv, write_csv):
+    """Per-kernel mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from two
+    rocprofv3 counter-collection CSVs, calibrated against the read probe
+    (fetch) and the 64 MiB device copy (write); prints a markdown summary
+    whose last line is the JSON that bench.py reads back."""
+    import csv
+
+    def load(path, counter):
+        rows = {}
+        for row in csv.DictReader(open(path)):
+            if row.get("Counter_Name") != counter:
+                continue
+            name = row["Kernel_Name"]
+            rows.setdefault(name, []).append(float(row["Counter_Value"]))
+        return {n: (statistics.mean(v), len(v)) for n, v in rows.items()}
+
+    fetch, write = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+
+    def pick(table, key):
+        hits = [n for n in table if key in n]
+        return hits[0] if hits else None
+
+    probe_bytes = 113309696 // 256 * 256
+    copy_bytes = 64 << 20
+    probe_k = pick(fetch, "probe_read_kernel")
+    copy_kw = pick(write, "copyBuffer") or pick(write, "elementwise_kernel")
+    fetch_scale = probe_bytes / (fetch[probe_k][0] * 1024.0)
+    write_scale = copy_bytes / (write[copy_kw][0] * 1024.0)
+    keys = ("gate_up_swiglu_kernel", "down_reduce_kernel", "router_logits_kernel", "probe_read_kernel")
+    print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (calibrated) | written B (calibrated) |")
+    print("|---|---|---|---|---|---|")
+    out = {}
+    for name in sorted(set(fetch) | set(write)):
+        f = fetch.get(name, (float("nan"), 0))
+        w = write.get(name, (float("nan"), 0))
+        fb, wb = f[0] * 1024.0 * fetch_scale, w[0] * 1024.0 * write_scale
+        print(f"| {name[:90]} | {f[1]} | {f[0]:.1f} | {w[0]:.1f} | {fb:.0f} | {wb:.0f} |")
+        for key in keys:
+            if key in name:
+                out[key] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb)}
+    print()
+    print(f"calibration: read probe {probe_bytes} B -> FETCH_SIZE x {fetch_scale:.4f}; "
+          f"{copy_bytes} B device copy ({copy_kw[:60]}) -> WRITE_SIZE x {write_scale:.4f}")
+    print()
+    print("traffic_json: " + json.dumps({"fetch_scale": fetch_scale, "write_scale": write_scale, "kernels": out}))
+
+
+def load_traffic(kernel_key):
+    """HBM bytes per launch for `kernel_key` from the committed counter
+    summary, or None when no summary is present."""
+    path = ROOT / "profiles" / "decode_traffic_pmc.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_json: "):
+                entry = json.loads(line[len("traffic_json: "):])["kernels"].get(kernel_key)
+                return None if entry is None else entry["traffic_bytes"]
+    except (OSError, ValueError, KeyError):
+        return None
+    return None
 
 
 def cpu_model():
