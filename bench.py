@@ -7,11 +7,12 @@ experts, top-8, one shared expert, FP32 router; 229 GB of E4M3 banks
 resident in HBM), one BF16 token per step with a residual add, a fresh
 seeded input every step.  One step (42 x 3 launches + the input draw) is
 captured once as a HIP graph and replayed; `value` = microseconds per MoE
-layer = step time / 42.
+layer = step time / 42.  The dominant kernel (fused routed + shared
+gate/up/SwiGLU with the top-k prologue) is the `roofline` entry, timed with
+HIP events on its stream against the HBM roofline.  The one-launch form
+(decode_layer_kernel) is timed beside it for comparison.
 
-Also reported: the dominant kernel (fused routed+shared gate/up/SwiGLU)
-timed with HIP events on its stream against the HBM roofline, the grouped
-prefill configs 4 (256 tokens, near-uniform) and 5 (2,048 tokens, Zipf
+Also reported: the grouped prefill configs 4 (256 tokens, near-uniform) and 5 (2,048 tokens, Zipf
 router bias) as routes/s with HBM and FP8-MFMA roofline fractions, a parity
 sample against the CPU oracle, and the CPU oracle's own decode time on the
 host cores (the reference has no CPU FP8 path; MLX is not installable).
@@ -50,6 +51,7 @@ def parse():
     p.add_argument("--parity-layers", type=int, default=3)
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-single", action="store_true", help="skip timing the one-launch decode form")
     p.add_argument("--json-out", type=str, default="")
     p.add_argument("--traffic-run", action="store_true", help="short eager program for rocprofv3 --pmc passes")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -123,30 +125,37 @@ def main():
     counter = torch.zeros(1, dtype=torch.int32, device=dev)
     lib = N.lib()
 
+    def set_mode(mode):
+        for l in layers:
+            l.plan.set_mode(mode)
+
     def step():
         N.check(lib.glm53_synth_step_input(N.ptr(x), H, SEED, 1.0, N.ptr(counter), N.stream_handle(dev)))
         for l in layers:
             l.plan.step(l.bank, l.shared, l.gate, x, x, x, N.STAGE_ALL, dev)
 
-    for _ in range(2):
-        step()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_step = start.elapsed_time(end) / args.steps
+    def time_steps():
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        start.record()
+        for _ in range(args.steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps, time.perf_counter() - wall0
+
+    set_mode(N.DECODE_THREE_LAUNCH)
+    ms_step, wall = time_steps()
     us_layer = ms_step * 1000.0 / L
     finite = bool(torch.isfinite(x.float()).all().item())
     log(f"decode: {ms_step:.3f} ms/step, {us_layer:.2f} us/layer (wall {wall:.2f} s, finite={finite})")
@@ -155,17 +164,20 @@ def main():
     layer_gbs = bytes_layer["total"] / (us_layer * 1e-6) / 1e9
 
     # ------------------------------------------- per-launch HIP-event timing --
-    # Per-launch durations: one graph per stage holds that stage's launch for
-    # all L layers back to back (each layer's own weights, so no launch is
-    # served from L2 / MALL), replayed between two HIP events on the launch
-    # stream.  Event pairs around single eager launches would time host
-    # enqueue latency and the events' own cache flushes instead.
-    stage_us = {}
-    for name, mask in (("router", N.STAGE_ROUTER), ("gate_up", N.STAGE_GATE_UP), ("down", N.STAGE_DOWN)):
-        def run(mask=mask):
+    # Per-launch durations: a graph holds one launch kind for all L layers back
+    # to back (each layer's own weights, so no launch is served from L2 /
+    # MALL), replayed between two HIP events on the launch stream.  Event
+    # pairs around single eager launches would time host enqueue latency and
+    # the events' own cache flushes instead.
+    def run_stage(mask):
+        def run():
             for l in layers:
                 l.plan.step(l.bank, l.shared, l.gate, x, x, x, mask, dev)
-        stage_us[name] = time_graph(run, args.kernel_steps * 8, torch) / L
+        return run
+
+    stage_us = {}
+    for name, mask in (("router", N.STAGE_ROUTER), ("gate_up", N.STAGE_GATE_UP), ("down", N.STAGE_DOWN)):
+        stage_us[name] = time_graph(run_stage(mask), args.kernel_steps * 8, torch) / L
     router_us, gate_up_us, down_us = stage_us["router"], stage_us["gate_up"], stage_us["down"]
     probe = read_probe(lib, N, layers[-1].bank, dev, torch)
     gu_bytes = gate_up_launch_bytes(H, I, Is, k)
@@ -174,6 +186,16 @@ def main():
                   + (k + 1) * I * 2 + 2 * H * 2)
     log(f"launches: router {router_us:.2f} us, gate/up {gate_up_us:.2f} us ({gu_gbs:.0f} GB/s), "
         f"down {down_us:.2f} us ({down_bytes / (down_us * 1e-6) / 1e9:.0f} GB/s)")
+
+    # The one-launch form (decode_layer_kernel), for comparison.
+    single = None
+    if not args.no_single:
+        set_mode(N.DECODE_SINGLE_LAUNCH)
+        ms_single, _ = time_steps()
+        layer_us = time_graph(run_stage(N.STAGE_ALL), args.kernel_steps * 2, torch) / L
+        set_mode(N.DECODE_THREE_LAUNCH)
+        single = {"us_per_layer": round(ms_single * 1000.0 / L, 3), "launch_us": round(layer_us, 3)}
+        log(f"one-launch form: {ms_single * 1000.0 / L:.2f} us/layer")
 
     # -------------------------------------------------------------- parity ---
     parity = parity_sample(args, layers, cfg, dev, torch, np)
@@ -210,7 +232,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate_up_swiglu_kernel<16,4> (8 routed + shared gate/up rows, fused SwiGLU)",
+            "kernel": "gate_up_swiglu_kernel<16,4> (8 routed + shared gate/up rows, fused top-k and SwiGLU)",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
@@ -228,8 +250,11 @@ def main():
             "layer_hbm_frac": round(layer_gbs / PEAK_HBM_GBS, 4),
             "launch_us": {"router": round(router_us, 3), "gate_up": round(gate_up_us, 3),
                           "down_reduce": round(down_us, 3)},
-            "launch_GBps": {"gate_up": round(gu_gbs, 1), "down_reduce": round(down_bytes / (down_us * 1e-6) / 1e9, 1)},
+            "launch_GBps": {"gate_up": round(gu_gbs, 1),
+                            "down_reduce": round(down_bytes / (down_us * 1e-6) / 1e9, 1)},
+            "launch_note": "router stage-only graphs are dispatch-gap bound; its kernel time is in profiles/",
             "achievable_read_GBps": probe,
+            "one_launch_form": single,
             "weights_generated_s": round(gen_s, 1),
             "final_state_finite": finite,
         },
@@ -431,6 +456,11 @@ def traffic_run(args):
     torch.cuda.synchronize()
     for _ in range(4):
         for l in layers:
+            l.plan.set_mode(N.DECODE_SINGLE_LAUNCH)
+            l.plan.step(l.bank, l.shared, l.gate, x, None, x, N.STAGE_ALL, dev)
+    for _ in range(4):
+        for l in layers:
+            l.plan.set_mode(N.DECODE_THREE_LAUNCH)
             for mask in (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN):
                 l.plan.step(l.bank, l.shared, l.gate, x, None, x, mask, dev)
     lib = N.lib()
@@ -475,7 +505,8 @@ def summarize_traffic(fetch_csv, write_csv):
     copy_kw = pick(write, "copyBuffer") or pick(write, "elementwise_kernel")
     fetch_scale = probe_bytes / (fetch[probe_k][0] * 1024.0)
     write_scale = copy_bytes / (write[copy_kw][0] * 1024.0)
-    keys = ("gate_up_swiglu_kernel", "down_reduce_kernel", "router_logits_kernel", "probe_read_kernel")
+    keys = ("decode_layer_kernel", "gate_up_swiglu_kernel", "down_reduce_kernel", "router_logits_kernel",
+            "probe_read_kernel")
     print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (calibrated) | written B (calibrated) |")
     print("|---|---|---|---|---|---|")
     out = {}

@@ -22,6 +22,7 @@ LIB_PATH = Path(os.environ.get("GLM53_MOE_LIB", _PKG / "libglm53_moe.so"))
 OK, INVALID_ARGUMENT, BAD_STATE, DEVICE_ERROR = 0, 1, 2, 3
 REDUCE_GROUPED, REDUCE_DIRECT = 0, 1
 STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 4, 7
+DECODE_THREE_LAUNCH, DECODE_SINGLE_LAUNCH = 0, 1
 
 _lib = None
 
@@ -81,6 +82,7 @@ _SIGNATURES = {
     "glm53_decode_plan_bind": (ctypes.c_int, [P, P, P, P]),
     "glm53_decode_moe_bound": (ctypes.c_int, [P, P, P, P]),
     "glm53_decode_plan_tune": (ctypes.c_int, [P, I32, I32]),
+    "glm53_decode_plan_set_mode": (ctypes.c_int, [P, I32]),
     "glm53_decode_plan_scratch": (ctypes.c_int, [P, I32, P, P]),
     "glm53_decode_plan_error_flag": (ctypes.c_int, [P, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),

@@ -13,6 +13,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "grouped.h"
 #include "kernels.h"
@@ -112,6 +113,45 @@ int check_router(const glm53_router* r, int64_t H, int64_t E, int64_t k) {
             (long long)r->hidden, (long long)E, (long long)H);
   CHECK_ARG(r->top_k == k, "router top_k %lld != plan top_k %lld", (long long)r->top_k, (long long)k);
   return GLM53_OK;
+}
+
+// Exchange words and counters of the one-launch decode kernel live in
+// uncached device memory: its workgroups on different XCDs (each with its
+// own L2) read each other's words while the kernel runs, and consecutive
+// launches hand the ticket, exit count and epoch on to each other; uncached
+// memory keeps every such access at the memory itself.  Uncached blocks are never freed (a freed
+// uncached block has been seen to corrupt later allocations), so a destroyed
+// plan returns its block to this per-process pool for the next plan.
+struct UncachedBlock {
+  int device;
+  size_t bytes;
+  void* ptr;
+};
+std::mutex g_uncached_mutex;
+std::vector<UncachedBlock> g_uncached_free;
+
+hipError_t uncached_take(size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  {
+    std::lock_guard<std::mutex> lock(g_uncached_mutex);
+    for (size_t i = 0; i < g_uncached_free.size(); ++i) {
+      if (g_uncached_free[i].device == dev && g_uncached_free[i].bytes >= bytes) {
+        *out = g_uncached_free[i].ptr;
+        g_uncached_free.erase(g_uncached_free.begin() + static_cast<std::ptrdiff_t>(i));
+        return hipSuccess;
+      }
+    }
+  }
+  return hipExtMallocWithFlags(out, bytes, hipDeviceMallocUncached);
+}
+
+void uncached_give(void* ptr, size_t bytes) {
+  int dev = 0;
+  if (ptr == nullptr || hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_uncached_mutex);
+  g_uncached_free.push_back({dev, bytes, ptr});
 }
 
 std::mutex g_blas_mutex;
@@ -307,6 +347,15 @@ struct glm53_decode_plan {
   bool bound = false;
   int gate_up_rows_per_wave = 8;   // launch shape (glm53_decode_plan_tune), swept on MI355X
   int down_rows_per_wg = 16;
+  // one-launch layer kernel (layer.hip): epoch-tagged exchange words
+  int mode = GLM53_DECODE_THREE_LAUNCH;
+  uint64_t* logit_words = nullptr;   // [E]
+  uint64_t* hidden_words = nullptr;  // [(k + 1) * max(I, Is) / 2]
+  uint64_t* shared_words = nullptr;  // [H / 2]
+  uint32_t* control = nullptr;       // [4]: ticket, exits, epoch, last stale tag seen
+  int layer_grid = 0;                // persistent grid (CUs x resident workgroups), found on first use
+  void* exchange = nullptr;          // uncached block holding the three word arrays
+  size_t exchange_bytes = 0;
   glm53_bank bank{};
   glm53_shared_expert shared{};
   bool has_shared = false;
@@ -367,6 +416,39 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   p->shared_up = reinterpret_cast<uint16_t*>(b + o_su);
   p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
   p->moe_out = reinterpret_cast<uint16_t*>(b + o_mo);
+  {
+    size_t xo = 0;
+    auto xtake = [&](size_t bytes) {
+      size_t o = xo;
+      xo += round_up(bytes);
+      return o;
+    };
+    const size_t o_lw = xtake(8 * experts), o_hw = xtake(8 * ((top_k + 1) * Imax / 2 + 1));
+    const size_t o_sw = xtake(8 * (hidden / 2 + 1)), o_ctl = xtake(64);
+    p->exchange_bytes = xo;
+    e = uncached_take(xo, &p->exchange);
+    if (e == hipSuccess) e = hipMemset(p->exchange, 0, xo);  // tag 0: no launch's epoch
+    if (e != hipSuccess) {
+      if (p->exchange) uncached_give(p->exchange, xo);
+      (void)hipFree(p->arena);
+      delete p;
+      return hip_fail(e, "decode plan exchange words");
+    }
+    uint8_t* xb = static_cast<uint8_t*>(p->exchange);
+    p->logit_words = reinterpret_cast<uint64_t*>(xb + o_lw);
+    p->hidden_words = reinterpret_cast<uint64_t*>(xb + o_hw);
+    p->shared_words = reinterpret_cast<uint64_t*>(xb + o_sw);
+    p->control = reinterpret_cast<uint32_t*>(xb + o_ctl);
+  }
+  // epoch 1 for the first launch: the zeroed exchange words carry epoch 0
+  const uint32_t control0[16] = {0u, 0u, 1u, 0u};
+  e = hipMemcpy(p->control, control0, sizeof(control0), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    uncached_give(p->exchange, p->exchange_bytes);
+    (void)hipFree(p->arena);
+    delete p;
+    return hip_fail(e, "decode plan control init");
+  }
   *out = p;
   return GLM53_OK;
 }
@@ -374,6 +456,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
 void glm53_decode_plan_destroy(glm53_decode_plan* plan) {
   if (plan == nullptr) return;
   if (plan->arena) (void)hipFree(plan->arena);
+  uncached_give(plan->exchange, plan->exchange_bytes);
   delete plan;
 }
 
@@ -579,6 +662,87 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
   return GLM53_OK;
 }
 
+// One launch for the whole layer when the plan allows it and the shape has
+// an instantiated kernel; returns -1 (nothing launched) otherwise.  With a
+// router the selection is computed in the launch (ids / scores land in the
+// plan); otherwise `ids` / `scores` are used.  out may alias x or residual:
+// an output row is written only after every reader of x has finished (each
+// output row waits for all SwiGLU rows, which are produced after their
+// readers' loads of x).
+int run_layer(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+              const glm53_router* router, const void* x, const int32_t* ids, const float* scores,
+              const void* residual, void* out, hipStream_t st) {
+  if (p->mode != GLM53_DECODE_SINGLE_LAUNCH) return -1;
+  if (!decode_fast_ok(p, bank, shared, x) || !layer_shape_supported(p->H, p->I)) return -1;
+  if (router != nullptr && (router->experts > 320 || !aligned(router->weight, 16))) return -1;
+  if (p->layer_grid == 0) {
+    int dev = 0, cus = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+    const int occ = layer_occupancy(p->H, p->I);
+    if (occ <= 0 || cus <= 0) return -1;
+    p->layer_grid = cus * occ;
+  }
+  const int64_t H = p->H, I = p->I;
+  const int k = static_cast<int>(p->k);
+  const int rpw = std::max(2, p->gate_up_rows_per_wave & ~1);
+  const int sdr = 16;
+  LayerArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.out = static_cast<uint16_t*>(out);
+  a.hidden = H;
+  a.intermediate = I;
+  a.experts = p->E;
+  a.top_k = k;
+  a.limit = p->limit;
+  if (router != nullptr) {
+    a.router_weight = router->weight;
+    a.router_bias = router->bias;
+    a.routed_scaling_factor = router->routed_scaling_factor;
+    a.norm_topk_prob = router->norm_topk_prob;
+  } else {
+    a.given_ids = ids;
+    a.given_scores = scores;
+  }
+  a.gate_up_weight = bank->gate_up_weight;
+  a.gate_up_scale = bank->gate_up_scale_inv;
+  a.down_weight = bank->down_weight;
+  a.down_scale = bank->down_scale_inv;
+  a.routed_flags = bank->code_flags;
+  if (shared != nullptr) {
+    a.shared_gate_weight = shared->gate.weight;
+    a.shared_gate_scale = shared->gate.scale_inv;
+    a.shared_up_weight = shared->up.weight;
+    a.shared_up_scale = shared->up.scale_inv;
+    a.shared_down_weight = shared->down.weight;
+    a.shared_down_scale = shared->down.scale_inv;
+    a.shared_gate_flags = shared->gate.code_flags;
+    a.shared_up_flags = shared->up.code_flags;
+    a.shared_down_flags = shared->down.code_flags;
+  }
+  a.logits = p->logit_words;
+  a.hidden_words = p->hidden_words;
+  a.hidden_plain = p->hidden;
+  a.shared_words = p->shared_words;
+  a.control = p->control;
+  a.ids_out = p->ids;
+  a.scores_out = p->scores;
+  a.error_flag = p->err;
+  const int gu_items = static_cast<int>(cdiv(I, 4 * rpw));
+  a.n_router = router != nullptr ? static_cast<int>(cdiv(p->E, 4)) : 0;
+  a.n_shared_gu = shared != nullptr ? gu_items : 0;
+  a.n_routed_gu = k * gu_items;
+  a.n_shared_down = shared != nullptr ? static_cast<int>(cdiv(H, 4 * sdr)) : 0;
+  a.n_down = static_cast<int>(cdiv(H, kLayerDownRows));
+  a.gu_rows_per_wave = rpw;
+  a.shared_down_rows_per_wave = sdr;
+  const int items = a.n_router + a.n_shared_gu + a.n_routed_gu + a.n_shared_down + a.n_down;
+  const int grid = std::min(items, p->layer_grid);
+  HIP_TRY(launch_decode_layer(a, grid, st), "decode layer launch");
+  return GLM53_OK;
+}
+
 int run_router_decode(glm53_decode_plan* p, const glm53_router* r, const void* x, hipStream_t st) {
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -597,6 +761,8 @@ int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank, con
   int rc = check_decode_inputs(plan, bank, shared);
   if (rc) return rc;
   CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
+  rc = run_layer(plan, bank, shared, nullptr, x, expert_ids, scores, nullptr, out, S(stream));
+  if (rc >= 0) return rc;
   return run_decode(plan, bank, shared, x, expert_ids, scores, nullptr, nullptr, out, GLM53_STAGE_ALL, S(stream));
 }
 
@@ -608,9 +774,13 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm5
   if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
   CHECK_ARG(x && out, "null pointer argument");
   hipStream_t st = S(stream);
-  if ((rc = run_router_decode(plan, router, x, st))) return rc;
-  if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, nullptr, out, GLM53_STAGE_ALL, st)))
-    return rc;
+  rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, nullptr, out, st);
+  if (rc > 0) return rc;
+  if (rc < 0) {
+    if ((rc = run_router_decode(plan, router, x, st))) return rc;
+    if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, nullptr, out, GLM53_STAGE_ALL, st)))
+      return rc;
+  }
   if (ids_out) HIP_TRY(hipMemcpyAsync(ids_out, plan->ids, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy ids");
   if (scores_out)
     HIP_TRY(hipMemcpyAsync(scores_out, plan->scores, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy scores");
@@ -638,10 +808,12 @@ int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, vo
   if (!plan->bound) return fail(GLM53_BAD_STATE, "decode plan has no bound weights");
   CHECK_ARG(x && out, "null pointer argument");
   hipStream_t st = S(stream);
-  int rc = run_router_decode(plan, &plan->router, x, st);
-  if (rc) return rc;
-  return run_decode(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, x, plan->ids, plan->scores,
-                    &plan->router, nullptr, out, GLM53_STAGE_ALL, st);
+  const glm53_shared_expert* shared = plan->has_shared ? &plan->shared : nullptr;
+  int rc = run_layer(plan, &plan->bank, shared, &plan->router, x, nullptr, nullptr, nullptr, out, st);
+  if (rc >= 0) return rc;
+  if ((rc = run_router_decode(plan, &plan->router, x, st))) return rc;
+  return run_decode(plan, &plan->bank, shared, x, plan->ids, plan->scores, &plan->router, nullptr, out,
+                    GLM53_STAGE_ALL, st);
 }
 
 int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
@@ -654,6 +826,10 @@ int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const g
   hipStream_t st = S(stream);
   if (stages & (GLM53_STAGE_ROUTER | GLM53_STAGE_GATE_UP)) {
     if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  }
+  if (stages == GLM53_STAGE_ALL) {
+    rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, residual, out, st);
+    if (rc >= 0) return rc;
   }
   if (stages & GLM53_STAGE_ROUTER) {
     if ((rc = run_router_decode(plan, router, x, st))) return rc;
@@ -673,6 +849,13 @@ int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wav
   return GLM53_OK;
 }
 
+int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode) {
+  CHECK_ARG(plan != nullptr, "plan is null");
+  CHECK_ARG(mode == GLM53_DECODE_THREE_LAUNCH || mode == GLM53_DECODE_SINGLE_LAUNCH, "unknown decode mode %d", mode);
+  plan->mode = mode;
+  return GLM53_OK;
+}
+
 int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes) {
   CHECK_ARG(plan && ptr && bytes, "null pointer argument");
   switch (which) {
@@ -687,6 +870,10 @@ int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr
     case 2:
       *ptr = plan->scores;
       *bytes = 4 * plan->k;
+      return GLM53_OK;
+    case 3:
+      *ptr = plan->control;
+      *bytes = 64;
       return GLM53_OK;
     default:
       return fail(GLM53_INVALID_ARGUMENT, "unknown scratch id %d", which);

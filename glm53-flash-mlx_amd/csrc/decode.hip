@@ -14,221 +14,9 @@
 // (block_fp8_linear), patch.py:131-142 (FP32 router).
 #include "common.h"
 #include "kernels.h"
+#include "stream_gemv.h"
 
 namespace glm53 {
-
-// ------------------------------------------------------------ helpers ----
-
-// A lane's activation slice: CH chunks of VB consecutive elements at
-// positions VB*lane + 64*VB*c, held as FP16 pairs.  HW = true pairs them
-// (x0,x1),(x2,x3) for the gfx950 E4M3->FP16 converter; HW = false pairs
-// them (x0,x2),(x1,x3) for the exact SWAR decode in common.h.
-template <int VB, int CH, bool HW>
-struct XSlice {
-  uint32_t p[CH][VB / 2];
-  float factor;  // 2^shift (HW) or 2^(8 + shift) (SWAR bias of 2^-8)
-};
-
-template <int VB, int CH, bool HW>
-__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane, XSlice<VB, CH, HW>& xs) {
-  float v[CH][VB];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const uint16_t* src = x + VB * lane + 64 * VB * c;
-#pragma unroll
-    for (int i = 0; i < VB; i += 8) {
-      uint4 q = *reinterpret_cast<const uint4*>(src + i);
-      uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[c][i + 2 * j] = __uint_as_float(w[j] << 16);
-        v[c][i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-      }
-    }
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int c = 0; c < CH; ++c)
-#pragma unroll
-    for (int i = 0; i < VB; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
-  const int shift = f16_shift_for(amax);
-  const float down = ldexpf(1.0f, -shift);
-  xs.factor = ldexpf(1.0f, (HW ? 0 : 8) + shift);
-#pragma unroll
-  for (int c = 0; c < CH; ++c)
-#pragma unroll
-    for (int j = 0; j < VB / 4; ++j) {
-      if (HW) {
-        xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 1] * down);
-        xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 2] * down, v[c][4 * j + 3] * down);
-      } else {
-        xs.p[c][2 * j] = pack_f16x2(v[c][4 * j] * down, v[c][4 * j + 2] * down);
-        xs.p[c][2 * j + 1] = pack_f16x2(v[c][4 * j + 1] * down, v[c][4 * j + 3] * down);
-      }
-    }
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-// One lane's VB weight bytes of a chunk.  Weights are streamed exactly once
-// per launch, so they are loaded non-temporally (no L2 / MALL retention).
-template <int VB>
-struct WChunk;
-template <>
-struct WChunk<16> {
-  u32x4 q;
-  __device__ __forceinline__ void load(const uint8_t* p) {
-    q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  }
-  __device__ __forceinline__ uint32_t word(int j) const { return q[j]; }
-};
-template <>
-struct WChunk<8> {
-  u32x2 q;
-  __device__ __forceinline__ void load(const uint8_t* p) {
-    q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-  }
-  __device__ __forceinline__ uint32_t word(int j) const { return q[j]; }
-};
-
-// Unscaled partial dot of one chunk (VB weight bytes) with the lane's
-// activations of that chunk.
-template <int VB, int CH, bool HW>
-__device__ __forceinline__ float chunk_dot(const WChunk<VB>& w, const XSlice<VB, CH, HW>& xs, int c) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VB / 4; ++j) {
-    if (HW) {
-      // v_cvt_scalef32_pk_f16_fp8: two E4M3 bytes -> two exact FP16 (OCP;
-      // only used when the weights hold no 0x7F / 0xFF code)
-      const half2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.word(j), 1.0f, false);
-      const half2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.word(j), 1.0f, true);
-      acc = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(half2_t, xs.p[c][2 * j]), acc, false);
-      acc = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(half2_t, xs.p[c][2 * j + 1]), acc, false);
-    } else {
-      acc = dot4_e4m3(w.word(j), xs.p[c][2 * j], xs.p[c][2 * j + 1], acc);
-    }
-  }
-  return acc;
-}
-
-// Lane partial of one row whose block-scale row is `srow` (SC scales).
-template <int VB, int CH, bool HW>
-__device__ __forceinline__ float row_partial(const WChunk<VB> (&w)[CH], const float* __restrict__ srow,
-                                             const XSlice<VB, CH, HW>& xs, int lane) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    float s = srow[(VB * lane + 64 * VB * c) >> 7];
-    acc += chunk_dot<VB, CH, HW>(w[c], xs, c) * s;
-  }
-  return acc * xs.factor;
-}
-
-// The register decode is usable unless a (device) scan flagged 0x7F / 0xFF
-// codes; a null flag means "not scanned" and keeps the exact SWAR decode.
-__device__ __forceinline__ bool hw_decode_ok(const int32_t* flag) { return flag != nullptr && *flag == 0; }
-
-template <int VB, int CH>
-__device__ __forceinline__ void load_row(WChunk<VB> (&w)[CH], const uint8_t* __restrict__ row, int lane) {
-#pragma unroll
-  for (int c = 0; c < CH; ++c) w[c].load(row + VB * lane + 64 * VB * c);
-}
-
-__device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
-  return e < 0 || static_cast<int64_t>(e) >= experts;
-}
-
-// 64-bit top-k key: order-preserving bits of the choice score above the
-// complemented expert id, so max(key) = max score, then min id.  NaN -> -inf.
-__device__ __forceinline__ uint64_t topk_key(float v, uint32_t id) {
-  if (v != v) v = -__builtin_inff();
-  uint32_t u = __float_as_uint(v);
-  u ^= (u & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u;
-  return (static_cast<uint64_t>(u) << 32) | (0xFFFFFFFFu - id);
-}
-
-// ------------------------------------------------------------------ top-k --
-//
-// Selection half of the router (patch.py:131-142 with the DeepSeek-V3
-// aux-loss-free rule): one wavefront reads the FP32 logits of one token,
-// forms sigma = sigmoid(logit) and choice = sigma + bias, and picks top_k by
-// (choice desc, expert id asc).  Lane l holds candidates l, l+64, ... as
-// 64-bit keys, so each round is one max-reduction.  Weights = sigma of the
-// picks, normalised in slot order when norm, times the scaling factor.
-// Emits ids[slot] / weights[slot] (lane 0 stores; dst may be LDS or global).
-// PER_LANE = candidates per lane, a compile-time bound (experts <= 64 *
-// PER_LANE) that keeps the selection in a handful of registers.
-template <int PER_LANE>
-__device__ __forceinline__ void wave_topk_emit(const float* __restrict__ logits, const float* __restrict__ bias,
-                                               int64_t experts, int top_k, float scaling, int norm, int lane,
-                                               int32_t* ids_dst, float* w_dst) {
-  uint64_t keys[PER_LANE];
-  float sigs[PER_LANE];
-#pragma unroll
-  for (int i = 0; i < PER_LANE; ++i) {
-    const int64_t c = lane + 64 * i;
-    float sg = 0.0f;
-    keys[i] = 0ull;
-    if (c < experts) {
-      sg = 1.0f / (1.0f + expf(-logits[c]));
-      keys[i] = topk_key(__fadd_rn(sg, bias[c]), static_cast<uint32_t>(c));
-    }
-    sigs[i] = sg;
-  }
-  float total = 0.0f;
-#pragma unroll 1
-  for (int slot = 0; slot < top_k; ++slot) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) best = keys[i] > best ? keys[i] : best;
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint64_t other = __shfl_xor(best, off);
-      best = other > best ? other : best;
-    }
-    const int32_t best_id = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
-    float mine = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) {
-      if (keys[i] == best) {
-        mine = sigs[i];
-        keys[i] = 0ull;  // taken
-      }
-    }
-    const float w = __shfl(mine, best_id & 63);
-    total = __fadd_rn(total, w);
-    if (lane == 0) {
-      ids_dst[slot] = best_id;
-      w_dst[slot] = w;
-    }
-  }
-  if (lane == 0) {
-    for (int slot = 0; slot < top_k; ++slot) {
-      float v = w_dst[slot];
-      if (top_k > 1 && norm) v = v / total;
-      w_dst[slot] = __fmul_rn(v, scaling);
-    }
-  }
-}
-
-__device__ __forceinline__ void wave_topk(const float* __restrict__ logits, const float* __restrict__ bias,
-                                          int64_t experts, int top_k, float scaling, int norm, int lane,
-                                          int32_t* ids_dst, float* w_dst) {
-  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else if (experts <= 320) wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else wave_topk_emit<kMaxRouterExperts / 64>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-}
-
-// Narrow form for the gate/up prologue (experts <= 320; wider routers select
-// in topk_kernel first), so the selection never raises the streaming kernel's
-// register count.
-__device__ __forceinline__ void wave_topk_narrow(const float* __restrict__ logits, const float* __restrict__ bias,
-                                                 int64_t experts, int top_k, float scaling, int norm, int lane,
-                                                 int32_t* ids_dst, float* w_dst) {
-  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-}
 
 // --------------------------------------------- fused routed gate/up/SwiGLU --
 //

@@ -62,6 +62,54 @@ struct DownArgs {
   const int32_t* shared_flags;
 };
 
+// One-launch decode layer (layer.hip).
+constexpr int kLayerDownRows = 16;  // output rows of one routed down item
+
+struct LayerArgs {
+  const uint16_t* x;              // [H] bf16
+  const uint16_t* residual;       // [H] bf16 or null
+  uint16_t* out;                  // [H] bf16
+  int64_t hidden, intermediate;   // H, I (shared expert width == I)
+  int64_t experts;
+  int top_k;
+  float limit;
+  // routing: router (weight non-null) or given ids / scores
+  const float* router_weight;     // [E, H]
+  const float* router_bias;       // [E]
+  float routed_scaling_factor;
+  int norm_topk_prob;
+  const int32_t* given_ids;       // [top_k] or null
+  const float* given_scores;      // [top_k]
+  // packed bank and shared expert (shared pointers null when absent)
+  const uint8_t* gate_up_weight;
+  const float* gate_up_scale;
+  const uint8_t* down_weight;
+  const float* down_scale;
+  const uint8_t* shared_gate_weight;
+  const float* shared_gate_scale;
+  const uint8_t* shared_up_weight;
+  const float* shared_up_scale;
+  const uint8_t* shared_down_weight;
+  const float* shared_down_scale;
+  const int32_t* routed_flags;
+  const int32_t* shared_gate_flags;
+  const int32_t* shared_up_flags;
+  const int32_t* shared_down_flags;
+  // plan scratch
+  uint64_t* logits;               // [E] epoch-tagged FP32
+  uint64_t* hidden_words;         // [(top_k + 1) * I / 2] epoch-tagged BF16 pairs
+  uint16_t* hidden_plain;         // [(top_k + 1) * I] bf16 copy (diagnostics)
+  uint64_t* shared_words;         // [H / 2] epoch-tagged BF16 pairs (shared down)
+  uint32_t* control;              // [0] ticket, [1] exits, [2] epoch
+  int32_t* ids_out;               // [top_k]
+  float* scores_out;              // [top_k]
+  int* error_flag;
+  // work items, in ticket order
+  int n_router, n_shared_gu, n_routed_gu, n_shared_down, n_down;
+  int gu_rows_per_wave;           // even
+  int shared_down_rows_per_wave;  // even
+};
+
 struct RouterArgs {
   const uint16_t* x;       // [H] bf16
   const float* weight;     // [E, H]
@@ -129,6 +177,9 @@ struct TopkArgs {
 constexpr int kGenericRows = 8;
 
 bool fast_width_supported(int64_t K);
+bool layer_shape_supported(int64_t H, int64_t I);
+int layer_occupancy(int64_t H, int64_t I);
+hipError_t launch_decode_layer(const LayerArgs& a, int grid, hipStream_t st);
 hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st);
 hipError_t launch_down(const DownArgs& a, hipStream_t st);
 hipError_t launch_router(const RouterArgs& a, hipStream_t st);

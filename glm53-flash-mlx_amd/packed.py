@@ -219,6 +219,10 @@ class DecodePlan:
     def tune(self, gate_up_rows_per_wave: int = 8, down_rows_per_wg: int = 16) -> None:
         N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))
 
+    def set_mode(self, mode: int) -> None:
+        """N.DECODE_SINGLE_LAUNCH (default) or N.DECODE_THREE_LAUNCH."""
+        N.check(self._lib.glm53_decode_plan_set_mode(self.handle, int(mode)))
+
     def error_flag(self) -> int:
         value = ctypes.c_int32()
         N.check(self._lib.glm53_decode_plan_error_flag(self.handle, ctypes.byref(value)))

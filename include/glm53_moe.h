@@ -185,13 +185,31 @@ int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, vo
 int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wave,
                            int32_t down_rows_per_wg);
 
+/* Execution form of the full decode calls (glm53_decode_moe, _routed,
+ * _bound, and _ex with GLM53_STAGE_ALL):
+ *   GLM53_DECODE_THREE_LAUNCH (default) -- router, gate/up, down as three
+ *     launches;
+ *   GLM53_DECODE_SINGLE_LAUNCH -- one persistent launch per layer (router,
+ *     top-k, routed + shared gate/up/SwiGLU, down, reduction, residual) for
+ *     the instantiated shapes (H, I) in {(4096, 1536), (4096, 2048),
+ *     (2048, 1024), (1024, 512)} with experts <= 320 (other shapes and
+ *     partial stage masks run the three-launch form).  Its workgroups on
+ *     different XCDs exchange data through uncached memory, which makes it
+ *     slower than the three-launch form on MI355X today.
+ * With given expert ids both forms give the same bits; with the router they
+ * differ only in the FP32 summation order of the router logits. */
+#define GLM53_DECODE_THREE_LAUNCH 0
+#define GLM53_DECODE_SINGLE_LAUNCH 1
+int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode);
+
 /* Device scratch of the last call (read-only diagnostics): which = 0 hidden
  * bf16 [top_k + 1, I] (routed rows, then shared), 1 expert ids int32
  * [top_k], 2 scores f32 [top_k]. */
 int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes);
 
-/* Synchronous: copies the plan's device error flag to *host_value (nonzero
- * when an expert id was out of range) and clears it. */
+/* Synchronous: copies the plan's device error flag to *host_value and
+ * clears it: bit 0 = an expert id was out of range, bit 1 = a wait of the
+ * single-launch kernel gave up (its outputs are then not valid). */
 int glm53_decode_plan_error_flag(glm53_decode_plan* plan, int32_t* host_value);
 
 /* ------------------------------------------------------------------------

@@ -74,6 +74,8 @@ def test_abi_version_and_constants(N, libso):
         header_define(n) for n in ("GLM53_OK", "GLM53_INVALID_ARGUMENT", "GLM53_BAD_STATE", "GLM53_DEVICE_ERROR"))
     assert (N.REDUCE_GROUPED, N.REDUCE_DIRECT) == (header_define("GLM53_REDUCE_GROUPED"),
                                                    header_define("GLM53_REDUCE_DIRECT"))
+    assert (N.DECODE_THREE_LAUNCH, N.DECODE_SINGLE_LAUNCH) == (header_define("GLM53_DECODE_THREE_LAUNCH"),
+                                                             header_define("GLM53_DECODE_SINGLE_LAUNCH"))
     assert (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN, N.STAGE_ALL) == tuple(
         header_define(n) for n in ("GLM53_STAGE_ROUTER", "GLM53_STAGE_GATE_UP", "GLM53_STAGE_DOWN",
                                    "GLM53_STAGE_ALL"))
