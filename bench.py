@@ -7,8 +7,8 @@ experts, top-8, one shared expert, FP32 router; 229 GB of E4M3 banks
 resident in HBM), one BF16 token per step with a residual add, a fresh
 seeded input every step.  One step (42 x 3 launches + the input draw) is
 captured once as a HIP graph and replayed; `value` = microseconds per MoE
-layer = step time / 42.  The dominant kernel (fused routed + shared
-gate/up/SwiGLU with the top-k prologue) is the `roofline` entry, timed with
+layer = step time / 42.  The dominant kernel (top-k prologue, routed
+gate/up/SwiGLU, shared down) is the `roofline` entry, timed with
 HIP events on its stream against the HBM roofline.  The one-launch form
 (decode_layer_kernel) is timed beside it for comparison.
 
@@ -74,10 +74,14 @@ def decode_layer_bytes(H, I, Is, E, k):
             "activations": 2 * H * 2, "total": router + gate_up + down + shared + 2 * H * 2}
 
 
-def gate_up_launch_bytes(H, I, Is, k):
+def step_launch_bytes(H, I, Is, E, k):
+    """Algorithmic bytes of the three decode launches (each weight byte once,
+    activations read / written once, the residual read once)."""
     sr, sh, srs = math.ceil(I / 128), math.ceil(H / 128), math.ceil(Is / 128)
-    weights = k * (2 * I * H + 2 * sr * sh * 4) + 2 * Is * H + 2 * srs * sh * 4
-    return weights + H * 2 + (k * I + Is) * 2
+    router_shared = E * H * 4 + (2 * Is * H + 2 * srs * sh * 4) + H * 2 + E * 4 + Is * 2
+    gate_up = k * (2 * I * H + 2 * sr * sh * 4) + (Is * H + sh * srs * 4) + H * 2 + E * 4 * 2 + k * I * 2 + Is * 2 + H * 2
+    down = k * (H * I + sh * sr * 4) + k * I * 2 + H * 2 + H * 2 + H * 2
+    return {"router_shared": router_shared, "gate_up": gate_up, "down": down}
 
 
 def main():
@@ -180,11 +184,11 @@ def main():
         stage_us[name] = time_graph(run_stage(mask), args.kernel_steps * 8, torch) / L
     router_us, gate_up_us, down_us = stage_us["router"], stage_us["gate_up"], stage_us["down"]
     probe = read_probe(lib, N, layers[-1].bank, dev, torch)
-    gu_bytes = gate_up_launch_bytes(H, I, Is, k)
+    launch_bytes = step_launch_bytes(H, I, Is, E, k)
+    gu_bytes = launch_bytes["gate_up"]
     gu_gbs = gu_bytes / (gate_up_us * 1e-6) / 1e9
-    down_bytes = (bytes_layer["routed_down"] + Is * H + math.ceil(H / 128) * math.ceil(Is / 128) * 4
-                  + (k + 1) * I * 2 + 2 * H * 2)
-    log(f"launches: router {router_us:.2f} us, gate/up {gate_up_us:.2f} us ({gu_gbs:.0f} GB/s), "
+    down_bytes = launch_bytes["down"]
+    log(f"launches: router+shared {router_us:.2f} us, gate/up {gate_up_us:.2f} us ({gu_gbs:.0f} GB/s), "
         f"down {down_us:.2f} us ({down_bytes / (down_us * 1e-6) / 1e9:.0f} GB/s)")
 
     # The one-launch form (decode_layer_kernel), for comparison.
@@ -232,12 +236,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate_up_swiglu_kernel<16,4> (8 routed + shared gate/up rows, fused top-k and SwiGLU)",
+            "kernel": "step_gate_up_kernel<16,4,3> (top-k, 8 routed gate/up rows with SwiGLU, shared down rows)",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
-            "traffic": load_traffic("gate_up_swiglu_kernel"),
+            "traffic": load_traffic("step_gate_up_kernel"),
             "traffic_source": "profiles/decode_traffic_pmc.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)",
             "bytes_per_launch": gu_bytes,
             "avg_launch_us": round(gate_up_us, 3),
@@ -248,11 +252,13 @@ def main():
             "layer_bytes": bytes_layer["total"],
             "layer_GBps": round(layer_gbs, 1),
             "layer_hbm_frac": round(layer_gbs / PEAK_HBM_GBS, 4),
-            "launch_us": {"router": round(router_us, 3), "gate_up": round(gate_up_us, 3),
+            "launch_us": {"router_shared": round(router_us, 3), "gate_up": round(gate_up_us, 3),
                           "down_reduce": round(down_us, 3)},
-            "launch_GBps": {"gate_up": round(gu_gbs, 1),
+            "launch_bytes": launch_bytes,
+            "launch_GBps": {"router_shared": round(launch_bytes["router_shared"] / (router_us * 1e-6) / 1e9, 1),
+                            "gate_up": round(gu_gbs, 1),
                             "down_reduce": round(down_bytes / (down_us * 1e-6) / 1e9, 1)},
-            "launch_note": "router stage-only graphs are dispatch-gap bound; its kernel time is in profiles/",
+            "launch_note": "stage-only graphs of one launch kind; kernel durations in profiles/",
             "achievable_read_GBps": probe,
             "one_launch_form": single,
             "weights_generated_s": round(gen_s, 1),
@@ -505,7 +511,7 @@ def summarize_traffic(fetch_csv, write_csv):
     copy_kw = pick(write, "copyBuffer") or pick(write, "elementwise_kernel")
     fetch_scale = probe_bytes / (fetch[probe_k][0] * 1024.0)
     write_scale = copy_bytes / (write[copy_kw][0] * 1024.0)
-    keys = ("decode_layer_kernel", "gate_up_swiglu_kernel", "down_reduce_kernel", "router_logits_kernel",
+    keys = ("step_router_shared_kernel", "step_gate_up_kernel", "step_down_kernel", "decode_layer_kernel",
             "probe_read_kernel")
     print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (calibrated) | written B (calibrated) |")
     print("|---|---|---|---|---|---|")

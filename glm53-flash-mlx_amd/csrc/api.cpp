@@ -354,6 +354,8 @@ struct glm53_decode_plan {
   uint64_t* shared_words = nullptr;  // [H / 2]
   uint32_t* control = nullptr;       // [4]: ticket, exits, epoch, last stale tag seen
   int layer_grid = 0;                // persistent grid (CUs x resident workgroups), found on first use
+  int step_slots = 0;                // CUs x resident workgroups of the routed gate/up launch
+  uint32_t* router_count = nullptr;  // arrival counter of the step's router launch
   void* exchange = nullptr;          // uncached block holding the three word arrays
   size_t exchange_bytes = 0;
   glm53_bank bank{};
@@ -390,7 +392,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   size_t o_gate = take(2 * top_k * intermediate), o_up = take(2 * top_k * intermediate);
   size_t o_down = take(2 * top_k * hidden), o_routed = take(2 * hidden);
   size_t o_sg = take(2 * std::max<int64_t>(shared_intermediate, 1)), o_su = take(2 * std::max<int64_t>(shared_intermediate, 1));
-  size_t o_so = take(2 * hidden), o_mo = take(2 * hidden);
+  size_t o_so = take(2 * hidden), o_mo = take(2 * hidden), o_rc = take(4);
   hipError_t e = hipMalloc(&p->arena, off);
   if (e != hipSuccess) {
     delete p;
@@ -416,6 +418,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   p->shared_up = reinterpret_cast<uint16_t*>(b + o_su);
   p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
   p->moe_out = reinterpret_cast<uint16_t*>(b + o_mo);
+  p->router_count = reinterpret_cast<uint32_t*>(b + o_rc);
   {
     size_t xo = 0;
     auto xtake = [&](size_t bytes) {
@@ -743,6 +746,73 @@ int run_layer(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_e
   return GLM53_OK;
 }
 
+// The three-launch step (step.hip) when the shape is instantiated; returns
+// -1 (nothing launched) otherwise.  router != NULL: launch 1 computes the
+// logits and the selection into the plan's ids / scores; else `ids` /
+// `scores` are the caller's.
+int run_step(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+             const glm53_router* router, const void* x, const int32_t* ids, const float* scores,
+             const void* residual, void* out, int stages, hipStream_t st) {
+  if (!decode_fast_ok(p, bank, shared, x) || !step_shape_supported(p->H, p->I)) return -1;
+  if (router != nullptr && (router->experts > 320 || !aligned(router->weight, 16))) return -1;
+  if (!aligned(out, 4)) return -1;
+  if (p->step_slots == 0) {
+    int dev = 0, cus = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+    const int occ = step_gate_up_occupancy(p->H, p->I);
+    if (occ <= 0 || cus <= 0) return -1;
+    p->step_slots = cus * occ;
+  }
+  StepArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.out = static_cast<uint16_t*>(out);
+  a.hidden = p->H;
+  a.intermediate = p->I;
+  a.experts = p->E;
+  a.top_k = static_cast<int>(p->k);
+  a.limit = p->limit;
+  if (router != nullptr) {
+    a.router_weight = router->weight;
+    a.router_bias = router->bias;
+    a.routed_scaling_factor = router->routed_scaling_factor;
+    a.norm_topk_prob = router->norm_topk_prob;
+    a.ids = p->ids;
+    a.scores = p->scores;
+    a.router_wgs = static_cast<int>(cdiv(p->E, 4));
+  } else {
+    a.ids = const_cast<int32_t*>(ids);
+    a.scores = const_cast<float*>(scores);
+  }
+  a.logits = p->sig;
+  a.router_count = p->router_count;
+  a.gate_up_weight = bank->gate_up_weight;
+  a.gate_up_scale = bank->gate_up_scale_inv;
+  a.down_weight = bank->down_weight;
+  a.down_scale = bank->down_scale_inv;
+  a.routed_flags = bank->code_flags;
+  if (shared != nullptr) {
+    a.shared_gate_weight = shared->gate.weight;
+    a.shared_gate_scale = shared->gate.scale_inv;
+    a.shared_up_weight = shared->up.weight;
+    a.shared_up_scale = shared->up.scale_inv;
+    a.shared_down_weight = shared->down.weight;
+    a.shared_down_scale = shared->down.scale_inv;
+    a.shared_gate_flags = shared->gate.code_flags;
+    a.shared_up_flags = shared->up.code_flags;
+    a.shared_down_flags = shared->down.code_flags;
+  }
+  a.hidden_act = p->hidden;
+  a.shared_out = p->shared_out;
+  a.error_flag = p->err;
+  a.shared_rows_per_wave = 2;
+  const int sd_wgs = shared != nullptr ? static_cast<int>(cdiv(p->H, 64)) : 0;
+  a.routed_wgs = std::max(64, p->step_slots - sd_wgs);
+  HIP_TRY(launch_step(a, stages, st), "decode step launch");
+  return GLM53_OK;
+}
+
 int run_router_decode(glm53_decode_plan* p, const glm53_router* r, const void* x, hipStream_t st) {
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -763,6 +833,8 @@ int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank, con
   CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
   rc = run_layer(plan, bank, shared, nullptr, x, expert_ids, scores, nullptr, out, S(stream));
   if (rc >= 0) return rc;
+  rc = run_step(plan, bank, shared, nullptr, x, expert_ids, scores, nullptr, out, GLM53_STAGE_ALL, S(stream));
+  if (rc >= 0) return rc;
   return run_decode(plan, bank, shared, x, expert_ids, scores, nullptr, nullptr, out, GLM53_STAGE_ALL, S(stream));
 }
 
@@ -775,6 +847,7 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm5
   CHECK_ARG(x && out, "null pointer argument");
   hipStream_t st = S(stream);
   rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, nullptr, out, st);
+  if (rc < 0) rc = run_step(plan, bank, shared, router, x, nullptr, nullptr, nullptr, out, GLM53_STAGE_ALL, st);
   if (rc > 0) return rc;
   if (rc < 0) {
     if ((rc = run_router_decode(plan, router, x, st))) return rc;
@@ -811,6 +884,8 @@ int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, vo
   const glm53_shared_expert* shared = plan->has_shared ? &plan->shared : nullptr;
   int rc = run_layer(plan, &plan->bank, shared, &plan->router, x, nullptr, nullptr, nullptr, out, st);
   if (rc >= 0) return rc;
+  rc = run_step(plan, &plan->bank, shared, &plan->router, x, nullptr, nullptr, nullptr, out, GLM53_STAGE_ALL, st);
+  if (rc >= 0) return rc;
   if ((rc = run_router_decode(plan, &plan->router, x, st))) return rc;
   return run_decode(plan, &plan->bank, shared, x, plan->ids, plan->scores, &plan->router, nullptr, out,
                     GLM53_STAGE_ALL, st);
@@ -831,6 +906,8 @@ int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const g
     rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, residual, out, st);
     if (rc >= 0) return rc;
   }
+  rc = run_step(plan, bank, shared, router, x, nullptr, nullptr, residual, out, stages, st);
+  if (rc >= 0) return rc;
   if (stages & GLM53_STAGE_ROUTER) {
     if ((rc = run_router_decode(plan, router, x, st))) return rc;
   }

@@ -62,6 +62,49 @@ struct DownArgs {
   const int32_t* shared_flags;
 };
 
+// Three-launch decode step (step.hip).
+struct StepArgs {
+  const uint16_t* x;              // [H] bf16
+  const uint16_t* residual;       // [H] bf16 or null
+  uint16_t* out;                  // [H] bf16
+  int64_t hidden, intermediate;   // H, I (shared expert width == I)
+  int64_t experts;
+  int top_k;
+  float limit;
+  const float* router_weight;     // [E, H] (null: ids / scores given)
+  const float* router_bias;       // [E]
+  float routed_scaling_factor;
+  int norm_topk_prob;
+  float* logits;                  // [E] router logits (read-modify-write exchange in launch 1)
+  uint32_t* router_count;         // arrival counter of launch 1 (self-resetting)
+  int32_t* ids;                   // [top_k]: launch 1 writes (router) or given
+  float* scores;                  // [top_k]
+  const uint8_t* gate_up_weight;
+  const float* gate_up_scale;
+  const uint8_t* down_weight;
+  const float* down_scale;
+  const uint8_t* shared_gate_weight;  // null: no shared expert
+  const float* shared_gate_scale;
+  const uint8_t* shared_up_weight;
+  const float* shared_up_scale;
+  const uint8_t* shared_down_weight;
+  const float* shared_down_scale;
+  const int32_t* routed_flags;
+  const int32_t* shared_gate_flags;
+  const int32_t* shared_up_flags;
+  const int32_t* shared_down_flags;
+  uint16_t* hidden_act;           // [top_k + 1, I] SwiGLU rows (routed slots, then shared)
+  uint16_t* shared_out;           // [H] T(shared down)
+  int* error_flag;
+  int router_wgs;                 // ceil(E / 4) or 0
+  int shared_rows_per_wave;       // launch 1 shared gate/up rows per wavefront
+  int routed_wgs;                 // launch 2 workgroups over the routed units
+};
+
+bool step_shape_supported(int64_t H, int64_t I);
+int step_gate_up_occupancy(int64_t H, int64_t I);
+hipError_t launch_step(const StepArgs& a, int stages, hipStream_t st);
+
 // One-launch decode layer (layer.hip).
 constexpr int kLayerDownRows = 16;  // output rows of one routed down item
 

@@ -45,24 +45,46 @@ __device__ __forceinline__ void pack_x_slice(const float (&v)[CH][VB], XSlice<VB
     }
 }
 
+// The raw BF16 words of a lane's slice.  Issuing these loads first and
+// packing after the weight loads are issued keeps the wait for the
+// activations from also waiting for the weights (vector loads retire in
+// order).
+template <int VB, int CH>
+struct XRaw {
+  uint4 q[CH][VB / 8];
+};
+
+template <int VB, int CH>
+__device__ __forceinline__ void load_x_raw(const uint16_t* __restrict__ x, int lane, XRaw<VB, CH>& raw) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int i = 0; i < VB / 8; ++i)
+      raw.q[c][i] = *reinterpret_cast<const uint4*>(x + VB * lane + 64 * VB * c + 8 * i);
+}
+
 template <int VB, int CH, bool HW>
-__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane, XSlice<VB, CH, HW>& xs) {
+__device__ __forceinline__ void pack_x_raw(const XRaw<VB, CH>& raw, XSlice<VB, CH, HW>& xs) {
   float v[CH][VB];
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const uint16_t* src = x + VB * lane + 64 * VB * c;
+  for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int i = 0; i < VB; i += 8) {
-      uint4 q = *reinterpret_cast<const uint4*>(src + i);
-      uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    for (int i = 0; i < VB / 8; ++i) {
+      const uint32_t w[4] = {raw.q[c][i].x, raw.q[c][i].y, raw.q[c][i].z, raw.q[c][i].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        v[c][i + 2 * j] = __uint_as_float(w[j] << 16);
-        v[c][i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        v[c][8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+        v[c][8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
       }
     }
-  }
   pack_x_slice<VB, CH, HW>(v, xs);
+}
+
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ void load_x_slice(const uint16_t* __restrict__ x, int lane, XSlice<VB, CH, HW>& xs) {
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(x, lane, raw);
+  pack_x_raw<VB, CH, HW>(raw, xs);
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -123,6 +145,34 @@ __device__ __forceinline__ float row_partial(const WChunk<VB> (&w)[CH], const fl
   return acc * xs.factor;
 }
 
+// One weight row as a lane sees it: its CH chunks and the block scale of
+// each chunk.  The scales are loaded with the chunks, in the same batch of
+// vector loads: loaded later, next to the arithmetic, they would make the
+// compiler wait for every load in flight (prefetched rows included) before
+// the first product, since vector loads retire in order.
+template <int VB, int CH>
+struct WRow {
+  WChunk<VB> c[CH];
+  float s[CH];
+};
+
+template <int VB, int CH>
+__device__ __forceinline__ void load_wrow(WRow<VB, CH>& r, const uint8_t* __restrict__ row,
+                                          const float* __restrict__ srow, int lane) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) r.c[c].load(row + VB * lane + 64 * VB * c);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) r.s[c] = srow[(VB * lane + 64 * VB * c) >> 7];
+}
+
+template <int VB, int CH, bool HW>
+__device__ __forceinline__ float wrow_partial(const WRow<VB, CH>& r, const XSlice<VB, CH, HW>& xs) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) acc += chunk_dot<VB, CH, HW>(r.c[c], xs, c) * r.s[c];
+  return acc * xs.factor;
+}
+
 // The register decode is usable unless a (device) scan flagged 0x7F / 0xFF
 // codes; a null flag means "not scanned" and keeps the exact SWAR decode.
 __device__ __forceinline__ bool hw_decode_ok(const int32_t* flag) { return flag != nullptr && *flag == 0; }
@@ -137,77 +187,102 @@ __device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
   return e < 0 || static_cast<int64_t>(e) >= experts;
 }
 
-// 64-bit top-k key: order-preserving bits of the choice score above the
-// complemented expert id, so max(key) = max score, then min id.  NaN -> -inf.
-__device__ __forceinline__ uint64_t topk_key(float v, uint32_t id) {
-  if (v != v) v = -__builtin_inff();
-  uint32_t u = __float_as_uint(v);
-  u ^= (u & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u;
-  return (static_cast<uint64_t>(u) << 32) | (0xFFFFFFFFu - id);
-}
-
 // ------------------------------------------------------------------ top-k --
 //
 // Selection half of the router (patch.py:131-142 with the DeepSeek-V3
 // aux-loss-free rule): one wavefront reads the FP32 logits of one token,
 // forms sigma = sigmoid(logit) and choice = sigma + bias, and picks top_k by
-// (choice desc, expert id asc).  Lane l holds candidates l, l+64, ... as
-// 64-bit keys, so each round is one max-reduction.  Weights = sigma of the
-// picks, normalised in slot order when norm, times the scaling factor.
-// Emits ids[slot] / weights[slot] (lane 0 stores; dst may be LDS or global).
-// PER_LANE = candidates per lane, a compile-time bound (experts <= 64 *
-// PER_LANE) that keeps the selection in a handful of registers.
+// (choice desc, expert id asc).  Lane l holds candidates l, l+64, ...
+// Weights = sigma of the picks, normalised in slot order when norm, times
+// the scaling factor.  Emits ids[slot] (lane 0) and weights[slot] (lane
+// slot); dst may be LDS or global.  PER_LANE = candidates per lane, a
+// compile-time bound (experts <= 64 * PER_LANE) that keeps the selection in
+// a handful of registers.
+
+// DPP wave reductions of unsigned 32-bit values (every lane gets the result).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dpp_u32<0xB1>(v));
+  v = min(v, dpp_u32<0x4E>(v));
+  v = min(v, dpp_u32<0x141>(v));
+  v = min(v, dpp_u32<0x140>(v));
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return min(min(a, b), min(c, d));
+}
+
+// Order-preserving u32 image of a float (NaN ranks as -inf): a > b as floats
+// iff image(a) > image(b), with +0 above -0.
+__device__ __forceinline__ uint32_t orderable_bits(float v) {
+  if (v != v) v = -__builtin_inff();
+  const uint32_t u = __float_as_uint(v);
+  return u ^ ((u & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
 // Core selection over logits already in registers: lg[i] is the logit of
-// expert lane + 64 * i (ignored when that is >= experts).
+// expert lane + 64 * i (ignored when that is >= experts).  Each of the top_k
+// rounds is two DPP reductions: the largest biased score (as its orderable
+// image), then the smallest expert id holding it, i.e. the order
+// (choice desc, expert id asc).
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], const float* __restrict__ bias,
                                                int64_t experts, int top_k, float scaling, int norm, int lane,
                                                int32_t* ids_dst, float* w_dst) {
-  uint64_t keys[PER_LANE];
+  uint32_t key[PER_LANE];  // orderable image of the biased score; 0 = taken / absent
   float sigs[PER_LANE];
 #pragma unroll
   for (int i = 0; i < PER_LANE; ++i) {
     const int64_t c = lane + 64 * i;
     float sg = 0.0f;
-    keys[i] = 0ull;
+    key[i] = 0u;
     if (c < experts) {
       sg = 1.0f / (1.0f + expf(-lg[i]));
-      keys[i] = topk_key(__fadd_rn(sg, bias[c]), static_cast<uint32_t>(c));
+      key[i] = max(orderable_bits(__fadd_rn(sg, bias[c])), 1u);
     }
     sigs[i] = sg;
   }
   float total = 0.0f;
+  float w_mine = 0.0f;  // lane `slot` keeps the weight of its slot
 #pragma unroll 1
   for (int slot = 0; slot < top_k; ++slot) {
-    uint64_t best = 0;
+    uint32_t best = 0;
 #pragma unroll
-    for (int i = 0; i < PER_LANE; ++i) best = keys[i] > best ? keys[i] : best;
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint64_t other = __shfl_xor(best, off);
-      best = other > best ? other : best;
-    }
-    const int32_t best_id = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+    for (int i = 0; i < PER_LANE; ++i) best = max(best, key[i]);
+    best = wave_max_u32(best);
+    uint32_t id = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i)
+      if (key[i] == best) id = min(id, static_cast<uint32_t>(lane + 64 * i));
+    id = wave_min_u32(id);
     float mine = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i) {
-      if (keys[i] == best) {
+      if (static_cast<uint32_t>(lane + 64 * i) == id) {
         mine = sigs[i];
-        keys[i] = 0ull;  // taken
+        key[i] = 0u;  // taken
       }
     }
-    const float w = __shfl(mine, best_id & 63);
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), static_cast<int>(id & 63)));
     total = __fadd_rn(total, w);
-    if (lane == 0) {
-      ids_dst[slot] = best_id;
-      w_dst[slot] = w;
-    }
+    if (lane == slot) w_mine = w;
+    if (lane == 0) ids_dst[slot] = static_cast<int32_t>(id);
   }
-  if (lane == 0) {
-    for (int slot = 0; slot < top_k; ++slot) {
-      float v = w_dst[slot];
-      if (top_k > 1 && norm) v = v / total;
-      w_dst[slot] = __fmul_rn(v, scaling);
-    }
+  if (lane < top_k) {
+    float v = w_mine;
+    if (top_k > 1 && norm) v = v / total;
+    w_dst[lane] = __fmul_rn(v, scaling);
   }
 }
 

@@ -196,8 +196,9 @@ int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wav
  *     partial stage masks run the three-launch form).  Its workgroups on
  *     different XCDs exchange data through uncached memory, which makes it
  *     slower than the three-launch form on MI355X today.
- * With given expert ids both forms give the same bits; with the router they
- * differ only in the FP32 summation order of the router logits. */
+ * Both forms apply the same BF16 roundings; the FP32 summation order inside
+ * a row differs (router logits, down rows), so they agree to within the BF16
+ * rounding of those sums. */
 #define GLM53_DECODE_THREE_LAUNCH 0
 #define GLM53_DECODE_SINGLE_LAUNCH 1
 int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode);

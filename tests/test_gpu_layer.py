@@ -1,11 +1,12 @@
 """GPU parity of the one-launch decode layer (layer.hip) against the
 three-launch kernels and the CPU oracle.
 
-With given expert ids both forms compute the same arithmetic, so they must
-agree bit for bit; with the router they differ only in the FP32 summation
-order of the logits (one wavefront per logit vs one workgroup), so the
-selection is checked against the oracle with the near-tie rule and outputs
-against the oracle's tolerance gates.
+Both forms compute the same roundings (T(gate), T(up), SwiGLU, T(down),
+ordered FP32 slot sum); they differ in the FP32 summation order inside a
+down-projection row (one wavefront vs one half-wavefront per row) and of
+the router logits, so outputs agree to within the BF16 rounding of those
+sums: checked against each other with the tolerance gates and a floor on
+bit-identical outputs, and against the CPU oracle.
 """
 
 from __future__ import annotations
@@ -53,9 +54,9 @@ def _bits_equal(a, b):
 
 
 @pytest.mark.parametrize("which", ["small", "config2"])
-def test_routed_single_launch_equals_three_launch(which, small, config2, dev):
-    """Given ids: identical bits, over several calls (the launch epoch
-    advances every call), with and without the shared expert."""
+def test_routed_single_launch_matches_three_launch(which, small, config2, dev, O):
+    """Given ids, over several calls (the launch epoch advances every call),
+    with and without the shared expert."""
     import torch
 
     syn = submodule("synthetic")
@@ -72,7 +73,7 @@ def test_routed_single_launch_equals_three_launch(which, small, config2, dev):
         single.routed(bank, sh, x, ids, sc, y1, dev)
         three.routed(bank, sh, x, ids, sc, y3, dev)
         torch.cuda.synchronize()
-        assert _bits_equal(y1, y3), (which, step)
+        assert_parity(to_bits(y1).reshape(-1), to_bits(y3).reshape(-1), O, exact_fraction=0.95)
     assert single.error_flag() == 0 and three.error_flag() == 0
 
 
