@@ -261,7 +261,7 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
     g.N = N;
     g.out = static_cast<uint16_t*>(y);
     g.out_row_stride = N;
-    HIP_TRY(launch_grouped_gemm(g, GEMM_PLAIN, cdiv(M, kGroupedTileRows), st), "grouped gemm launch");
+    HIP_TRY(launch_grouped_gemm(g, GEMM_PLAIN, cdiv(M, kGemmTileRows), st), "grouped gemm launch");
     return GLM53_OK;
   }
   GenericLinearArgs a{};
@@ -1187,7 +1187,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->max_tokens = max_tokens;
   p->limit = swiglu_limit;
   const int64_t T = max_tokens, R = T * top_k, Ism = std::max<int64_t>(shared_intermediate, 128);
-  p->capacity_max = cdiv(R, kGroupedTileRows) + experts;
+  p->capacity_max = cdiv(R, kGemmTileRows) + experts;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -1317,8 +1317,8 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   // 1. activations -> exact hi/lo E4M3 split
   HIP_TRY(split(x, T, H, p->xq, st), "split x");
   // 2. expert-sorted route plan
-  const int64_t cap = cdiv(R, kGroupedTileRows) + E;
-  if ((rc = route_plan_impl(ids, sc, R, k, E, kGroupedTileRows, p->sorted_route, p->inverse, p->sorted_expert,
+  const int64_t cap = cdiv(R, kGemmTileRows) + E;
+  if ((rc = route_plan_impl(ids, sc, R, k, E, kGemmTileRows, p->sorted_route, p->inverse, p->sorted_expert,
                             p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,
                             p->tile_start, p->tile_len, cap, p->status, p->plan_ws, st)))
     return rc;
@@ -1389,7 +1389,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     sg.out = p->hs;
     sg.out_row_stride = Is;
     sg.fixup = shared_gu_flag;
-    HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, kGroupedTileRows), st), "shared gate/up launch");
+    HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, kGemmTileRows), st), "shared gate/up launch");
     HIP_TRY(split(p->hs, T, Is, p->sq, st), "split shared hidden");
     GroupedGemmArgs sd{};
     sd.a_hi = p->sq.hi;
@@ -1405,7 +1405,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     sd.out = p->shared_out;
     sd.out_row_stride = H;
     sd.fixup = shared_down_flag;
-    HIP_TRY(launch_grouped_gemm(sd, GEMM_PLAIN, cdiv(T, kGroupedTileRows), st), "shared down launch");
+    HIP_TRY(launch_grouped_gemm(sd, GEMM_PLAIN, cdiv(T, kGemmTileRows), st), "shared down launch");
     shared_add = p->shared_out;
   }
   // 7. combine

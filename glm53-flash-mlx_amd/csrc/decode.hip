@@ -37,32 +37,35 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const uint8_t*
                                              int64_t r0, int64_t r_end, int lane) {
   const int64_t K = a.hidden;
   const int64_t SC = (K + kBlock - 1) / kBlock;
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(a.x, lane, raw);
   XSlice<VB, CH, HW> xs;
-  load_x_slice<VB, CH, HW>(a.x, lane, xs);
+  bool packed = false;
   int64_t r = r0;
   for (; r + 1 < r_end; r += 2) {
-    WChunk<VB> g0[CH], u0[CH], g1[CH], u1[CH];
-    load_row<VB, CH>(g0, gate_w + r * K, lane);
-    load_row<VB, CH>(u0, up_w + r * K, lane);
-    load_row<VB, CH>(g1, gate_w + (r + 1) * K, lane);
-    load_row<VB, CH>(u1, up_w + (r + 1) * K, lane);
-    float pg0 = row_partial<VB, CH, HW>(g0, gate_s + (r >> 7) * SC, xs, lane);
-    float pu0 = row_partial<VB, CH, HW>(u0, up_s + (r >> 7) * SC, xs, lane);
-    float pg1 = row_partial<VB, CH, HW>(g1, gate_s + ((r + 1) >> 7) * SC, xs, lane);
-    float pu1 = row_partial<VB, CH, HW>(u1, up_s + ((r + 1) >> 7) * SC, xs, lane);
-    float tg0 = wave_sum(pg0), tu0 = wave_sum(pu0);
-    float tg1 = wave_sum(pg1), tu1 = wave_sum(pu1);
+    WRow<VB, CH> g0, u0, g1, u1;
+    load_wrow<VB, CH>(g0, gate_w + r * K, gate_s + (r >> 7) * SC, lane);
+    load_wrow<VB, CH>(u0, up_w + r * K, up_s + (r >> 7) * SC, lane);
+    load_wrow<VB, CH>(g1, gate_w + (r + 1) * K, gate_s + ((r + 1) >> 7) * SC, lane);
+    load_wrow<VB, CH>(u1, up_w + (r + 1) * K, up_s + ((r + 1) >> 7) * SC, lane);
+    if (!packed) {
+      pack_x_raw<VB, CH, HW>(raw, xs);
+      packed = true;
+    }
+    float tg0 = wave_sum(wrow_partial<VB, CH, HW>(g0, xs)), tu0 = wave_sum(wrow_partial<VB, CH, HW>(u0, xs));
+    float tg1 = wave_sum(wrow_partial<VB, CH, HW>(g1, xs)), tu1 = wave_sum(wrow_partial<VB, CH, HW>(u1, xs));
     if (lane == 0) {
       out[r] = swiglu_mlx(tg0, tu0, a.limit);
       out[r + 1] = swiglu_mlx(tg1, tu1, a.limit);
     }
   }
   if (r < r_end) {
-    WChunk<VB> g0[CH], u0[CH];
-    load_row<VB, CH>(g0, gate_w + r * K, lane);
-    load_row<VB, CH>(u0, up_w + r * K, lane);
-    float tg0 = wave_sum(row_partial<VB, CH, HW>(g0, gate_s + (r >> 7) * SC, xs, lane));
-    float tu0 = wave_sum(row_partial<VB, CH, HW>(u0, up_s + (r >> 7) * SC, xs, lane));
+    WRow<VB, CH> g0, u0;
+    load_wrow<VB, CH>(g0, gate_w + r * K, gate_s + (r >> 7) * SC, lane);
+    load_wrow<VB, CH>(u0, up_w + r * K, up_s + (r >> 7) * SC, lane);
+    if (!packed) pack_x_raw<VB, CH, HW>(raw, xs);
+    float tg0 = wave_sum(wrow_partial<VB, CH, HW>(g0, xs));
+    float tu0 = wave_sum(wrow_partial<VB, CH, HW>(u0, xs));
     if (lane == 0) out[r] = swiglu_mlx(tg0, tu0, a.limit);
   }
 }
@@ -162,17 +165,23 @@ __device__ __forceinline__ void down_rows(const DownArgs& a, const uint8_t* __re
                                           int64_t h_end, int lane) {
   const int64_t K = a.intermediate;
   const int64_t SC = (K + kBlock - 1) / kBlock;
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, raw);
   XSlice<VB, CH, HW> xs;
-  load_x_slice<VB, CH, HW>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, xs);
+  bool packed = false;
   for (int64_t hb = h0; hb < h_end; hb += 8) {
-    WChunk<VB> rowsv[8][CH];
+    WRow<VB, CH> rowsv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (hb + j < h_end) load_row<VB, CH>(rowsv[j], w + (hb + j) * K, lane);
+      if (hb + j < h_end) load_wrow<VB, CH>(rowsv[j], w + (hb + j) * K, s + ((hb + j) >> 7) * SC, lane);
+    if (!packed) {
+      pack_x_raw<VB, CH, HW>(raw, xs);
+      packed = true;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (hb + j < h_end) {
-        const float t = wave_sum(row_partial<VB, CH, HW>(rowsv[j], s + ((hb + j) >> 7) * SC, xs, lane));
+        const float t = wave_sum(wrow_partial<VB, CH, HW>(rowsv[j], xs));
         if (lane == 0) parked_row[hb + j - h0] = bf16_round(t);
       }
     }
@@ -270,19 +279,25 @@ template <int VB, int CH, bool HW>
 __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int64_t n0, int64_t n_end, int lane) {
   const int64_t K = a.K;
   const int64_t SC = (K + kBlock - 1) / kBlock;
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(a.x, lane, raw);
   XSlice<VB, CH, HW> xs;
-  load_x_slice<VB, CH, HW>(a.x, lane, xs);
+  bool packed = false;
   int64_t n = n0;
   for (; n + 3 < n_end; n += 4) {
-    WChunk<VB> w0[CH], w1[CH], w2[CH], w3[CH];
-    load_row<VB, CH>(w0, a.weight + n * K, lane);
-    load_row<VB, CH>(w1, a.weight + (n + 1) * K, lane);
-    load_row<VB, CH>(w2, a.weight + (n + 2) * K, lane);
-    load_row<VB, CH>(w3, a.weight + (n + 3) * K, lane);
-    float t0 = wave_sum(row_partial<VB, CH, HW>(w0, a.scale + (n >> 7) * SC, xs, lane));
-    float t1 = wave_sum(row_partial<VB, CH, HW>(w1, a.scale + ((n + 1) >> 7) * SC, xs, lane));
-    float t2 = wave_sum(row_partial<VB, CH, HW>(w2, a.scale + ((n + 2) >> 7) * SC, xs, lane));
-    float t3 = wave_sum(row_partial<VB, CH, HW>(w3, a.scale + ((n + 3) >> 7) * SC, xs, lane));
+    WRow<VB, CH> w0, w1, w2, w3;
+    load_wrow<VB, CH>(w0, a.weight + n * K, a.scale + (n >> 7) * SC, lane);
+    load_wrow<VB, CH>(w1, a.weight + (n + 1) * K, a.scale + ((n + 1) >> 7) * SC, lane);
+    load_wrow<VB, CH>(w2, a.weight + (n + 2) * K, a.scale + ((n + 2) >> 7) * SC, lane);
+    load_wrow<VB, CH>(w3, a.weight + (n + 3) * K, a.scale + ((n + 3) >> 7) * SC, lane);
+    if (!packed) {
+      pack_x_raw<VB, CH, HW>(raw, xs);
+      packed = true;
+    }
+    float t0 = wave_sum(wrow_partial<VB, CH, HW>(w0, xs));
+    float t1 = wave_sum(wrow_partial<VB, CH, HW>(w1, xs));
+    float t2 = wave_sum(wrow_partial<VB, CH, HW>(w2, xs));
+    float t3 = wave_sum(wrow_partial<VB, CH, HW>(w3, xs));
     if (lane == 0) {
       a.y[n] = f32_to_bf16(t0);
       a.y[n + 1] = f32_to_bf16(t1);
@@ -291,9 +306,13 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int64_t n0, int64_t
     }
   }
   for (; n < n_end; ++n) {
-    WChunk<VB> w0[CH];
-    load_row<VB, CH>(w0, a.weight + n * K, lane);
-    float t0 = wave_sum(row_partial<VB, CH, HW>(w0, a.scale + (n >> 7) * SC, xs, lane));
+    WRow<VB, CH> w0;
+    load_wrow<VB, CH>(w0, a.weight + n * K, a.scale + (n >> 7) * SC, lane);
+    if (!packed) {
+      pack_x_raw<VB, CH, HW>(raw, xs);
+      packed = true;
+    }
+    float t0 = wave_sum(wrow_partial<VB, CH, HW>(w0, xs));
     if (lane == 0) a.y[n] = f32_to_bf16(t0);
   }
 }

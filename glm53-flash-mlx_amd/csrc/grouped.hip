@@ -16,10 +16,11 @@
 //    (< 2.8e-7 * amax of the row block); the MFMA then multiplies these
 //    operands by the raw weight codes with no further rounding of products.
 //  * Grouped GEMM (grouped_fp8.py:30-140): gfx950 v_mfma_f32_16x16x128 with
-//    E4M3 weights fed raw from HBM as the B operand (no decode, no LDS) and
-//    the hi/lo activation rows as the A operand.  One MFMA covers exactly
-//    one 128-deep scale block; its result is scaled by the weight block scale
-//    and the activation scale and accumulated in FP32 registers.
+//    raw E4M3 weight codes as the B operand (no decode) and the hi/lo
+//    activation rows as the A operand, both streamed from HBM into an LDS
+//    ring by direct global->LDS loads.  One MFMA covers exactly one 128-deep
+//    scale block; its result is scaled by the weight block scale and the
+//    activation scale and accumulated in FP32 registers.
 //  * Reductions: grouped FP32 slot-order restore (grouped_fp8.py:273-276) or
 //    the exact Direct ascending-expert BF16 order
 //    (native_indexer_plan.metal:2174-2207), each with the shared-expert add.
@@ -200,18 +201,29 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
 
 // --------------------------------------------------------- grouped GEMM --
 //
-// Workgroup = 4 wavefronts on one descriptor (<= 32 routes of one expert,
-// four groups of 8) and one column tile.  Per 128-deep K block each wave
-// loads its 16 weight rows (32 bytes per lane, straight into the MFMA B
-// registers) and, for each 8-route group, the 16 A rows
-// [hi(t0), lo(t0), hi(t1), lo(t1), ...] so that lane l's four accumulator
-// rows are hi/lo of routes 2(l/16) and 2(l/16)+1 of the group.
+// Workgroup = 4 wavefronts on one work item: one descriptor (<= 64 routes of
+// one expert, 8 groups of 8) times one 128-row weight tile.  Per 128-deep K
+// block (a "stage", 32 KB of LDS):
+//   * B: the tile's 128 weight rows of raw E4M3 codes (16 KB),
+//   * A: per 8-route group, 16 activation rows ordered [hi(r0), lo(r0),
+//     hi(r1), lo(r1), ...], gathered through the sorted token index (2 KB),
+// both brought straight from global memory into LDS by direct loads
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no
+// registers hold data in flight and NS - 1 stages stream while one is
+// multiplied.  A stage's LDS layout for a 16-row operand tile is
+// [half h][k-quarter q][row r] x 16 bytes, holding bytes 32 q + 16 h of row
+// r: the MFMA lane (r = l % 16, q = l / 16) then reads its 32 operand bytes
+// as two conflict-free 16-byte LDS reads at 16 l and 1024 + 16 l.
+// Wavefront w multiplies route groups 2w and 2w + 1 against the 8 weight
+// tiles, one v_mfma_scale_f32_16x16x128_f8f6f4 per (group, tile); lane l's
+// accumulator rows are hi/lo of routes 2 (l / 16) and 2 (l / 16) + 1, and
+// they combine as hi + lo / 16, times the route's activation block scale and
+// the tile's weight block scale (both staged in LDS at the start).
 //
-// mode GEMM_PLAIN : wave w owns output columns [64*tile + 16w, +16).
-// mode GEMM_SWIGLU: wave w owns intermediate columns j in [32*tile + 8w, +8):
-//   B rows 0-7 are gate rows j, rows 8-15 the matching up rows; after the K
-//   loop lane n<8 fetches its up partner from lane n+8 (DPP row_ror:8) and
-//   stores h = SwiGLU(T(gate), T(up)).
+// mode GEMM_PLAIN : the tile is output columns [128 tile, +128).
+// mode GEMM_SWIGLU: the tile is gate rows j in [64 tile, +64) (tiles 0-3)
+//   and the matching up rows (tiles 4-7), so h = SwiGLU(T(gate), T(up))
+//   forms in registers.
 //
 // E4M3 codes 0x7F / 0xFF decode to +-480 in the reference's table but are
 // NaN in the OCP E4M3 format the MFMA consumes.  Checkpoint quantisation
@@ -227,11 +239,149 @@ __device__ __forceinline__ void split_480(uint32_t w, uint32_t& fixed, uint32_t&
   corr = (m * 0x60u) | (w & z);                                // +-32 (code 0x60) where fixed
 }
 
+namespace {
+
+constexpr int kGroups = kGemmTileRows / 8;  // 8-route groups per descriptor: two per wavefront
+static_assert(kGroups == 8, "four wavefronts x two 8-route groups");
+constexpr int kTileRows = 128;                     // weight rows per work item
+constexpr int kOperand = 2048;                     // one 16-row x 128-byte operand tile in LDS
+constexpr int kStageB = (kTileRows / 16) * kOperand;  // 16 KB
+constexpr int kStage = kStageB + kGroups * kOperand;  // + 16 KB of activation rows
+constexpr int kStages = 2;                         // LDS ring depth (two workgroups per CU)
+
+// Direct global -> LDS load of 16 bytes per lane; lane l writes lds_base +
+// 16 l (lds_base wave-uniform).  Written as inline assembly so that the only
+// wait on it is the counted one in stage_barrier: the compiler otherwise
+// drains every direct load before any LDS read it cannot prove disjoint.
+__device__ __forceinline__ void lds_direct16(const uint8_t* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+
+// Waits until at most N of this wavefront's vector-memory loads are in
+// flight and its LDS reads have returned, then joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ i32x8 lds_operand(const uint8_t* p) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 1024);
+  return (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+}  // namespace
+
+template <int MODE, bool FIX, int NGW>
+__device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int64_t ntile, int32_t start, int32_t len,
+                                                  int64_t KB, const uint8_t* gb0, const uint8_t* gb1,
+                                                  const uint8_t* const (&ga)[2], uint8_t* lds, uint32_t lds_addr,
+                                                  const float* lds_sa, const float* lds_sw, int wave, int lane) {
+  constexpr int P = 4 + 2 * NGW;  // direct loads per stage of this wavefront
+  const int kq = lane >> 4;
+  auto issue = [&](int64_t kb, int slot) {
+    const int64_t ko = kb * kBlock;
+    const uint32_t sb = lds_addr + slot * kStage + 2 * wave * kOperand;
+    lds_direct16(gb0 + ko, sb);
+    lds_direct16(gb0 + ko + 16, sb + 1024);
+    lds_direct16(gb1 + ko, sb + kOperand);
+    lds_direct16(gb1 + ko + 16, sb + kOperand + 1024);
+    const uint32_t sa = lds_addr + slot * kStage + kStageB + 2 * wave * kOperand;
+#pragma unroll
+    for (int j = 0; j < NGW; ++j) {
+      lds_direct16(ga[j] + ko, sa + j * kOperand);
+      lds_direct16(ga[j] + ko + 16, sa + j * kOperand + 1024);
+    }
+  };
+
+  float acc[NGW > 0 ? NGW : 1][8][2];
+#pragma unroll
+  for (int j = 0; j < NGW; ++j)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[j][t][0] = acc[j][t][1] = 0.0f;
+
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < KB) issue(s, s);
+  int slot = 0;
+  for (int64_t kb = 0; kb < KB; ++kb) {
+    if (kb + kStages - 2 < KB) stage_barrier<P * (kStages - 2)>();
+    else stage_barrier<0>();
+    if (kb + kStages - 1 < KB) issue(kb + kStages - 1, slot == 0 ? kStages - 1 : slot - 1);
+    if (NGW > 0) {
+      const uint8_t* st = lds + slot * kStage;
+      i32x8 av[NGW > 0 ? NGW : 1];
+      float sa[NGW > 0 ? NGW : 1][2];
+#pragma unroll
+      for (int j = 0; j < NGW; ++j) {
+        av[j] = lds_operand(st + kStageB + (2 * wave + j) * kOperand + 16 * lane);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) sa[j][h] = lds_sa[((2 * wave + j) * 8 + 2 * kq + h) * KB + kb];
+      }
+      const float sw_lo = lds_sw[kb];
+      const float sw_hi = MODE == GEMM_SWIGLU ? lds_sw[KB + kb] : sw_lo;
+      i32x8 bt[8];  // all eight weight tiles read ahead: one LDS wait per stage
+#pragma unroll
+      for (int t = 0; t < 8; ++t) bt[t] = lds_operand(st + t * kOperand + 16 * lane);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        i32x8 bq = bt[t];
+        i32x8 bc = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+        if (FIX) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            uint32_t f, c;
+            split_480(static_cast<uint32_t>(bq[i]), f, c);
+            bq[i] = static_cast<int>(f);
+            bc[i] = static_cast<int>(c);
+          }
+        }
+        const float sw = t < 4 ? sw_lo : sw_hi;
+#pragma unroll
+        for (int j = 0; j < NGW; ++j) {
+          f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bq, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
+                                                                      0, 127, 0, 127);
+          if (FIX) c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bc, c, 0, 0, 0, 127, 0, 127);
+          // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
+          acc[j][t][0] = fmaf(fmaf(c[1], 0.0625f, c[0]), sa[j][0] * sw, acc[j][t][0]);
+          acc[j][t][1] = fmaf(fmaf(c[3], 0.0625f, c[2]), sa[j][1] * sw, acc[j][t][1]);
+        }
+      }
+    }
+    slot = slot == kStages - 1 ? 0 : slot + 1;
+  }
+
+  // epilogue: lane holds columns 16 t + l % 16 of routes 8 g + 2 kq + h
+  const int n16 = lane & 15;
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int g = 2 * wave + j;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = g * 8 + 2 * kq + h;
+      if (r >= len) continue;
+      uint16_t* orow = a.out + (static_cast<int64_t>(start) + r) * a.out_row_stride;
+      if (MODE == GEMM_PLAIN) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int64_t c = ntile * kTileRows + t * 16 + n16;
+          if (c < a.N) orow[c] = f32_to_bf16(acc[j][t][h]);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int64_t c = ntile * (kTileRows / 2) + t * 16 + n16;
+          if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][h], acc[j][t + 4][h], a.limit);
+        }
+      }
+    }
+  }
+}
+
 template <int MODE, bool FIX>
-__device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a) {
+__device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int64_t ntile, int64_t d, uint8_t* lds) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t d = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int32_t expert, start, len;
   if (a.tile_expert != nullptr) {
     expert = a.tile_expert[d];
@@ -239,138 +389,90 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a) {
     len = a.tile_len[d];
     if (start >= a.routes || len <= 0) return;
     if (expert < 0 || expert >= a.experts) return;
+    if (len > kGemmTileRows) len = kGemmTileRows;
+    if (start + len > a.routes) len = static_cast<int32_t>(a.routes - start);
   } else {
     expert = 0;
-    start = static_cast<int32_t>(d * kGroupedTileRows);
-    len = static_cast<int32_t>(a.routes - start < kGroupedTileRows ? a.routes - start : kGroupedTileRows);
+    start = static_cast<int32_t>(d * kGemmTileRows);
+    len = static_cast<int32_t>(a.routes - start < kGemmTileRows ? a.routes - start : kGemmTileRows);
     if (len <= 0) return;
   }
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
-  const int n16 = lane & 15;
-  const int kq = lane >> 4;  // which 32-byte quarter of the 128-deep block
-
-  // B row owned by this lane and the output column it lands on
-  int64_t brow;
-  int64_t col;
-  const uint8_t* wbase;
-  const float* sbase;
-  if (MODE == GEMM_PLAIN) {
-    col = static_cast<int64_t>(blockIdx.x) * 64 + wave * 16 + n16;
-    if (static_cast<int64_t>(blockIdx.x) * 64 + wave * 16 >= a.N) return;
-    brow = col;
-    wbase = a.weight + static_cast<int64_t>(expert) * a.w_expert_stride;
-    sbase = a.scale + static_cast<int64_t>(expert) * a.s_expert_stride;
-  } else {
-    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * 32 + wave * 8;
-    if (j0 >= a.N) return;
-    col = j0 + (n16 & 7);
-    brow = col;
-    if (n16 < 8) {
-      wbase = a.weight + static_cast<int64_t>(expert) * a.w_expert_stride;
-      sbase = a.scale + static_cast<int64_t>(expert) * a.s_expert_stride;
-    } else {
-      wbase = a.weight_up + static_cast<int64_t>(expert) * a.w_expert_stride;
-      sbase = a.scale_up + static_cast<int64_t>(expert) * a.s_expert_stride;
-    }
-  }
-  const bool col_ok = col < a.N;
-  const uint8_t* bptr = wbase + (col_ok ? brow : 0) * K + kq * 32;
-  const float* srow = sbase + ((col_ok ? brow : 0) >> 7) * a.s_cols;
-
-  // A rows: lane's A row rho = n16 -> route 2*(rho/4) + ((rho>>1)&1) of each
-  // 8-route group, hi if rho even else lo.
-  const int tok_in_group = 2 * (n16 >> 2) + ((n16 >> 1) & 1);
-  const uint8_t* aplane = (n16 & 1) ? a.a_lo : a.a_hi;
+  const int kq = lane >> 4;
   const int groups = (len + 7) >> 3;
-  int64_t arow[kGroupedTileRows / 8];
-  bool aok[kGroupedTileRows / 8];
-#pragma unroll
-  for (int g = 0; g < kGroupedTileRows / 8; ++g) {
-    const int tt = g * 8 + tok_in_group;
-    aok[g] = g < groups && tt < len;
-    const int64_t route = start + (aok[g] ? tt : 0);
-    arow[g] = a.a_row_index != nullptr ? a.a_row_index[route] : route;
-  }
-  // activation rows of the two routes whose hi/lo rows land in this lane's
-  // accumulator (routes 2kq and 2kq+1 of each group)
-  int64_t srow0[kGroupedTileRows / 8], srow1[kGroupedTileRows / 8];
-#pragma unroll
-  for (int g = 0; g < kGroupedTileRows / 8; ++g) {
-    const int t0 = g * 8 + 2 * kq, t1 = t0 + 1;
-    const int64_t r0 = start + (t0 < len ? t0 : 0);
-    const int64_t r1 = start + (t1 < len ? t1 : 0);
-    srow0[g] = (a.a_row_index != nullptr ? a.a_row_index[r0] : r0) * KB;
-    srow1[g] = (a.a_row_index != nullptr ? a.a_row_index[r1] : r1) * KB;
-  }
+  float* lds_sa = reinterpret_cast<float*>(lds + kStages * kStage);  // [64 routes][KB]
+  float* lds_sw = lds_sa + kGemmTileRows * KB;                        // [2][KB]
 
-  float acc[kGroupedTileRows / 8][2];
-#pragma unroll
-  for (int g = 0; g < kGroupedTileRows / 8; ++g) acc[g][0] = acc[g][1] = 0.0f;
+  // ---- block scales of the work item: activations of every route, weights
+  // of the tile (one 128-row scale block: PLAIN tiles are 128-aligned, SWIGLU
+  // tiles 64-aligned within one block)
+  auto token_of = [&](int r) -> int64_t {
+    const int64_t route = start + (r < len ? r : len - 1);
+    return a.a_row_index != nullptr ? a.a_row_index[route] : route;
+  };
+  for (int64_t i = threadIdx.x; i < kGemmTileRows * KB; i += 256) {
+    const int r = static_cast<int>(i / KB);
+    lds_sa[i] = a.a_scale[token_of(r) * KB + (i - r * KB)];
+  }
+  const int64_t srow = MODE == GEMM_PLAIN ? ntile : (ntile >> 1);
+  const int64_t soff = static_cast<int64_t>(expert) * a.s_expert_stride + srow * a.s_cols;
+  for (int64_t i = threadIdx.x; i < (MODE == GEMM_SWIGLU ? 2 : 1) * KB; i += 256)
+    lds_sw[i] = i < KB ? a.scale[soff + i] : a.scale_up[soff + i - KB];
+  __syncthreads();
 
-  for (int64_t kb = 0; kb < KB; ++kb) {
-    i32x8 b;
-    if (col_ok) {
-      u32x4 b0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bptr + kb * kBlock));
-      u32x4 b1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bptr + kb * kBlock + 16));
-      b = (i32x8){(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+  // ---- per-lane global sources of the direct loads
+  auto b_row = [&](int t) -> const uint8_t* {
+    int64_t row;
+    const uint8_t* w;
+    if (MODE == GEMM_PLAIN) {
+      row = ntile * kTileRows + t * 16 + (lane & 15);
+      w = a.weight;
     } else {
-      b = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+      row = ntile * (kTileRows / 2) + (t & 3) * 16 + (lane & 15);
+      w = t < 4 ? a.weight : a.weight_up;
     }
-    i32x8 bc = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
-    if (FIX) {
+    if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
+    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + kq * 32;
+  };
+  const uint8_t* gb0 = b_row(2 * wave);
+  const uint8_t* gb1 = b_row(2 * wave + 1);
+  const uint8_t* ga[2];
+  {
+    const int rho = lane & 15;
+    const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
+    const uint8_t* plane = (rho & 1) ? a.a_lo : a.a_hi;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        uint32_t f, c;
-        split_480(static_cast<uint32_t>(b[i]), f, c);
-        b[i] = static_cast<int>(f);
-        bc[i] = static_cast<int>(c);
-      }
-    }
-    const float sw = col_ok ? srow[kb] : 0.0f;
-#pragma unroll
-    for (int g = 0; g < kGroupedTileRows / 8; ++g) {
-      if (g >= groups) break;  // uniform across the wave
-      i32x8 av = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (aok[g]) {
-        const uint8_t* p = aplane + arow[g] * K + kb * kBlock + kq * 32;
-        u32x4 a0 = *reinterpret_cast<const u32x4*>(p);
-        u32x4 a1 = *reinterpret_cast<const u32x4*>(p + 16);
-        av = (i32x8){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-      }
-      f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
-                                                                  127, 0, 127);
-      if (FIX) c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bc, c, 0, 0, 0, 127, 0, 127);
-      // rows of c: hi(t0), lo(t0), hi(t1), lo(t1) for t0 = 2kq, t1 = 2kq+1
-      const float sa0 = a.a_scale[srow0[g] + kb];
-      const float sa1 = a.a_scale[srow1[g] + kb];
-      acc[g][0] = fmaf(fmaf(c[1], 0.0625f, c[0]), sa0 * sw, acc[g][0]);
-      acc[g][1] = fmaf(fmaf(c[3], 0.0625f, c[2]), sa1 * sw, acc[g][1]);
-    }
+    for (int j = 0; j < 2; ++j) ga[j] = plane + token_of((2 * wave + j) * 8 + rt) * K + kq * 32;
   }
-
-#pragma unroll
-  for (int g = 0; g < kGroupedTileRows / 8; ++g) {
-    if (g >= groups) break;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int tt = g * 8 + 2 * kq + h;
-      if (MODE == GEMM_PLAIN) {
-        if (col_ok && tt < len) a.out[(start + tt) * a.out_row_stride + col] = f32_to_bf16(acc[g][h]);
-      } else {
-        // row_ror:8 within each 16-lane row: lane n gets lane (n+8)&15
-        float up = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[g][h]), 0x128, 0xF, 0xF, true));
-        if (n16 < 8 && col_ok && tt < len)
-          a.out[(start + tt) * a.out_row_stride + col] = swiglu_mlx(acc[g][h], up, a.limit);
-      }
-    }
-  }
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const int ngw = (2 * wave < groups) + (2 * wave + 1 < groups);  // wave-uniform
+  if (ngw == 2)
+    grouped_gemm_loop<MODE, FIX, 2>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
+  else if (ngw == 1)
+    grouped_gemm_loop<MODE, FIX, 1>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
+  else
+    grouped_gemm_loop<MODE, FIX, 0>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
 }
 
+size_t grouped_gemm_lds_bytes(int64_t K) {
+  return static_cast<size_t>(kStages) * kStage + sizeof(float) * (kGemmTileRows + 2) * static_cast<size_t>(K / kBlock);
+}
+
+// Work items (column tile, descriptor) are dealt to the XCDs in contiguous
+// runs: workgroup i runs on XCD i % 8, and item w = (i % 8) * ceil(W / 8) +
+// i / 8 keeps neighbouring items (same tile, consecutive descriptors of one
+// expert) on one XCD and its L2.
 template <int MODE>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
-  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true>(a);
-  else grouped_gemm_body<MODE, false>(a);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+  const int64_t items = a.n_tiles * a.descriptors;
+  const int64_t per_xcd = (items + 7) / 8;
+  const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (w >= items) return;
+  const int64_t ntile = w / a.descriptors, d = w % a.descriptors;
+  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true>(a, ntile, d, lds_dyn);
+  else grouped_gemm_body<MODE, false>(a, ntile, d, lds_dyn);
 }
 
 // Sets *flag (pre-cleared by clear_flag_kernel) when any byte of codes is
@@ -472,13 +574,17 @@ hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st) {
 
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st) {
   if (descriptors == 0) return hipSuccess;
-  if (mode == GEMM_PLAIN) {
-    dim3 grid(static_cast<unsigned>((a.N + 63) / 64), static_cast<unsigned>(descriptors));
-    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_PLAIN>, grid, dim3(256), 0, st, a);
-  } else {
-    dim3 grid(static_cast<unsigned>((a.N + 31) / 32), static_cast<unsigned>(descriptors));
-    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_SWIGLU>, grid, dim3(256), 0, st, a);
-  }
+  GroupedGemmArgs g = a;
+  g.n_tiles = mode == GEMM_PLAIN ? (a.N + 127) / 128 : (a.N + 63) / 64;
+  g.descriptors = descriptors;
+  const int64_t items = g.n_tiles * descriptors;
+  const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
+  const size_t lds = grouped_gemm_lds_bytes(a.K);
+  if (a.K % kBlock != 0 || a.K <= 0 || lds > 160 * 1024) return hipErrorInvalidValue;
+  if (mode == GEMM_PLAIN)
+    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_PLAIN>, dim3(grid), dim3(256), lds, st, g);
+  else
+    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_SWIGLU>, dim3(grid), dim3(256), lds, st, g);
   return hipGetLastError();
 }
 

@@ -165,19 +165,25 @@ __device__ __forceinline__ void gate_up_pairs(const LayerArgs& a, const uint8_t*
                                               uint32_t* done, int64_t r0, int64_t r_end, int lane, uint32_t epoch) {
   const int64_t K = a.hidden;
   const int64_t SC = K / kBlock;
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(a.x, lane, raw);
   XSlice<VB, CH, HW> xs;
-  load_x_slice<VB, CH, HW>(a.x, lane, xs);
+  bool packed = false;
 #pragma unroll 1
   for (int64_t r = r0; r < r_end; r += 2) {
-    WChunk<VB> g0[CH], u0[CH], g1[CH], u1[CH];
-    load_row<VB, CH>(g0, gate_w + r * K, lane);
-    load_row<VB, CH>(u0, up_w + r * K, lane);
-    load_row<VB, CH>(g1, gate_w + (r + 1) * K, lane);
-    load_row<VB, CH>(u1, up_w + (r + 1) * K, lane);
-    const float pg0 = row_partial<VB, CH, HW>(g0, gate_s + (r >> 7) * SC, xs, lane);
-    const float pu0 = row_partial<VB, CH, HW>(u0, up_s + (r >> 7) * SC, xs, lane);
-    const float pg1 = row_partial<VB, CH, HW>(g1, gate_s + ((r + 1) >> 7) * SC, xs, lane);
-    const float pu1 = row_partial<VB, CH, HW>(u1, up_s + ((r + 1) >> 7) * SC, xs, lane);
+    WRow<VB, CH> g0, u0, g1, u1;
+    load_wrow<VB, CH>(g0, gate_w + r * K, gate_s + (r >> 7) * SC, lane);
+    load_wrow<VB, CH>(u0, up_w + r * K, up_s + (r >> 7) * SC, lane);
+    load_wrow<VB, CH>(g1, gate_w + (r + 1) * K, gate_s + ((r + 1) >> 7) * SC, lane);
+    load_wrow<VB, CH>(u1, up_w + (r + 1) * K, up_s + ((r + 1) >> 7) * SC, lane);
+    if (!packed) {
+      pack_x_raw<VB, CH, HW>(raw, xs);
+      packed = true;
+    }
+    const float pg0 = wrow_partial<VB, CH, HW>(g0, xs);
+    const float pu0 = wrow_partial<VB, CH, HW>(u0, xs);
+    const float pg1 = wrow_partial<VB, CH, HW>(g1, xs);
+    const float pu1 = wrow_partial<VB, CH, HW>(u1, xs);
     const float tg0 = wave_sum(pg0), tu0 = wave_sum(pu0);
     const float tg1 = wave_sum(pg1), tu1 = wave_sum(pu1);
     if (lane == 0) {
@@ -207,10 +213,10 @@ __device__ __forceinline__ void down_batch_rows(const LayerArgs& a, const uint8_
   bool have_x = false;
 #pragma unroll 1
   for (int64_t hb = h0; hb < h_end; hb += 8) {
-    WChunk<VB> rows[8][CH];
+    WRow<VB, CH> rows[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (hb + j < h_end) load_row<VB, CH>(rows[j], w + (hb + j) * K, lane);
+      if (hb + j < h_end) load_wrow<VB, CH>(rows[j], w + (hb + j) * K, s + ((hb + j) >> 7) * SC, lane);
     if (!have_x) {
       load_tagged_slice<VB, CH, HW>(act, act_done, act_want, lane, epoch, xs, a.error_flag);
       have_x = true;
@@ -218,9 +224,7 @@ __device__ __forceinline__ void down_batch_rows(const LayerArgs& a, const uint8_
     float t[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      t[j] = (hb + j < h_end) ? bf16_round(wave_sum(row_partial<VB, CH, HW>(rows[j], s + ((hb + j) >> 7) * SC, xs,
-                                                                              lane)))
-                              : 0.0f;
+      t[j] = (hb + j < h_end) ? bf16_round(wave_sum(wrow_partial<VB, CH, HW>(rows[j], xs))) : 0.0f;
     if (lane == 0) {
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {

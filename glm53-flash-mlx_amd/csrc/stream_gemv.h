@@ -132,19 +132,6 @@ __device__ __forceinline__ float chunk_dot(const WChunk<VB>& w, const XSlice<VB,
   return acc;
 }
 
-// Lane partial of one row whose block-scale row is `srow` (SC scales).
-template <int VB, int CH, bool HW>
-__device__ __forceinline__ float row_partial(const WChunk<VB> (&w)[CH], const float* __restrict__ srow,
-                                             const XSlice<VB, CH, HW>& xs, int lane) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    float s = srow[(VB * lane + 64 * VB * c) >> 7];
-    acc += chunk_dot<VB, CH, HW>(w[c], xs, c) * s;
-  }
-  return acc * xs.factor;
-}
-
 // One weight row as a lane sees it: its CH chunks and the block scale of
 // each chunk.  The scales are loaded with the chunks, in the same batch of
 // vector loads: loaded later, next to the arithmetic, they would make the
@@ -176,12 +163,6 @@ __device__ __forceinline__ float wrow_partial(const WRow<VB, CH>& r, const XSlic
 // The register decode is usable unless a (device) scan flagged 0x7F / 0xFF
 // codes; a null flag means "not scanned" and keeps the exact SWAR decode.
 __device__ __forceinline__ bool hw_decode_ok(const int32_t* flag) { return flag != nullptr && *flag == 0; }
-
-template <int VB, int CH>
-__device__ __forceinline__ void load_row(WChunk<VB> (&w)[CH], const uint8_t* __restrict__ row, int lane) {
-#pragma unroll
-  for (int c = 0; c < CH; ++c) w[c].load(row + VB * lane + 64 * VB * c);
-}
 
 __device__ __forceinline__ bool bad_expert(int32_t e, int64_t experts) {
   return e < 0 || static_cast<int64_t>(e) >= experts;
