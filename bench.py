@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--cpu-steps", type=int, default=24, help="tokens through all layers for the CPU oracle timing")
     p.add_argument("--parity-layers", type=int, default=3)
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="one synthetic layer, configs 4 and 5 prefill only (for profiling the grouped GEMM)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-single", action="store_true", help="skip timing the one-launch decode form")
     p.add_argument("--json-out", type=str, default="")
@@ -109,7 +111,7 @@ def main():
     cfg = syn.layer_config()
     H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
     Is = I * cfg.n_shared_experts
-    L = args.layers
+    L = 1 if args.prefill_only else args.layers
 
     # ------------------------------------------------------------ weights ---
     t0 = time.perf_counter()
@@ -123,6 +125,10 @@ def main():
     gen_s = time.perf_counter() - t0
     resident = sum(l.bank.nbytes for l in layers) + L * (3 * Is * H + E * H * 4)
     log(f"generated {L} layers, {resident / 1e9:.1f} GB resident, in {gen_s:.1f} s")
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn)}))
+        return
 
     # ------------------------------------------------------- decode graph ---
     x = torch.empty(H, dtype=torch.bfloat16, device=dev)
@@ -497,7 +503,7 @@ def summarize_traffic(fetch_csv, write_csv):
                 continue
             name = row["Kernel_Name"]
             rows.setdefault(name, []).append(float(row["Counter_Value"]))
-        return {n: (statistics.mean(v), len(v)) for n, v in rows.items()}
+        return {n: (statistics.mean(v), len(v), sum(v)) for n, v in rows.items()}
 
     fetch, write = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
 
@@ -505,28 +511,31 @@ def summarize_traffic(fetch_csv, write_csv):
         hits = [n for n in table if key in n]
         return hits[0] if hits else None
 
+    # totals over the calibration dispatches: the runtime may split one copy
+    # into several dispatches, so calibrate on sums (4 probes, 4 copies)
     probe_bytes = 113309696 // 256 * 256
     copy_bytes = 64 << 20
     probe_k = pick(fetch, "probe_read_kernel")
     copy_kw = pick(write, "copyBuffer") or pick(write, "elementwise_kernel")
-    fetch_scale = probe_bytes / (fetch[probe_k][0] * 1024.0)
-    write_scale = copy_bytes / (write[copy_kw][0] * 1024.0)
+    fetch_scale = 4 * probe_bytes / (fetch[probe_k][2] * 1024.0)
+    write_scale = 4 * copy_bytes / (write[copy_kw][2] * 1024.0)
     keys = ("step_router_shared_kernel", "step_gate_up_kernel", "step_down_kernel", "decode_layer_kernel",
             "probe_read_kernel")
     print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (calibrated) | written B (calibrated) |")
     print("|---|---|---|---|---|---|")
     out = {}
     for name in sorted(set(fetch) | set(write)):
-        f = fetch.get(name, (float("nan"), 0))
-        w = write.get(name, (float("nan"), 0))
+        f = fetch.get(name, (float("nan"), 0, 0.0))
+        w = write.get(name, (float("nan"), 0, 0.0))
         fb, wb = f[0] * 1024.0 * fetch_scale, w[0] * 1024.0 * write_scale
         print(f"| {name[:90]} | {f[1]} | {f[0]:.1f} | {w[0]:.1f} | {fb:.0f} | {wb:.0f} |")
         for key in keys:
             if key in name:
                 out[key] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb)}
     print()
-    print(f"calibration: read probe {probe_bytes} B -> FETCH_SIZE x {fetch_scale:.4f}; "
-          f"{copy_bytes} B device copy ({copy_kw[:60]}) -> WRITE_SIZE x {write_scale:.4f}")
+    print(f"calibration: 4 read probes of {probe_bytes} B -> FETCH_SIZE x {fetch_scale:.4f}; "
+          f"4 device copies of {copy_bytes} B ({copy_kw[:60]}, {write[copy_kw][1]} dispatches) "
+          f"-> WRITE_SIZE x {write_scale:.4f}")
     print()
     print("traffic_json: " + json.dumps({"fetch_scale": fetch_scale, "write_scale": write_scale, "kernels": out}))
 
