@@ -1187,7 +1187,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->max_tokens = max_tokens;
   p->limit = swiglu_limit;
   const int64_t T = max_tokens, R = T * top_k, Ism = std::max<int64_t>(shared_intermediate, 128);
-  p->capacity_max = cdiv(R, kGemmTileRows) + experts;
+  p->capacity_max = cdiv(R, kGemmMinTileRows) + experts;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -1316,9 +1316,12 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   }
   // 1. activations -> exact hi/lo E4M3 split
   HIP_TRY(split(x, T, H, p->xq, st), "split x");
-  // 2. expert-sorted route plan
-  const int64_t cap = cdiv(R, kGemmTileRows) + E;
-  if ((rc = route_plan_impl(ids, sc, R, k, E, kGemmTileRows, p->sorted_route, p->inverse, p->sorted_expert,
+  // 2. expert-sorted route plan: 64-route descriptors when experts average
+  // at least 32 routes (fewer re-reads of each weight tile), 32-route ones
+  // (a deeper load ring per workgroup) otherwise
+  const int tile = R >= 32 * E ? kGemmTileRows : kGemmMinTileRows;
+  const int64_t cap = cdiv(R, tile) + E;
+  if ((rc = route_plan_impl(ids, sc, R, k, E, tile, p->sorted_route, p->inverse, p->sorted_expert,
                             p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,
                             p->tile_start, p->tile_len, cap, p->status, p->plan_ws, st)))
     return rc;
@@ -1333,6 +1336,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   g.tile_expert = p->tile_expert;
   g.tile_start = p->tile_start;
   g.tile_len = p->tile_len;
+  g.tile_rows = tile;
   g.experts = E;
   g.weight = bank->gate_up_weight;
   g.weight_up = bank->gate_up_weight + I * H;
@@ -1358,6 +1362,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   d.tile_expert = p->tile_expert;
   d.tile_start = p->tile_start;
   d.tile_len = p->tile_len;
+  d.tile_rows = tile;
   d.experts = E;
   d.weight = bank->down_weight;
   d.w_expert_stride = H * I;
@@ -1389,7 +1394,9 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     sg.out = p->hs;
     sg.out_row_stride = Is;
     sg.fixup = shared_gu_flag;
-    HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, kGemmTileRows), st), "shared gate/up launch");
+    const int stile = T >= 16 * kGemmTileRows ? kGemmTileRows : kGemmMinTileRows;
+    sg.tile_rows = stile;
+    HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, stile), st), "shared gate/up launch");
     HIP_TRY(split(p->hs, T, Is, p->sq, st), "split shared hidden");
     GroupedGemmArgs sd{};
     sd.a_hi = p->sq.hi;
@@ -1405,7 +1412,8 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     sd.out = p->shared_out;
     sd.out_row_stride = H;
     sd.fixup = shared_down_flag;
-    HIP_TRY(launch_grouped_gemm(sd, GEMM_PLAIN, cdiv(T, kGemmTileRows), st), "shared down launch");
+    sd.tile_rows = stile;
+    HIP_TRY(launch_grouped_gemm(sd, GEMM_PLAIN, cdiv(T, stile), st), "shared down launch");
     shared_add = p->shared_out;
   }
   // 7. combine

@@ -8,7 +8,8 @@ namespace glm53 {
 
 constexpr int kPlanMaxExperts = 1024;
 constexpr int kGroupedTileRows = 32;   // routes per descriptor of the reference (grouped_fp8.py:20)
-constexpr int kGemmTileRows = 64;      // routes per descriptor of the MFMA grouped GEMM (<= 64 accepted)
+constexpr int kGemmTileRows = 64;      // routes per descriptor of the MFMA grouped GEMM (many routes per expert)
+constexpr int kGemmMinTileRows = 32;   // its narrow form (one group per wavefront, deeper ring)
 constexpr int kMaxReduceTopK = 16;
 enum { GEMM_PLAIN = 0, GEMM_SWIGLU = 1 };
 
@@ -68,6 +69,7 @@ struct GroupedGemmArgs {
   uint16_t* out;              // [routes, out_row_stride] bf16
   int64_t out_row_stride;
   const int32_t* fixup;       // device flag: weights hold 0x7F/0xFF codes (or null)
+  int tile_rows;                 // routes per descriptor: kGemmMinTileRows, or kGemmTileRows (also 0)
   int64_t n_tiles, descriptors;  // set by the launcher
 };
 

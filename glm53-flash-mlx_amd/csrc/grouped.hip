@@ -201,24 +201,26 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
 
 // --------------------------------------------------------- grouped GEMM --
 //
-// Workgroup = 4 wavefronts on one work item: one descriptor (<= 64 routes of
-// one expert, 8 groups of 8) times one 128-row weight tile.  Per 128-deep K
-// block (a "stage", 32 KB of LDS):
+// Workgroup = 4 wavefronts on one work item: one descriptor (32 GPW routes
+// of one expert, 4 GPW groups of 8) times one 128-row weight tile.  Per
+// 128-deep K block (a "stage"):
 //   * B: the tile's 128 weight rows of raw E4M3 codes (16 KB),
 //   * A: per 8-route group, 16 activation rows ordered [hi(r0), lo(r0),
 //     hi(r1), lo(r1), ...], gathered through the sorted token index (2 KB),
-// both brought straight from global memory into LDS by direct loads
+// both brought straight from global memory into an LDS ring by direct loads
 // (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no
-// registers hold data in flight and NS - 1 stages stream while one is
-// multiplied.  A stage's LDS layout for a 16-row operand tile is
+// registers hold data in flight and the ring's other stages stream while
+// one is multiplied.  A stage's LDS layout for a 16-row operand tile is
 // [half h][k-quarter q][row r] x 16 bytes, holding bytes 32 q + 16 h of row
 // r: the MFMA lane (r = l % 16, q = l / 16) then reads its 32 operand bytes
 // as two conflict-free 16-byte LDS reads at 16 l and 1024 + 16 l.
-// Wavefront w multiplies route groups 2w and 2w + 1 against the 8 weight
-// tiles, one v_mfma_scale_f32_16x16x128_f8f6f4 per (group, tile); lane l's
-// accumulator rows are hi/lo of routes 2 (l / 16) and 2 (l / 16) + 1, and
-// they combine as hi + lo / 16, times the route's activation block scale and
-// the tile's weight block scale (both staged in LDS at the start).
+// Wavefront w multiplies route groups GPW w .. GPW w + GPW - 1 against the 8
+// weight tiles, one v_mfma_scale_f32_16x16x128_f8f6f4 per (group, tile);
+// lane l's accumulator rows are hi/lo of routes 2 (l / 16) and 2 (l / 16) +
+// 1, and they combine as hi + lo / 16, times the route's activation block
+// scale and the tile's weight block scale (both staged in LDS at the start).
+// Two shapes: GPW = 2 (64-route descriptors, 2-stage ring) for many routes
+// per expert, GPW = 1 (32 routes, 3-stage ring) otherwise.
 //
 // mode GEMM_PLAIN : the tile is output columns [128 tile, +128).
 // mode GEMM_SWIGLU: the tile is gate rows j in [64 tile, +64) (tiles 0-3)
@@ -241,13 +243,23 @@ __device__ __forceinline__ void split_480(uint32_t w, uint32_t& fixed, uint32_t&
 
 namespace {
 
-constexpr int kGroups = kGemmTileRows / 8;  // 8-route groups per descriptor: two per wavefront
-static_assert(kGroups == 8, "four wavefronts x two 8-route groups");
 constexpr int kTileRows = 128;                     // weight rows per work item
 constexpr int kOperand = 2048;                     // one 16-row x 128-byte operand tile in LDS
 constexpr int kStageB = (kTileRows / 16) * kOperand;  // 16 KB
-constexpr int kStage = kStageB + kGroups * kOperand;  // + 16 KB of activation rows
-constexpr int kStages = 2;                         // LDS ring depth (two workgroups per CU)
+// LDS ring depth of each shape: 32-route descriptors keep 2 stages in
+// flight in 72 KB, 64-route descriptors 1 stage in 64 KB (two workgroups
+// per CU either way).
+template <int GPW>
+constexpr int ring_stages() {
+  return GPW == 1 ? 3 : 2;
+}
+// GPW 8-route groups per wavefront: descriptors of 32 GPW routes, 4 GPW
+// groups of activation rows per stage
+template <int GPW>
+constexpr int stage_bytes() {
+  return kStageB + 4 * GPW * kOperand;
+}
+static_assert(kGemmTileRows == 64 && kGemmMinTileRows == 32, "descriptor sizes of the two GEMM shapes");
 
 // Direct global -> LDS load of 16 bytes per lane; lane l writes lds_base +
 // 16 l (lds_base wave-uniform).  Written as inline assembly so that the only
@@ -272,11 +284,12 @@ __device__ __forceinline__ i32x8 lds_operand(const uint8_t* p) {
 
 }  // namespace
 
-template <int MODE, bool FIX, int NGW>
+template <int MODE, bool FIX, int GPW, int NGW>
 __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int64_t ntile, int32_t start, int32_t len,
                                                   int64_t KB, const uint8_t* gb0, const uint8_t* gb1,
-                                                  const uint8_t* const (&ga)[2], uint8_t* lds, uint32_t lds_addr,
+                                                  const uint8_t* const (&ga)[GPW], uint8_t* lds, uint32_t lds_addr,
                                                   const float* lds_sa, const float* lds_sw, int wave, int lane) {
+  constexpr int kStage = stage_bytes<GPW>();
   constexpr int P = 4 + 2 * NGW;  // direct loads per stage of this wavefront
   const int kq = lane >> 4;
   auto issue = [&](int64_t kb, int slot) {
@@ -286,7 +299,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
     lds_direct16(gb0 + ko + 16, sb + 1024);
     lds_direct16(gb1 + ko, sb + kOperand);
     lds_direct16(gb1 + ko + 16, sb + kOperand + 1024);
-    const uint32_t sa = lds_addr + slot * kStage + kStageB + 2 * wave * kOperand;
+    const uint32_t sa = lds_addr + slot * kStage + kStageB + GPW * wave * kOperand;
 #pragma unroll
     for (int j = 0; j < NGW; ++j) {
       lds_direct16(ga[j] + ko, sa + j * kOperand);
@@ -300,6 +313,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[j][t][0] = acc[j][t][1] = 0.0f;
 
+  constexpr int kStages = ring_stages<GPW>();
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s)
     if (s < KB) issue(s, s);
@@ -314,9 +328,9 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
       float sa[NGW > 0 ? NGW : 1][2];
 #pragma unroll
       for (int j = 0; j < NGW; ++j) {
-        av[j] = lds_operand(st + kStageB + (2 * wave + j) * kOperand + 16 * lane);
+        av[j] = lds_operand(st + kStageB + (GPW * wave + j) * kOperand + 16 * lane);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) sa[j][h] = lds_sa[((2 * wave + j) * 8 + 2 * kq + h) * KB + kb];
+        for (int h = 0; h < 2; ++h) sa[j][h] = lds_sa[((GPW * wave + j) * 8 + 2 * kq + h) * KB + kb];
       }
       const float sw_lo = lds_sw[kb];
       const float sw_hi = MODE == GEMM_SWIGLU ? lds_sw[KB + kb] : sw_lo;
@@ -355,7 +369,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
   const int n16 = lane & 15;
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
-    const int g = 2 * wave + j;
+    const int g = GPW * wave + j;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int r = g * 8 + 2 * kq + h;
@@ -378,8 +392,10 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
   }
 }
 
-template <int MODE, bool FIX>
+template <int MODE, bool FIX, int GPW>
 __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int64_t ntile, int64_t d, uint8_t* lds) {
+  constexpr int kRoutes = 32 * GPW;  // routes per descriptor
+  constexpr int kStage = stage_bytes<GPW>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int32_t expert, start, len;
@@ -389,20 +405,20 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
     len = a.tile_len[d];
     if (start >= a.routes || len <= 0) return;
     if (expert < 0 || expert >= a.experts) return;
-    if (len > kGemmTileRows) len = kGemmTileRows;
+    if (len > kRoutes) len = kRoutes;
     if (start + len > a.routes) len = static_cast<int32_t>(a.routes - start);
   } else {
     expert = 0;
-    start = static_cast<int32_t>(d * kGemmTileRows);
-    len = static_cast<int32_t>(a.routes - start < kGemmTileRows ? a.routes - start : kGemmTileRows);
+    start = static_cast<int32_t>(d * kRoutes);
+    len = static_cast<int32_t>(a.routes - start < kRoutes ? a.routes - start : kRoutes);
     if (len <= 0) return;
   }
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
   const int kq = lane >> 4;
   const int groups = (len + 7) >> 3;
-  float* lds_sa = reinterpret_cast<float*>(lds + kStages * kStage);  // [64 routes][KB]
-  float* lds_sw = lds_sa + kGemmTileRows * KB;                        // [2][KB]
+  float* lds_sa = reinterpret_cast<float*>(lds + ring_stages<GPW>() * kStage);  // [kRoutes][KB]
+  float* lds_sw = lds_sa + kRoutes * KB;                              // [2][KB]
 
   // ---- block scales of the work item: activations of every route, weights
   // of the tile (one 128-row scale block: PLAIN tiles are 128-aligned, SWIGLU
@@ -411,7 +427,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
     const int64_t route = start + (r < len ? r : len - 1);
     return a.a_row_index != nullptr ? a.a_row_index[route] : route;
   };
-  for (int64_t i = threadIdx.x; i < kGemmTileRows * KB; i += 256) {
+  for (int64_t i = threadIdx.x; i < kRoutes * KB; i += 256) {
     const int r = static_cast<int>(i / KB);
     lds_sa[i] = a.a_scale[token_of(r) * KB + (i - r * KB)];
   }
@@ -437,33 +453,36 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
   };
   const uint8_t* gb0 = b_row(2 * wave);
   const uint8_t* gb1 = b_row(2 * wave + 1);
-  const uint8_t* ga[2];
+  const uint8_t* ga[GPW];
   {
     const int rho = lane & 15;
     const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
     const uint8_t* plane = (rho & 1) ? a.a_lo : a.a_hi;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) ga[j] = plane + token_of((2 * wave + j) * 8 + rt) * K + kq * 32;
+    for (int j = 0; j < GPW; ++j) ga[j] = plane + token_of((GPW * wave + j) * 8 + rt) * K + kq * 32;
   }
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  const int ngw = (2 * wave < groups) + (2 * wave + 1 < groups);  // wave-uniform
-  if (ngw == 2)
-    grouped_gemm_loop<MODE, FIX, 2>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
-  else if (ngw == 1)
-    grouped_gemm_loop<MODE, FIX, 1>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
-  else
-    grouped_gemm_loop<MODE, FIX, 0>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane);
+  int ngw = groups - GPW * wave;  // wave-uniform
+  ngw = ngw < 0 ? 0 : (ngw > GPW ? GPW : ngw);
+#define GLM53_LOOP(n) \
+  grouped_gemm_loop<MODE, FIX, GPW, n>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
+  if (GPW >= 2 && ngw == 2) GLM53_LOOP(GPW >= 2 ? 2 : 0);
+  else if (ngw == 1) GLM53_LOOP(1);
+  else GLM53_LOOP(0);
+#undef GLM53_LOOP
 }
 
-size_t grouped_gemm_lds_bytes(int64_t K) {
-  return static_cast<size_t>(kStages) * kStage + sizeof(float) * (kGemmTileRows + 2) * static_cast<size_t>(K / kBlock);
+template <int GPW>
+size_t gemm_lds_bytes(int64_t K) {
+  return static_cast<size_t>(ring_stages<GPW>()) * stage_bytes<GPW>() +
+         sizeof(float) * (32 * GPW + 2) * static_cast<size_t>(K / kBlock);
 }
 
 // Work items (column tile, descriptor) are dealt to the XCDs in contiguous
 // runs: workgroup i runs on XCD i % 8, and item w = (i % 8) * ceil(W / 8) +
 // i / 8 keeps neighbouring items (same tile, consecutive descriptors of one
 // expert) on one XCD and its L2.
-template <int MODE>
+template <int MODE, int GPW>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
   const int64_t items = a.n_tiles * a.descriptors;
@@ -471,8 +490,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (w >= items) return;
   const int64_t ntile = w / a.descriptors, d = w % a.descriptors;
-  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true>(a, ntile, d, lds_dyn);
-  else grouped_gemm_body<MODE, false>(a, ntile, d, lds_dyn);
+  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true, GPW>(a, ntile, d, lds_dyn);
+  else grouped_gemm_body<MODE, false, GPW>(a, ntile, d, lds_dyn);
 }
 
 // Sets *flag (pre-cleared by clear_flag_kernel) when any byte of codes is
@@ -579,12 +598,20 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descr
   g.descriptors = descriptors;
   const int64_t items = g.n_tiles * descriptors;
   const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
-  const size_t lds = grouped_gemm_lds_bytes(a.K);
+  if (a.tile_rows != 0 && a.tile_rows != kGemmMinTileRows && a.tile_rows != kGemmTileRows)
+    return hipErrorInvalidValue;
+  const bool narrow = a.tile_rows == kGemmMinTileRows;
+  const size_t lds = narrow ? gemm_lds_bytes<1>(a.K) : gemm_lds_bytes<2>(a.K);
   if (a.K % kBlock != 0 || a.K <= 0 || lds > 160 * 1024) return hipErrorInvalidValue;
-  if (mode == GEMM_PLAIN)
-    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_PLAIN>, dim3(grid), dim3(256), lds, st, g);
-  else
-    hipLaunchKernelGGL(grouped_gemm_kernel<GEMM_SWIGLU>, dim3(grid), dim3(256), lds, st, g);
+#define GLM53_GEMM(m, w) hipLaunchKernelGGL((grouped_gemm_kernel<m, w>), dim3(grid), dim3(256), lds, st, g)
+  if (mode == GEMM_PLAIN) {
+    if (narrow) GLM53_GEMM(GEMM_PLAIN, 1);
+    else GLM53_GEMM(GEMM_PLAIN, 2);
+  } else {
+    if (narrow) GLM53_GEMM(GEMM_SWIGLU, 1);
+    else GLM53_GEMM(GEMM_SWIGLU, 2);
+  }
+#undef GLM53_GEMM
   return hipGetLastError();
 }
 

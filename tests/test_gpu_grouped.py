@@ -197,3 +197,48 @@ def test_config4_prefill_256_tokens_matches_oracle(M, O, dev, config2_layer, red
     else:
         want_grouped = O.grouped_moe(xb, sub, local, sc, cfg.swiglu_limit, host_shared(shared))
         assert_parity(to_bits(y).reshape(256, -1), want_grouped, O, exact_fraction=0.75)
+
+
+class SkewedGate:
+    """Experts 0, 1 and 2 take every token, the other 5 slots are drawn from
+    the remaining experts: the heavy experts hold many descriptors and the
+    light ones partial ones."""
+
+    def __init__(self, experts, seed):
+        self.experts, self.seed = experts, seed
+
+    def __call__(self, x):
+        import torch
+
+        rows = x.reshape(-1, x.shape[-1]).shape[0]
+        rng = np.random.default_rng(self.seed)
+        ids = np.stack([np.concatenate([[0, 1, 2], 3 + rng.choice(self.experts - 3, size=5, replace=False)])
+                        for _ in range(rows)]).astype(np.int32)
+        sc = rng.uniform(0.05, 0.3, size=ids.shape).astype(np.float32)
+        return (torch.from_numpy(ids).to(x.device).reshape(*x.shape[:-1], 8),
+                torch.from_numpy(sc).to(x.device).reshape(*x.shape[:-1], 8))
+
+
+@pytest.mark.parametrize("reduction", ["grouped", "direct"])
+def test_skewed_routing_many_descriptors_matches_oracle(M, O, dev, reduction):
+    """1,024 tokens over 16 experts (512 routes per expert on average): the
+    prefill takes 64-route descriptors for the routed GEMMs and 64-token
+    tiles for the shared expert; experts 0-2 hold 1,024 routes each (16
+    descriptors of one expert side by side)."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=256, intermediate=128, experts=16, top_k=8, limit=7.0)
+    bank, shared, _ = syn.synth_layer(cfg, seed=77, device=dev)
+    gate = SkewedGate(16, 5)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared, reduction=reduction)
+    T = 1024
+    x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(77, "wide"), device=dev)
+    y = moe(x)
+    ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
+    xb = to_bits(x).reshape(T, -1)
+    want = O.direct_moe(xb, host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    stats = assert_parity(to_bits(y).reshape(T, -1), want, O)
+    if reduction == "grouped":
+        want_g = O.grouped_moe(xb, host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+        assert_parity(to_bits(y).reshape(T, -1), want_g, O, exact_fraction=0.75)
+    else:
+        assert stats["bit_exact_fraction"] >= 0.75, stats
