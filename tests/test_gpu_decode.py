@@ -156,6 +156,38 @@ def test_fast_decode_matches_oracle_small(M, O, dev, small_layer):
         assert_parity(to_bits(y).reshape(-1), want, O, exact_fraction=0.9)
 
 
+def test_fast_decode_full_byte_range_codes(M, O, dev):
+    """Expert and shared weights drawn over all 256 E4M3 codes, so 0x7F
+    (+480) and 0xFF (-480) occur in every matrix: the fast decode launches
+    take their exact software decode (the hardware conversion reads those
+    codes as NaN) and must match the reference LUT's finite +-480."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=1024, intermediate=512, experts=32, top_k=8, limit=10.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=480, device=dev)
+    rng = np.random.default_rng(480)
+    with torch.no_grad():
+        for w in (bank.gate_up_weight, bank.down_weight, shared.gate_proj.weight, shared.up_proj.weight,
+                  shared.down_proj.weight):
+            w.copy_(torch.from_numpy(random_codes(rng, tuple(w.shape), high=256)))
+        for s in (bank.gate_up_scale_inv, bank.down_scale_inv, shared.gate_proj.weight_scale_inv,
+                  shared.up_proj.weight_scale_inv, shared.down_proj.weight_scale_inv):
+            s.copy_(torch.from_numpy((rng.uniform(size=tuple(s.shape)) * 0.0005).astype(np.float32)))
+    assert int(bank.code_flags().item()) != 0
+    moe = M.PackedFP8MoE(bank, cfg, gate, shared)
+    hb, hs = host_bank(bank), host_shared(shared)
+    for step in range(3):
+        x = syn.normal_bf16((1, 1, cfg.hidden_size), syn.key(480, step), device=dev)
+        y = moe(x)
+        gids, gsc = gate(x.reshape(1, -1))
+        ids, sc = gids.cpu().numpy(), gsc.cpu().numpy()
+        want = O.decode_moe(to_bits(x).reshape(-1), hb, ids[0], sc[0], cfg.swiglu_limit, hs)
+        got = to_bits(y).reshape(-1)
+        assert np.isfinite(O.bf16_to_f32(got)).all()
+        assert_parity(got, want, O, exact_fraction=0.9)
+
+
 def test_fast_and_any_shape_decode_agree(M, O, dev, small_layer):
     """The fused kernels and the stage-by-stage composition (the path odd
     shapes take) compute the same function."""

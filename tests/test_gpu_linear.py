@@ -77,6 +77,27 @@ def test_multi_row_mfma_path_matches_oracle(M, O, dev, rows):
     assert_parity(got, O.fp8_linear(x, codes, scale), O, exact_fraction=0.97)
 
 
+@pytest.mark.parametrize("rows", [1, 5, 64])
+def test_both_480_codes_gemv_and_mfma(M, O, dev, rows):
+    """Codes over the whole byte range, so 0x7F (+480) and 0xFF (-480) both
+    occur: the reference LUT decodes them as finite +-480 (fp8.py:22-27),
+    OCP E4M3 (and the MFMA) as NaN.  M = 1 takes the register-decode GEMV,
+    M > 1 the MFMA GEMM with its chained +-32 correction."""
+    rng = np.random.default_rng(480 + rows)
+    k, n = 1024, 272
+    codes = random_codes(rng, (n, k), high=256)
+    codes[:, :8] = 0xFF  # every row carries both signs
+    codes[:, 8:16] = 0x7F
+    scale = (rng.uniform(size=(-(-n // 128), k // 128)) * 0.002).astype(np.float32)
+    x = O.f32_to_bf16(rng.normal(size=(rows, k)).astype(np.float32))
+    got = _linear(M, dev, x, codes, scale)
+    want = O.fp8_linear(x, codes, scale)
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+    # full-range codes spread the products over ~2^16: more FP32 sums land
+    # one BF16 ulp from the exact one than for checkpoint-like weights
+    assert_parity(got, want, O, exact_fraction=0.95)
+
+
 def test_input_layout_invariance(M, O, dev):
     """tests/test_metal_input_layout.py:27-95: strided / offset inputs give
     byte-identical results to row-contiguous ones."""
