@@ -331,6 +331,7 @@ struct glm53_decode_plan {
   // fixed scratch (allocated once)
   uint16_t* hidden = nullptr;  // [(k + 1) * max(I, Is)]
   float* sig = nullptr;        // [E] router logits
+  unsigned long long* route_words = nullptr;  // [E] three-launch step's router exchange
   int32_t* ids = nullptr;      // [k]
   float* scores = nullptr;     // [k]
   int* err = nullptr;
@@ -387,7 +388,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
     return o;
   };
   size_t o_hidden = take(2 * (top_k + 1) * Imax);
-  size_t o_sig = take(4 * experts), o_choice = take(4 * experts), o_arr = take(4), o_ids = take(4 * top_k);
+  size_t o_sig = take(4 * experts), o_words = take(8 * experts), o_ids = take(4 * top_k);
   size_t o_scores = take(4 * top_k), o_err = take(4);
   size_t o_gate = take(2 * top_k * intermediate), o_up = take(2 * top_k * intermediate);
   size_t o_down = take(2 * top_k * hidden), o_routed = take(2 * hidden);
@@ -407,6 +408,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   uint8_t* b = static_cast<uint8_t*>(p->arena);
   p->hidden = reinterpret_cast<uint16_t*>(b + o_hidden);
   p->sig = reinterpret_cast<float*>(b + o_sig);
+  p->route_words = reinterpret_cast<unsigned long long*>(b + o_words);
   p->ids = reinterpret_cast<int32_t*>(b + o_ids);
   p->scores = reinterpret_cast<float*>(b + o_scores);
   p->err = reinterpret_cast<int*>(b + o_err);
@@ -785,7 +787,7 @@ int run_step(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_ex
     a.ids = const_cast<int32_t*>(ids);
     a.scores = const_cast<float*>(scores);
   }
-  a.logits = p->sig;
+  a.route_words = p->route_words;
   a.router_count = p->router_count;
   a.gate_up_weight = bank->gate_up_weight;
   a.gate_up_scale = bank->gate_up_scale_inv;
@@ -807,6 +809,7 @@ int run_step(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_ex
   a.shared_out = p->shared_out;
   a.error_flag = p->err;
   a.shared_rows_per_wave = 2;
+  a.shared_delay = kStepSharedDelay;
   const int sd_wgs = shared != nullptr ? static_cast<int>(cdiv(p->H, 64)) : 0;
   a.routed_wgs = std::max(64, p->step_slots - sd_wgs);
   HIP_TRY(launch_step(a, stages, st), "decode step launch");

@@ -75,7 +75,7 @@ struct StepArgs {
   const float* router_bias;       // [E]
   float routed_scaling_factor;
   int norm_topk_prob;
-  float* logits;                  // [E] router logits (read-modify-write exchange in launch 1)
+  unsigned long long* route_words;  // [E] launch 1 exchange: sigmoid bits << 32 | selection key
   uint32_t* router_count;         // arrival counter of launch 1 (self-resetting)
   int32_t* ids;                   // [top_k]: launch 1 writes (router) or given
   float* scores;                  // [top_k]
@@ -99,8 +99,13 @@ struct StepArgs {
   int router_wgs;                 // ceil(E / 4) or 0
   int shared_rows_per_wave;       // launch 1 shared gate/up rows per wavefront
   int routed_wgs;                 // launch 2 workgroups over the routed units
+  int shared_delay;               // launch 1: sleeps of ~512 clocks before the shared rows load
 };
 
+// Launch 1's shared-expert workgroups wait this many ~512-clock sleeps before
+// loading, so the router rows (on the selection's critical path) meet an
+// idle memory system.
+constexpr int kStepSharedDelay = 2;
 bool step_shape_supported(int64_t H, int64_t I);
 int step_gate_up_occupancy(int64_t H, int64_t I);
 hipError_t launch_step(const StepArgs& a, int stages, hipStream_t st);

@@ -177,12 +177,15 @@ struct GateUpUnit {
 
 // ---------------------------------------------------------------- launch 1
 
-// Router logit of expert e (patch.py:133): lane l covers columns 4 l + 256 j;
-// a batch's loads are all in flight at once.  The result goes out by a
-// read-modify-write, performed where every workgroup's atomics meet, so the
-// selecting workgroup reads it back without fences.
+// Router word of expert e (patch.py:131-142): the FP32 logit x_f32 . W_f32^T
+// (lane l covers columns 4 l + 256 j; a batch's loads are all in flight at
+// once), its sigmoid s and the selection key, the order-preserving image of
+// the FP32 sum s + bias (at least 1, so 0 marks an absent expert), published
+// as one word s_bits << 32 | key by a read-modify-write, performed where every
+// workgroup's atomics meet, so the selecting workgroup reads it back without
+// fences and does no per-expert arithmetic itself.
 template <int kCols>
-__device__ __forceinline__ void router_logit(const StepArgs& a, int64_t e, int lane) {
+__device__ __forceinline__ void router_word(const StepArgs& a, int64_t e, int lane) {
   constexpr int kChunks = kCols / 256;
   constexpr int kBatch = kChunks <= 16 ? kChunks
                          : kChunks % 16 == 0 ? 16
@@ -191,6 +194,7 @@ __device__ __forceinline__ void router_logit(const StepArgs& a, int64_t e, int l
                                              : 8;
   static_assert(kCols % 256 == 0 && kChunks % kBatch == 0, "router row must split into whole batches");
   const float* w = a.router_weight + e * kCols;
+  const float bias = a.router_bias[e];
   float acc = 0.0f;
 #pragma unroll
   for (int j0 = 0; j0 < kChunks; j0 += kBatch) {
@@ -210,7 +214,11 @@ __device__ __forceinline__ void router_logit(const StepArgs& a, int64_t e, int l
     }
   }
   acc = wave_sum(acc);
-  if (lane == 0) (void)atomicExch(reinterpret_cast<uint32_t*>(a.logits) + e, __float_as_uint(acc));
+  if (lane == 0) {
+    const float sg = router_sigmoid(acc);
+    const uint32_t key = max(orderable_bits(__fadd_rn(sg, bias)), 1u);
+    (void)atomicExch(a.route_words + e, (static_cast<unsigned long long>(__float_as_uint(sg)) << 32) | key);
+  }
 }
 
 template <int VBH, int CHH>
@@ -224,21 +232,20 @@ __global__ __launch_bounds__(256) void step_router_shared_kernel(StepArgs a) {
   if (bid < a.router_wgs) {
     // ---- router logit of expert e = 4 bid + wave
     const int64_t e = static_cast<int64_t>(bid) * 4 + wave;
-    if (e < a.experts) router_logit<VBH * CHH * 64>(a, e, lane);
+    if (e < a.experts) router_word<VBH * CHH * 64>(a, e, lane);
     // the last workgroup to arrive selects: every logit is in place
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) s_last = atomicAdd(a.router_count, 1u) == static_cast<unsigned>(a.router_wgs - 1);
     __syncthreads();
     if (s_last && wave == 0) {
-      float lg[5];
+      unsigned long long wd[5];
 #pragma unroll
       for (int i = 0; i < 5; ++i) {
         const int64_t c = lane + 64 * i;
-        lg[i] = c < a.experts ? __uint_as_float(atomicOr(reinterpret_cast<uint32_t*>(a.logits) + c, 0u)) : 0.0f;
+        wd[i] = c < a.experts ? atomicOr(a.route_words + c, 0ull) : 0ull;
       }
-      wave_topk_regs<5>(lg, a.router_bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids,
-                        s_w);
+      wave_topk_words<5>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids, s_w);
       if (lane < a.top_k) {
         a.ids[lane] = s_ids[lane];
         a.scores[lane] = s_w[lane];
@@ -253,6 +260,8 @@ __global__ __launch_bounds__(256) void step_router_shared_kernel(StepArgs a) {
   const int64_t r_end = r0 + a.shared_rows_per_wave < a.intermediate ? r0 + a.shared_rows_per_wave : a.intermediate;
   const int64_t K = a.hidden, SC = K / kBlock;
   uint16_t* out = a.hidden_act + static_cast<int64_t>(a.top_k) * a.intermediate;
+  if (a.router_wgs > 0)
+    for (int i = 0; i < a.shared_delay; ++i) __builtin_amdgcn_s_sleep(8);
   XRaw<VBH, CHH> raw;
   load_x_raw<VBH, CHH>(a.x, lane, raw);
   auto run = [&](auto hw) {

@@ -212,6 +212,10 @@ __device__ __forceinline__ uint32_t orderable_bits(float v) {
   return u ^ ((u & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
+// sigmoid of a router logit, the one expression every selection path uses
+// (so a score computed where the logit is made equals one computed later).
+__device__ __forceinline__ float router_sigmoid(float logit) { return 1.0f / (1.0f + expf(-logit)); }
+
 // Core selection over logits already in registers: lg[i] is the logit of
 // expert lane + 64 * i (ignored when that is >= experts).  Each of the top_k
 // rounds is two DPP reductions: the largest biased score (as its orderable
@@ -229,7 +233,7 @@ __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], cons
     float sg = 0.0f;
     key[i] = 0u;
     if (c < experts) {
-      sg = 1.0f / (1.0f + expf(-lg[i]));
+      sg = router_sigmoid(lg[i]);
       key[i] = max(orderable_bits(__fadd_rn(sg, bias[c])), 1u);
     }
     sigs[i] = sg;
@@ -259,6 +263,72 @@ __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], cons
     total = __fadd_rn(total, w);
     if (lane == slot) w_mine = w;
     if (lane == 0) ids_dst[slot] = static_cast<int32_t>(id);
+  }
+  if (lane < top_k) {
+    float v = w_mine;
+    if (top_k > 1 && norm) v = v / total;
+    w_dst[lane] = __fmul_rn(v, scaling);
+  }
+}
+
+// Selection over published router words (sigmoid bits << 32 | key, key 0 =
+// absent): wd[i] belongs to expert lane + 64 i.  Same order as
+// wave_topk_regs, (key desc, expert id asc), with one reduction per pick:
+// each lane keeps a head (its largest key, lowest id among equals), a DPP max
+// over the heads finds the key, a ballot finds the lanes holding it (one
+// lane: its head is the pick; several: a DPP min over their head ids), and
+// the winning lane drops that entry and recomputes its head.
+template <int PER_LANE>
+__device__ __forceinline__ void wave_topk_words(const unsigned long long (&wd)[PER_LANE], int top_k, float scaling,
+                                                int norm, int lane, int32_t* ids_dst, float* w_dst) {
+  uint32_t key[PER_LANE];
+  float sig[PER_LANE];
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    key[i] = static_cast<uint32_t>(wd[i]);
+    sig[i] = __uint_as_float(static_cast<uint32_t>(wd[i] >> 32));
+  }
+  uint32_t hk;
+  int hi;
+  float hs;
+  auto head = [&]() {
+    hk = key[0];
+    hi = 0;
+    hs = sig[0];
+#pragma unroll
+    for (int i = 1; i < PER_LANE; ++i)
+      if (key[i] > hk) {
+        hk = key[i];
+        hi = i;
+        hs = sig[i];
+      }
+  };
+  head();
+  float total = 0.0f;
+  float w_mine = 0.0f;  // lane `slot` keeps the weight of its slot
+#pragma unroll 1
+  for (int slot = 0; slot < top_k; ++slot) {
+    const uint32_t best = wave_max_u32(hk);
+    const unsigned long long holders = __ballot(hk == best);
+    int wl;
+    uint32_t id;
+    if (__popcll(holders) == 1) {
+      wl = __ffsll(static_cast<long long>(holders)) - 1;
+      id = static_cast<uint32_t>(wl + 64 * __builtin_amdgcn_readlane(hi, wl));
+    } else {
+      id = wave_min_u32(hk == best ? static_cast<uint32_t>(lane + 64 * hi) : 0xFFFFFFFFu);
+      wl = static_cast<int>(id & 63);
+    }
+    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs), wl));
+    total = __fadd_rn(total, w);
+    if (lane == slot) w_mine = w;
+    if (lane == 0) ids_dst[slot] = static_cast<int32_t>(id);
+    if (lane == wl) {
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i)
+        if (i == hi) key[i] = 0u;
+      head();
+    }
   }
   if (lane < top_k) {
     float v = w_mine;

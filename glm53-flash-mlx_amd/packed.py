@@ -220,7 +220,7 @@ class DecodePlan:
         N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))
 
     def set_mode(self, mode: int) -> None:
-        """N.DECODE_SINGLE_LAUNCH (default) or N.DECODE_THREE_LAUNCH."""
+        """N.DECODE_THREE_LAUNCH (default) or N.DECODE_SINGLE_LAUNCH."""
         N.check(self._lib.glm53_decode_plan_set_mode(self.handle, int(mode)))
 
     def error_flag(self) -> int:

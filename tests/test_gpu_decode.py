@@ -100,7 +100,9 @@ def config2_layer(dev):
 def _router_check(O, gate, x_bits, ids_gpu, scores_gpu):
     w = gate.weight.cpu().numpy()
     b = gate.e_score_correction_bias.cpu().numpy()
-    ids_o, sc_o, choice = O.router(x_bits, w, b, top_k=gate.top_k, return_choice=True)
+    ids_o, sc_o, choice = O.router(x_bits, w, b, top_k=gate.top_k,
+                                   routed_scaling_factor=getattr(gate, "routed_scaling_factor", 1.0),
+                                   norm_topk_prob=getattr(gate, "norm_topk_prob", True), return_choice=True)
     for t in range(ids_o.shape[0]):
         got, want = set(ids_gpu[t].tolist()), set(ids_o[t].tolist())
         if got != want:
@@ -138,6 +140,62 @@ def test_router_scores_kat(M, dev, tokens):
     raw = 1.0 / (1.0 + np.exp(-np.array([3.0, 2.0])))
     for t in range(tokens):
         np.testing.assert_allclose(scores.cpu().numpy()[t], raw / raw.sum() * 2.0, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("case", ["random", "all_equal", "lane_and_slot_ties"])
+def test_step_router_selection_matches_oracle(M, O, dev, case):
+    """The three-launch step selects in its router launch, from per-expert
+    (sigmoid, biased key) words.  Exact ties must come out in (choice desc,
+    expert id asc) order with the reference weights: ties between experts
+    one lane apart (10, 11), between entries of one lane (5, 69, 133, 197 sit
+    on lane 5) and all 288 experts equal.  ids and scores are read from the
+    plan (glm53_decode_moe's ids_out / scores_out) and checked against the
+    oracle router; the layer output against the oracle decode."""
+    import torch
+
+    syn = submodule("synthetic")
+    packed = submodule("packed")
+    N = submodule("_native")
+    cfg = syn.layer_config(hidden=1024, intermediate=512, experts=288, top_k=8, limit=10.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=31, device=dev)
+    w = gate.weight.clone()
+    b = gate.e_score_correction_bias.clone()
+    if case == "all_equal":
+        w.zero_()
+        b.zero_()
+    elif case == "lane_and_slot_ties":
+        for e in (69, 133, 197):
+            w[e] = w[5]
+        b[[5, 69, 133, 197]] = 2.0  # sigmoid < 1: these four lead, then the next three
+        for e in (11, 75):
+            w[e] = w[10]
+        b[[10, 11, 75]] = 1.0
+    g = M.Float32Gate(w, b, top_k=8, routed_scaling_factor=2.5, norm_topk_prob=True)
+    plan = packed.DecodePlan(1024, 512, 512, 288, 8, cfg.swiglu_limit)
+    plan.set_mode(N.DECODE_THREE_LAUNCH)
+    hs = host_shared(shared)
+    for step in range(3):
+        x = syn.normal_bf16((cfg.hidden_size,), syn.key(43, case, step), device=dev)
+        y = torch.empty_like(x)
+        ids_d = torch.empty(8, dtype=torch.int32, device=dev)
+        sc_d = torch.empty(8, dtype=torch.float32, device=dev)
+        plan.full(bank, shared, g, x, y, ids_d, sc_d, dev)
+        torch.cuda.synchronize()
+        xb = to_bits(x).reshape(-1)
+        ids, sc = ids_d.cpu().numpy()[None], sc_d.cpu().numpy()[None]
+        ids_o, sc_o = O.router(xb[None], w.cpu().numpy(), b.cpu().numpy(), top_k=8, routed_scaling_factor=2.5)
+        if case == "all_equal":
+            assert ids[0].tolist() == list(range(8))
+            np.testing.assert_array_equal(sc[0], np.full(8, np.float32(2.5 / 8)))
+        elif case == "lane_and_slot_ties":
+            assert ids[0].tolist()[:7] == [5, 69, 133, 197, 10, 11, 75]
+        if case != "random":
+            np.testing.assert_array_equal(ids[0], ids_o[0])
+            np.testing.assert_allclose(sc[0], sc_o[0], rtol=2e-6, atol=1e-7)
+        _router_check(O, g, xb[None], ids, sc)
+        want = O.decode_moe(xb, _touched_bank(bank, ids[0]), np.arange(8), sc[0], cfg.swiglu_limit, hs)
+        assert_parity(to_bits(y).reshape(-1), want, O, exact_fraction=0.9)
+    assert plan.error_flag() == 0
 
 
 def test_fast_decode_matches_oracle_small(M, O, dev, small_layer):
