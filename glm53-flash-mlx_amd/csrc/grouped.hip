@@ -210,10 +210,12 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
 // both brought straight from global memory into an LDS ring by direct loads
 // (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no
 // registers hold data in flight and the ring's other stages stream while
-// one is multiplied.  A stage's LDS layout for a 16-row operand tile is
-// [half h][k-quarter q][row r] x 16 bytes, holding bytes 32 q + 16 h of row
-// r: the MFMA lane (r = l % 16, q = l / 16) then reads its 32 operand bytes
-// as two conflict-free 16-byte LDS reads at 16 l and 1024 + 16 l.
+// one is multiplied.  Each direct load reads 8 rows as whole 128-byte lines
+// (a 16-row operand tile takes two); in LDS a row's 16-byte pieces are
+// permuted by an XOR of the row index, so the MFMA lane (r = l % 16, q =
+// l / 16) reads its 32 operand bytes (row r, bytes 32 q .. 32 q + 31) as two
+// conflict-free 16-byte LDS reads (operand_slots).  Whole lines per load
+// stream weight tiles about 14% faster than 64 bytes of 16 rows per load.
 // Wavefront w multiplies route groups GPW w .. GPW w + GPW - 1 against the 8
 // weight tiles, one v_mfma_scale_f32_16x16x128_f8f6f4 per (group, tile);
 // lane l's accumulator rows are hi/lo of routes 2 (l / 16) and 2 (l / 16) +
@@ -276,9 +278,29 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ i32x8 lds_operand(const uint8_t* p) {
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 1024);
+// LDS layout of one 16-row x 128-byte operand tile: row r's 16-byte piece p
+// sits in slot p ^ ((r >> 1) & 7) of the row's 128 bytes, so the two direct
+// loads that fill a tile each read 8 rows as whole 128-byte lines (lane l:
+// row l / 8, slot l % 8), and the MFMA reads below (lane l: row l % 16,
+// pieces 2 (l / 16) and 2 (l / 16) + 1) hit 16 distinct 16-byte bank groups
+// per 16 lanes.
+struct OperandSlots {
+  uint32_t lo, hi;  // byte offsets of the lane's two pieces in a tile
+};
+__device__ __forceinline__ OperandSlots operand_slots(int lane) {
+  const int r = lane & 15, kq = lane >> 4, g = (r >> 1) & 7;
+  return {static_cast<uint32_t>(128 * r + 16 * ((2 * kq) ^ g)), static_cast<uint32_t>(128 * r + 16 * ((2 * kq + 1) ^ g))};
+}
+// Byte offset, within its row's 128-byte K block, of the piece lane l loads
+// in load h (0: rows 0-7, 1: rows 8-15) of a tile; its row is 8 h + l / 8.
+__device__ __forceinline__ int load_piece_offset(int lane, int h) {
+  const int r = 8 * h + (lane >> 3);
+  return 16 * ((lane & 7) ^ ((r >> 1) & 7));
+}
+
+__device__ __forceinline__ i32x8 lds_operand(const uint8_t* tile, OperandSlots o) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + o.lo);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + o.hi);
   return (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
@@ -286,24 +308,25 @@ __device__ __forceinline__ i32x8 lds_operand(const uint8_t* p) {
 
 template <int MODE, bool FIX, int GPW, int NGW>
 __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int64_t ntile, int32_t start, int32_t len,
-                                                  int64_t KB, const uint8_t* gb0, const uint8_t* gb1,
-                                                  const uint8_t* const (&ga)[GPW], uint8_t* lds, uint32_t lds_addr,
+                                                  int64_t KB, const uint8_t* const (&gb)[2][2],
+                                                  const uint8_t* const (&ga)[GPW][2], uint8_t* lds, uint32_t lds_addr,
                                                   const float* lds_sa, const float* lds_sw, int wave, int lane) {
   constexpr int kStage = stage_bytes<GPW>();
   constexpr int P = 4 + 2 * NGW;  // direct loads per stage of this wavefront
   const int kq = lane >> 4;
+  const OperandSlots slots = operand_slots(lane);
   auto issue = [&](int64_t kb, int slot) {
     const int64_t ko = kb * kBlock;
     const uint32_t sb = lds_addr + slot * kStage + 2 * wave * kOperand;
-    lds_direct16(gb0 + ko, sb);
-    lds_direct16(gb0 + ko + 16, sb + 1024);
-    lds_direct16(gb1 + ko, sb + kOperand);
-    lds_direct16(gb1 + ko + 16, sb + kOperand + 1024);
+    lds_direct16(gb[0][0] + ko, sb);
+    lds_direct16(gb[0][1] + ko, sb + 1024);
+    lds_direct16(gb[1][0] + ko, sb + kOperand);
+    lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
     const uint32_t sa = lds_addr + slot * kStage + kStageB + GPW * wave * kOperand;
 #pragma unroll
     for (int j = 0; j < NGW; ++j) {
-      lds_direct16(ga[j] + ko, sa + j * kOperand);
-      lds_direct16(ga[j] + ko + 16, sa + j * kOperand + 1024);
+      lds_direct16(ga[j][0] + ko, sa + j * kOperand);
+      lds_direct16(ga[j][1] + ko, sa + j * kOperand + 1024);
     }
   };
 
@@ -328,7 +351,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
       float sa[NGW > 0 ? NGW : 1][2];
 #pragma unroll
       for (int j = 0; j < NGW; ++j) {
-        av[j] = lds_operand(st + kStageB + (GPW * wave + j) * kOperand + 16 * lane);
+        av[j] = lds_operand(st + kStageB + (GPW * wave + j) * kOperand, slots);
 #pragma unroll
         for (int h = 0; h < 2; ++h) sa[j][h] = lds_sa[((GPW * wave + j) * 8 + 2 * kq + h) * KB + kb];
       }
@@ -336,7 +359,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
       const float sw_hi = MODE == GEMM_SWIGLU ? lds_sw[KB + kb] : sw_lo;
       i32x8 bt[8];  // all eight weight tiles read ahead: one LDS wait per stage
 #pragma unroll
-      for (int t = 0; t < 8; ++t) bt[t] = lds_operand(st + t * kOperand + 16 * lane);
+      for (int t = 0; t < 8; ++t) bt[t] = lds_operand(st + t * kOperand, slots);
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         i32x8 bq = bt[t];
@@ -415,7 +438,6 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
   }
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
-  const int kq = lane >> 4;
   const int groups = (len + 7) >> 3;
   float* lds_sa = reinterpret_cast<float*>(lds + ring_stages<GPW>() * kStage);  // [kRoutes][KB]
   float* lds_sw = lds_sa + kRoutes * KB;                              // [2][KB]
@@ -437,35 +459,43 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
     lds_sw[i] = i < KB ? a.scale[soff + i] : a.scale_up[soff + i - KB];
   __syncthreads();
 
-  // ---- per-lane global sources of the direct loads
-  auto b_row = [&](int t) -> const uint8_t* {
+  // ---- per-lane global sources of the direct loads: load h of a tile
+  // fills its rows 8 h .. 8 h + 7, lane l reading row 8 h + l / 8
+  auto b_row = [&](int t, int h) -> const uint8_t* {
+    const int rr = 8 * h + (lane >> 3);
     int64_t row;
     const uint8_t* w;
     if (MODE == GEMM_PLAIN) {
-      row = ntile * kTileRows + t * 16 + (lane & 15);
+      row = ntile * kTileRows + t * 16 + rr;
       w = a.weight;
     } else {
-      row = ntile * (kTileRows / 2) + (t & 3) * 16 + (lane & 15);
+      row = ntile * (kTileRows / 2) + (t & 3) * 16 + rr;
       w = t < 4 ? a.weight : a.weight_up;
     }
     if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
-    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + kq * 32;
+    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + load_piece_offset(lane, h);
   };
-  const uint8_t* gb0 = b_row(2 * wave);
-  const uint8_t* gb1 = b_row(2 * wave + 1);
-  const uint8_t* ga[GPW];
-  {
-    const int rho = lane & 15;
+  const uint8_t* gb[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) gb[t][h] = b_row(2 * wave + t, h);
+  // activation operand row rho: route 2 (rho / 4) + (rho / 2) % 2 of the
+  // group, hi plane for even rho, lo plane for odd
+  const uint8_t* ga[GPW][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rho = 8 * h + (lane >> 3);
     const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
     const uint8_t* plane = (rho & 1) ? a.a_lo : a.a_hi;
 #pragma unroll
-    for (int j = 0; j < GPW; ++j) ga[j] = plane + token_of((GPW * wave + j) * 8 + rt) * K + kq * 32;
+    for (int j = 0; j < GPW; ++j) ga[j][h] = plane + token_of((GPW * wave + j) * 8 + rt) * K + load_piece_offset(lane, h);
   }
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   int ngw = groups - GPW * wave;  // wave-uniform
   ngw = ngw < 0 ? 0 : (ngw > GPW ? GPW : ngw);
 #define GLM53_LOOP(n) \
-  grouped_gemm_loop<MODE, FIX, GPW, n>(a, ntile, start, len, KB, gb0, gb1, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
+  grouped_gemm_loop<MODE, FIX, GPW, n>(a, ntile, start, len, KB, gb, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
   if (GPW >= 2 && ngw == 2) GLM53_LOOP(GPW >= 2 ? 2 : 0);
   else if (ngw == 1) GLM53_LOOP(1);
   else GLM53_LOOP(0);
