@@ -226,6 +226,7 @@ __global__ __launch_bounds__(256) void step_router_shared_kernel(StepArgs a) {
   __shared__ int s_last;
   __shared__ int32_t s_ids[kMaxTopK];
   __shared__ float s_w[kMaxTopK];
+  __shared__ TopkScratch s_topk;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int bid = blockIdx.x;
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(256) void step_router_shared_kernel(StepArgs a) {
         const int64_t c = lane + 64 * i;
         wd[i] = c < a.experts ? atomicOr(a.route_words + c, 0ull) : 0ull;
       }
-      wave_topk_words<5>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids, s_w);
+      wave_topk_words_sorted<5>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids, s_w, s_topk);
       if (lane < a.top_k) {
         a.ids[lane] = s_ids[lane];
         a.scores[lane] = s_w[lane];

@@ -337,6 +337,141 @@ __device__ __forceinline__ void wave_topk_words(const unsigned long long (&wd)[P
   }
 }
 
+// Value held by lane (lane ^ J) for J = 1 .. 32: DPP within 16-lane rows
+// (row_ror:4 reads lane (i - 4) mod 16, row_ror:12 lane (i + 4) mod 16,
+// row_ror:8 lane i ^ 8), ds_swizzle across 16, a lane shuffle across 32.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
+  if constexpr (J == 1) {
+    return dpp_u32<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (J == 2) {
+    return dpp_u32<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (J == 4) {
+    const uint32_t down = dpp_u32<0x124>(v);
+    const uint32_t up = dpp_u32<0x12C>(v);
+    return (lane & 4) ? down : up;
+  } else if constexpr (J == 8) {
+    return dpp_u32<0x128>(v);
+  } else if constexpr (J == 16) {
+    return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+  } else {
+    return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32));
+  }
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint32_t bitonic_step(uint32_t v, int lane) {
+  const uint32_t u = xor_lane<J>(v, lane);
+  return (((lane & J) == 0) == ((lane & K) == 0)) ? max(v, u) : min(v, u);
+}
+
+// One value per lane sorted descending over lanes 0..63 (bitonic network,
+// 21 compare-exchange steps).
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v, int lane) {
+  v = bitonic_step<2, 1>(v, lane);
+  v = bitonic_step<4, 2>(v, lane);
+  v = bitonic_step<4, 1>(v, lane);
+  v = bitonic_step<8, 4>(v, lane);
+  v = bitonic_step<8, 2>(v, lane);
+  v = bitonic_step<8, 1>(v, lane);
+  v = bitonic_step<16, 8>(v, lane);
+  v = bitonic_step<16, 4>(v, lane);
+  v = bitonic_step<16, 2>(v, lane);
+  v = bitonic_step<16, 1>(v, lane);
+  v = bitonic_step<32, 16>(v, lane);
+  v = bitonic_step<32, 8>(v, lane);
+  v = bitonic_step<32, 4>(v, lane);
+  v = bitonic_step<32, 2>(v, lane);
+  v = bitonic_step<32, 1>(v, lane);
+  v = bitonic_step<64, 32>(v, lane);
+  v = bitonic_step<64, 16>(v, lane);
+  v = bitonic_step<64, 8>(v, lane);
+  v = bitonic_step<64, 4>(v, lane);
+  v = bitonic_step<64, 2>(v, lane);
+  v = bitonic_step<64, 1>(v, lane);
+  return v;
+}
+
+// LDS of the threshold selection: compacted candidates, then the weights
+// by slot.
+struct TopkScratch {
+  uint32_t key[64];
+  uint32_t id[64];
+  float sig[64];
+  float w[kMaxTopK];
+};
+
+// The selection of wave_topk_words, found without sequential picks: the
+// top_k-th largest of the 64 lane heads (each lane's largest key, after a
+// bitonic sort) bounds the top_k-th largest key from below, so every entry
+// that can be picked has key >= that bound.  Those candidates (at least
+// top_k, usually few) are compacted into LDS and each one's slot is its rank
+// under (key desc, expert id asc); more than 64 candidates (ties at the
+// bound) fall back to the sequential picks.  Same ids, weights and FP32
+// summation order as wave_topk_words.  (A single wavefront issues about one
+// dependent instruction per ~12 cycles here, so the sort, the compaction,
+// the rank loop and the slot sum each take ~0.3-0.5 us.)
+template <int PER_LANE>
+__device__ __forceinline__ void wave_topk_words_sorted(const unsigned long long (&wd)[PER_LANE], int top_k,
+                                                       float scaling, int norm, int lane, int32_t* ids_dst,
+                                                       float* w_dst, TopkScratch& s) {
+  uint32_t key[PER_LANE];
+  float sig[PER_LANE];
+  uint32_t head = 0;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    key[i] = static_cast<uint32_t>(wd[i]);
+    sig[i] = __uint_as_float(static_cast<uint32_t>(wd[i] >> 32));
+    head = max(head, key[i]);
+  }
+  const uint32_t bound = __builtin_amdgcn_readlane(wave_sort_desc(head, lane), top_k - 1);
+  unsigned long long mask[PER_LANE];
+  int count = 0;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    mask[i] = __ballot(key[i] >= bound && key[i] != 0u);
+    count += __popcll(mask[i]);
+  }
+  if (count > 64) {
+    wave_topk_words<PER_LANE>(wd, top_k, scaling, norm, lane, ids_dst, w_dst);
+    return;
+  }
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    if ((mask[i] >> lane) & 1ull) {
+      const int pos = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                 static_cast<uint32_t>(mask[i] >> 32),
+                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[i]), 0u)));
+      s.key[pos] = key[i];
+      s.id[pos] = static_cast<uint32_t>(lane + 64 * i);
+      s.sig[pos] = sig[i];
+    }
+    base += __popcll(mask[i]);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (lane < count) {
+    const uint32_t k = s.key[lane], id = s.id[lane];
+    int rank = 0;
+    for (int m = 0; m < count; ++m) {
+      const uint32_t km = s.key[m], im = s.id[m];
+      rank += (km > k || (km == k && im < id)) ? 1 : 0;
+    }
+    if (rank < top_k) {
+      ids_dst[rank] = static_cast<int32_t>(id);
+      s.w[rank] = s.sig[lane];
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  float total = 0.0f;
+  for (int sl = 0; sl < top_k; ++sl) total = __fadd_rn(total, s.w[sl]);
+  if (lane < top_k) {
+    float v = s.w[lane];
+    if (top_k > 1 && norm) v = v / total;
+    w_dst[lane] = __fmul_rn(v, scaling);
+  }
+}
+
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_emit(const float* __restrict__ logits, const float* __restrict__ bias,
                                                int64_t experts, int top_k, float scaling, int norm, int lane,

@@ -142,15 +142,19 @@ def test_router_scores_kat(M, dev, tokens):
         np.testing.assert_allclose(scores.cpu().numpy()[t], raw / raw.sum() * 2.0, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("case", ["random", "all_equal", "lane_and_slot_ties"])
+@pytest.mark.parametrize("case", ["random", "all_equal", "lane_and_slot_ties", "ties_at_bound"])
 def test_step_router_selection_matches_oracle(M, O, dev, case):
     """The three-launch step selects in its router launch, from per-expert
-    (sigmoid, biased key) words.  Exact ties must come out in (choice desc,
-    expert id asc) order with the reference weights: ties between experts
-    one lane apart (10, 11), between entries of one lane (5, 69, 133, 197 sit
-    on lane 5) and all 288 experts equal.  ids and scores are read from the
-    plan (glm53_decode_moe's ids_out / scores_out) and checked against the
-    oracle router; the layer output against the oracle decode."""
+    (sigmoid, biased key) words: a bitonic sort of the 64 lane maxima bounds
+    the 8th key from below and the candidates above the bound are ranked;
+    more than 64 candidates fall back to sequential picks.  Exact ties must
+    come out in (choice desc, expert id asc) order with the reference
+    weights: ties between experts one lane apart (10, 11), between entries
+    of one lane (5, 69, 133, 197 sit on lane 5), 20 experts tied at the
+    bound (100-119: 20 candidates for 8 slots) and all 288 experts equal
+    (the fallback).  ids and scores are read from the plan
+    (glm53_decode_moe's ids_out / scores_out) and checked against the oracle
+    router; the layer output against the oracle decode."""
     import torch
 
     syn = submodule("synthetic")
@@ -170,6 +174,10 @@ def test_step_router_selection_matches_oracle(M, O, dev, case):
         for e in (11, 75):
             w[e] = w[10]
         b[[10, 11, 75]] = 1.0
+    elif case == "ties_at_bound":
+        for e in range(101, 120):
+            w[e] = w[100]
+        b[100:120] = 3.0
     g = M.Float32Gate(w, b, top_k=8, routed_scaling_factor=2.5, norm_topk_prob=True)
     plan = packed.DecodePlan(1024, 512, 512, 288, 8, cfg.swiglu_limit)
     plan.set_mode(N.DECODE_THREE_LAUNCH)
@@ -189,6 +197,8 @@ def test_step_router_selection_matches_oracle(M, O, dev, case):
             np.testing.assert_array_equal(sc[0], np.full(8, np.float32(2.5 / 8)))
         elif case == "lane_and_slot_ties":
             assert ids[0].tolist()[:7] == [5, 69, 133, 197, 10, 11, 75]
+        elif case == "ties_at_bound":
+            assert ids[0].tolist() == list(range(100, 108))
         if case != "random":
             np.testing.assert_array_equal(ids[0], ids_o[0])
             np.testing.assert_allclose(sc[0], sc_o[0], rtol=2e-6, atol=1e-7)
