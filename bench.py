@@ -190,6 +190,7 @@ def main():
         stage_us[name] = time_graph(run_stage(mask), args.kernel_steps * 8, torch) / L
     router_us, gate_up_us, down_us = stage_us["router"], stage_us["gate_up"], stage_us["down"]
     probe = read_probe(lib, N, layers[-1].bank, dev, torch)
+    copy = copy_probe(dev, torch)
     launch_bytes = step_launch_bytes(H, I, Is, E, k)
     gu_bytes = launch_bytes["gate_up"]
     gu_gbs = gu_bytes / (gate_up_us * 1e-6) / 1e9
@@ -266,6 +267,7 @@ def main():
                             "down_reduce": round(down_bytes / (down_us * 1e-6) / 1e9, 1)},
             "launch_note": "stage-only graphs of one launch kind; kernel durations in profiles/",
             "achievable_read_GBps": probe,
+            "copy_GBps": copy,
             "one_launch_form": single,
             "weights_generated_s": round(gen_s, 1),
             "final_state_finite": finite,
@@ -317,6 +319,22 @@ def read_probe(lib, N, bank, dev, torch):
         us = time_graph(run, 4, torch) / regions
         out[label] = round(size / (us * 1e-6) / 1e9, 1)
     return out
+
+
+def copy_probe(dev, torch):
+    """STREAM-like device copy: 1 GiB read + 1 GiB written per copy, rate
+    counting both (graph of 4 copies between distinct buffers)."""
+    n = 1 << 30
+    src = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(2)]
+    dst = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(2)]
+
+    def run():
+        for i in range(4):
+            dst[i % 2].copy_(src[(i + 1) % 2])
+
+    us = time_graph(run, 4, torch) / 4
+    del src, dst
+    return round(2 * n / (us * 1e-6) / 1e9, 1)
 
 
 def host_layer_subset(layer, ids, torch, np):

@@ -70,6 +70,8 @@ _SIGNATURES = {
     "glm53_last_error": (ctypes.c_char_p, []),
     "glm53_abi_version": (ctypes.c_int, []),
     "glm53_e4m3_scan_codes": (ctypes.c_int, [P, I64, P, P]),
+    "glm53_bank_create": (ctypes.c_int, [P, P, P]),
+    "glm53_bank_destroy": (None, [P]),
     "glm53_fp8_linear_workspace_bytes": (SZ, [I64, I64, I64]),
     "glm53_fp8_linear": (ctypes.c_int, [P, I64, I64, P, I64, P, P, P, P, SZ, P]),
     "glm53_router_workspace_bytes": (SZ, [I64, I64, I64]),

@@ -218,6 +218,36 @@ int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* 
   return GLM53_OK;
 }
 
+int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out) {
+  CHECK_ARG(desc != nullptr && out != nullptr, "null pointer argument");
+  *out = nullptr;
+  CHECK_ARG(desc->gate_up_weight && desc->gate_up_scale_inv && desc->down_weight && desc->down_scale_inv,
+            "null bank tensor");
+  CHECK_ARG(desc->experts > 0 && desc->hidden > 0 && desc->intermediate > 0, "invalid bank dimensions");
+  CHECK_ARG(aligned(desc->gate_up_weight, 16) && aligned(desc->down_weight, 16),
+            "bank weights must be 16-byte aligned");
+  int32_t* flag = nullptr;
+  HIP_TRY(hipMalloc(&flag, sizeof(int32_t)), "bank code flag hipMalloc");
+  const int64_t gu = desc->experts * 2 * desc->intermediate * desc->hidden;
+  const int64_t dn = desc->experts * desc->hidden * desc->intermediate;
+  hipError_t e = launch_scan_480(desc->gate_up_weight, gu, flag, true, S(stream));
+  if (e == hipSuccess) e = launch_scan_480(desc->down_weight, dn, flag, false, S(stream));
+  if (e != hipSuccess) {
+    (void)hipFree(flag);
+    return hip_fail(e, "bank code scan");
+  }
+  auto* b = new glm53_bank(*desc);
+  b->code_flags = flag;
+  *out = b;
+  return GLM53_OK;
+}
+
+void glm53_bank_destroy(glm53_bank* bank) {
+  if (bank == nullptr) return;
+  (void)hipFree(const_cast<int32_t*>(bank->code_flags));
+  delete bank;
+}
+
 int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N, const float* scale_inv,
                      const int32_t* code_flags, void* y, void* workspace, size_t workspace_bytes, void* stream) {
   CHECK_ARG(M >= 0 && K > 0 && N > 0, "invalid shape M=%lld K=%lld N=%lld", (long long)M, (long long)K, (long long)N);

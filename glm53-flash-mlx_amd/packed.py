@@ -173,6 +173,38 @@ class PackedFP8ExpertBank(torch.nn.Module):
                       self.code_flags().data_ptr())
 
 
+class BankHandle:
+    """Native bank handle (glm53_bank_create): the bank's reference layout
+    validated once and its 0x7F/0xFF code flag scanned once and owned by the
+    handle.  `ptr` is a `glm53_bank*` for the C ABI's entry points; the bank
+    object (and so its weights) stays referenced while the handle lives."""
+
+    def __init__(self, bank: "PackedFP8ExpertBank", device: torch.device | None = None):
+        self._lib = N.lib()
+        self._bank = bank
+        self._device = device if device is not None else bank.gate_up_weight.device
+        N.require_device(bank.gate_up_weight, bank.down_weight)
+        desc = bank.as_c_struct()
+        self.ptr = ctypes.POINTER(N.Bank)()
+        N.check(self._lib.glm53_bank_create(ctypes.byref(desc), N.stream_handle(self._device), ctypes.byref(self.ptr)))
+
+    def close(self) -> None:
+        if self.ptr:
+            torch.cuda.synchronize(self._device)  # no call may still use the flag
+            self._lib.glm53_bank_destroy(self.ptr)
+            self.ptr = ctypes.POINTER(N.Bank)()
+
+    def __enter__(self) -> "BankHandle":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self.close()
+
+
 class DecodePlan:
     """Fixed-scratch batch-1 decode plan (one per layer and stream)."""
 

@@ -61,6 +61,20 @@ typedef struct glm53_bank {
   const int32_t* code_flags;
 } glm53_bank;
 
+/* Bank handle -- the native side of PackedFP8ExpertBank(...)
+ * (packed.py:747-876).  Validates the reference layout in `desc` (pointers,
+ * dimensions, 16-byte aligned weights), copies it, and owns a device code
+ * flag: both weight tensors are scanned once on `stream` for E4M3 codes
+ * 0x7F / 0xFF, so calls made with the handle never scan again (desc's own
+ * code_flags is ignored).  The layout is consumed as it is -- every kernel
+ * reads the [rows, K] row-major weights with whole 128-byte lines -- so no
+ * re-laid copy is made.  Weights stay borrowed: the caller keeps them alive
+ * and unchanged while the handle is in use.  The returned pointer is used
+ * wherever a `const glm53_bank*` is taken; destroy it (which frees the flag)
+ * only after the work that uses it has completed. */
+int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out);
+void glm53_bank_destroy(glm53_bank* bank);
+
 /* One BlockFP8Linear (fp8.py:302-326): weight u8 [out, in], scale
  * f32 [ceil(out/128), ceil(in/128)]. */
 typedef struct glm53_linear {

@@ -208,6 +208,56 @@ def test_step_router_selection_matches_oracle(M, O, dev, case):
     assert plan.error_flag() == 0
 
 
+def _device_int32(address):
+    """Reads one int32 at a raw device address (test helper, HIP runtime)."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    value = ctypes.c_int32(0)
+    assert hip.hipDeviceSynchronize() == 0
+    assert hip.hipMemcpy(ctypes.byref(value), ctypes.c_void_p(address), 4, 2) == 0  # device to host
+    return value.value
+
+
+def test_bank_handle_scans_once_and_decodes_like_the_bank(M, O, dev, small_layer):
+    """glm53_bank_create: the handle over a clean bank holds a zero code flag
+    and decodes bit-identically to the plain bank struct; a bank holding a
+    0x7F code gets a nonzero flag.  Bad descriptors are refused."""
+    import ctypes
+
+    import torch
+
+    syn = submodule("synthetic")
+    packed = submodule("packed")
+    N = submodule("_native")
+    cfg, bank, shared, gate = small_layer
+    plan = packed.DecodePlan(cfg.hidden_size, cfg.moe_intermediate_size, cfg.moe_intermediate_size,
+                             cfg.n_routed_experts, 8, cfg.swiglu_limit)
+    with packed.BankHandle(bank, dev) as handle:
+        assert _device_int32(handle.ptr.contents.code_flags) == 0
+        for step in range(2):
+            x = syn.normal_bf16((cfg.hidden_size,), syn.key(44, step), device=dev)
+            y_plain = torch.empty_like(x)
+            y_handle = torch.empty_like(x)
+            plan.full(bank, shared, gate, x, y_plain, None, None, dev)
+            s = shared.as_c_struct()
+            r = gate.as_c_struct()
+            N.check(N.lib().glm53_decode_moe(plan.handle, handle.ptr, ctypes.byref(s), ctypes.byref(r), N.ptr(x),
+                                             N.ptr(y_handle), None, None, N.stream_handle(dev)))
+            torch.cuda.synchronize()
+            assert torch.equal(y_plain.view(torch.int16), y_handle.view(torch.int16))
+    marked = packed.PackedFP8ExpertBank(bank.gate_up_weight.clone(), bank.gate_up_scale_inv, bank.down_weight,
+                                        bank.down_scale_inv, intermediate_size=bank.intermediate_size)
+    marked.gate_up_weight[3, 5, 7] = 0x7F
+    with packed.BankHandle(marked, dev) as handle:
+        assert _device_int32(handle.ptr.contents.code_flags) != 0
+    bad = bank.as_c_struct()
+    bad.experts = 0
+    out = ctypes.POINTER(N.Bank)()
+    assert N.lib().glm53_bank_create(ctypes.byref(bad), N.stream_handle(dev), ctypes.byref(out)) == 1
+    assert not out
+
+
 def test_fast_decode_matches_oracle_small(M, O, dev, small_layer):
     syn = submodule("synthetic")
     cfg, bank, shared, gate = small_layer

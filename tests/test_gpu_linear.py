@@ -109,7 +109,7 @@ def test_input_layout_invariance(M, O, dev):
     scale = (rng.uniform(size=(2, 8)) * 0.002).astype(np.float32)
     w = torch.from_numpy(codes).to(dev)
     s = torch.from_numpy(scale).to(dev)
-    for tokens in (1, 7, 8, 9, 127, 128, 129):
+    for tokens in (1, 7, 8, 9, 127, 128, 129, 255, 256, 1023, 1024):
         base = from_bits(O.f32_to_bf16(rng.normal(size=(tokens, 2 * k)).astype(np.float32)), dev)
         strided = base[:, ::2]
         contiguous = strided.contiguous()
