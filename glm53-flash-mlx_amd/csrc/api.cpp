@@ -1234,7 +1234,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   size_t o_ro = take(4 * (experts + 1)), o_to = take(4 * (experts + 1)), o_status = take(8);
   size_t o_te = take(4 * p->capacity_max), o_ts = take(4 * p->capacity_max), o_tl = take(4 * p->capacity_max);
   size_t o_h = take(2 * R * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
-  size_t o_so = take(2 * T * hidden), o_flags = take(16);
+  size_t o_so = take(2 * T * hidden), o_flags = take(32);
   hipError_t e = hipMalloc(&p->arena, off);
   if (e != hipSuccess) {
     delete p;
@@ -1358,7 +1358,11 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
                             p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,
                             p->tile_start, p->tile_len, cap, p->status, p->plan_ws, st)))
     return rc;
-  // 3. grouped gate/up + SwiGLU (token rows gathered through sorted_token)
+  // 3. grouped gate/up + SwiGLU (token rows gathered through sorted_token);
+  // with a shared expert of the routed width, its dense gate/up (all T
+  // tokens, identity rows) runs in the same launch as extra descriptors, so
+  // its few items fill in beside the routed ones instead of running alone
+  const bool merge_shared = shared != nullptr && Is == I;
   GroupedGemmArgs g{};
   g.a_hi = p->xq.hi;
   g.a_lo = p->xq.lo;
@@ -1383,9 +1387,25 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   g.out = p->h;
   g.out_row_stride = I;
   g.fixup = bank_flag;
+  if (merge_shared) {
+    g.x_descriptors = cdiv(T, tile);
+    g.x_routes = T;
+    g.x_a_hi = p->xq.hi;
+    g.x_a_lo = p->xq.lo;
+    g.x_a_scale = p->xq.scale;
+    g.x_weight = shared->gate.weight;
+    g.x_weight_up = shared->up.weight;
+    g.x_scale = shared->gate.scale_inv;
+    g.x_scale_up = shared->up.scale_inv;
+    g.x_out = p->hs;
+    g.x_out_row_stride = Is;
+    HIP_TRY(launch_or_flags(p->flags + 4, bank_flag, shared_gu_flag, st), "or flags");
+    g.fixup = p->flags + 4;
+  }
   HIP_TRY(launch_grouped_gemm(g, GEMM_SWIGLU, cap, st), "grouped gate/up launch");
-  // 4. hidden -> split, 5. grouped down
+  // 4. hidden -> split, 5. grouped down (+ the shared down when merged)
   HIP_TRY(split(p->h, R, I, p->hq, st), "split hidden");
+  const int32_t* down_flag = bank->code_flags != nullptr ? bank->code_flags : p->flags + 1;
   GroupedGemmArgs d{};
   d.a_hi = p->hq.hi;
   d.a_lo = p->hq.lo;
@@ -1405,11 +1425,25 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   d.N = H;
   d.out = p->down;
   d.out_row_stride = H;
-  d.fixup = bank->code_flags != nullptr ? bank->code_flags : p->flags + 1;
+  d.fixup = down_flag;
+  if (merge_shared) {
+    HIP_TRY(split(p->hs, T, Is, p->sq, st), "split shared hidden");
+    d.x_descriptors = cdiv(T, tile);
+    d.x_routes = T;
+    d.x_a_hi = p->sq.hi;
+    d.x_a_lo = p->sq.lo;
+    d.x_a_scale = p->sq.scale;
+    d.x_weight = shared->down.weight;
+    d.x_scale = shared->down.scale_inv;
+    d.x_out = p->shared_out;
+    d.x_out_row_stride = H;
+    HIP_TRY(launch_or_flags(p->flags + 5, down_flag, shared_down_flag, st), "or flags");
+    d.fixup = p->flags + 5;
+  }
   HIP_TRY(launch_grouped_gemm(d, GEMM_PLAIN, cap, st), "grouped down launch");
-  // 6. shared expert as a dense M = T GEMM pair
-  const uint16_t* shared_add = nullptr;
-  if (shared != nullptr) {
+  // 6. a shared expert of another width as its own dense M = T GEMM pair
+  const uint16_t* shared_add = merge_shared ? p->shared_out : nullptr;
+  if (shared != nullptr && !merge_shared) {
     GroupedGemmArgs sg{};
     sg.a_hi = p->xq.hi;
     sg.a_lo = p->xq.lo;

@@ -71,6 +71,21 @@ struct GroupedGemmArgs {
   const int32_t* fixup;       // device flag: weights hold 0x7F/0xFF codes (or null)
   int tile_rows;                 // routes per descriptor: kGemmMinTileRows, or kGemmTileRows (also 0)
   int64_t n_tiles, descriptors;  // set by the launcher
+  // A dense problem run by the same launch after the routed descriptors (the
+  // shared expert): x_descriptors implicit descriptors of tile_rows rows over
+  // rows 0 .. x_routes - 1 (identity activation rows), with its own
+  // activation planes, weights, block scales and output; same K, N and scale
+  // layout as the routed problem.  x_descriptors = 0: none.
+  int64_t x_descriptors, x_routes;
+  const uint8_t* x_a_hi;
+  const uint8_t* x_a_lo;
+  const float* x_a_scale;
+  const uint8_t* x_weight;
+  const uint8_t* x_weight_up;
+  const float* x_scale;
+  const float* x_scale_up;
+  uint16_t* x_out;
+  int64_t x_out_row_stride;
 };
 
 struct ReduceArgs {

@@ -306,8 +306,28 @@ __device__ __forceinline__ i32x8 lds_operand(const uint8_t* tile, OperandSlots o
 
 }  // namespace
 
+// What a work item reads and writes: the routed problem's operands or the
+// dense problem's (GroupedGemmArgs.x_*), chosen per item.
+struct ItemSource {
+  const uint8_t* a_hi;
+  const uint8_t* a_lo;
+  const float* a_scale;
+  const int32_t* a_row_index;
+  int64_t routes;
+  const int32_t* tile_expert;
+  const int32_t* tile_start;
+  const int32_t* tile_len;
+  int64_t experts;
+  const uint8_t* weight;
+  const uint8_t* weight_up;
+  const float* scale;
+  const float* scale_up;
+  uint16_t* out;
+  int64_t out_row_stride;
+};
+
 template <int MODE, bool FIX, int GPW, int NGW>
-__device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int64_t ntile, int32_t start, int32_t len,
+__device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile, int32_t start, int32_t len,
                                                   int64_t KB, const uint8_t* const (&gb)[2][2],
                                                   const uint8_t* const (&ga)[GPW][2], uint8_t* lds, uint32_t lds_addr,
                                                   const float* lds_sa, const float* lds_sw, int wave, int lane) {
@@ -397,7 +417,7 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
     for (int h = 0; h < 2; ++h) {
       const int r = g * 8 + 2 * kq + h;
       if (r >= len) continue;
-      uint16_t* orow = a.out + (static_cast<int64_t>(start) + r) * a.out_row_stride;
+      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
       if (MODE == GEMM_PLAIN) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -416,24 +436,25 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, int6
 }
 
 template <int MODE, bool FIX, int GPW>
-__device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int64_t ntile, int64_t d, uint8_t* lds) {
+__device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile, int64_t d,
+                                                  uint8_t* lds) {
   constexpr int kRoutes = 32 * GPW;  // routes per descriptor
   constexpr int kStage = stage_bytes<GPW>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int32_t expert, start, len;
-  if (a.tile_expert != nullptr) {
-    expert = a.tile_expert[d];
-    start = a.tile_start[d];
-    len = a.tile_len[d];
-    if (start >= a.routes || len <= 0) return;
-    if (expert < 0 || expert >= a.experts) return;
+  if (src.tile_expert != nullptr) {
+    expert = src.tile_expert[d];
+    start = src.tile_start[d];
+    len = src.tile_len[d];
+    if (start >= src.routes || len <= 0) return;
+    if (expert < 0 || expert >= src.experts) return;
     if (len > kRoutes) len = kRoutes;
-    if (start + len > a.routes) len = static_cast<int32_t>(a.routes - start);
+    if (start + len > src.routes) len = static_cast<int32_t>(src.routes - start);
   } else {
     expert = 0;
     start = static_cast<int32_t>(d * kRoutes);
-    len = static_cast<int32_t>(a.routes - start < kRoutes ? a.routes - start : kRoutes);
+    len = static_cast<int32_t>(src.routes - start < kRoutes ? src.routes - start : kRoutes);
     if (len <= 0) return;
   }
   const int64_t K = a.K;
@@ -447,16 +468,16 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
   // tiles 64-aligned within one block)
   auto token_of = [&](int r) -> int64_t {
     const int64_t route = start + (r < len ? r : len - 1);
-    return a.a_row_index != nullptr ? a.a_row_index[route] : route;
+    return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
   for (int64_t i = threadIdx.x; i < kRoutes * KB; i += 256) {
     const int r = static_cast<int>(i / KB);
-    lds_sa[i] = a.a_scale[token_of(r) * KB + (i - r * KB)];
+    lds_sa[i] = src.a_scale[token_of(r) * KB + (i - r * KB)];
   }
   const int64_t srow = MODE == GEMM_PLAIN ? ntile : (ntile >> 1);
   const int64_t soff = static_cast<int64_t>(expert) * a.s_expert_stride + srow * a.s_cols;
   for (int64_t i = threadIdx.x; i < (MODE == GEMM_SWIGLU ? 2 : 1) * KB; i += 256)
-    lds_sw[i] = i < KB ? a.scale[soff + i] : a.scale_up[soff + i - KB];
+    lds_sw[i] = i < KB ? src.scale[soff + i] : src.scale_up[soff + i - KB];
   __syncthreads();
 
   // ---- per-lane global sources of the direct loads: load h of a tile
@@ -467,10 +488,10 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
     const uint8_t* w;
     if (MODE == GEMM_PLAIN) {
       row = ntile * kTileRows + t * 16 + rr;
-      w = a.weight;
+      w = src.weight;
     } else {
       row = ntile * (kTileRows / 2) + (t & 3) * 16 + rr;
-      w = t < 4 ? a.weight : a.weight_up;
+      w = t < 4 ? src.weight : src.weight_up;
     }
     if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
     return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + load_piece_offset(lane, h);
@@ -487,7 +508,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
   for (int h = 0; h < 2; ++h) {
     const int rho = 8 * h + (lane >> 3);
     const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
-    const uint8_t* plane = (rho & 1) ? a.a_lo : a.a_hi;
+    const uint8_t* plane = (rho & 1) ? src.a_lo : src.a_hi;
 #pragma unroll
     for (int j = 0; j < GPW; ++j) ga[j][h] = plane + token_of((GPW * wave + j) * 8 + rt) * K + load_piece_offset(lane, h);
   }
@@ -495,7 +516,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, int6
   int ngw = groups - GPW * wave;  // wave-uniform
   ngw = ngw < 0 ? 0 : (ngw > GPW ? GPW : ngw);
 #define GLM53_LOOP(n) \
-  grouped_gemm_loop<MODE, FIX, GPW, n>(a, ntile, start, len, KB, gb, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
+  grouped_gemm_loop<MODE, FIX, GPW, n>(a, src, ntile, start, len, KB, gb, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
   if (GPW >= 2 && ngw == 2) GLM53_LOOP(GPW >= 2 ? 2 : 0);
   else if (ngw == 1) GLM53_LOOP(1);
   else GLM53_LOOP(0);
@@ -515,13 +536,33 @@ size_t gemm_lds_bytes(int64_t K) {
 template <int MODE, int GPW>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
-  const int64_t items = a.n_tiles * a.descriptors;
+  const int64_t D = a.descriptors + a.x_descriptors;
+  const int64_t items = a.n_tiles * D;
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (w >= items) return;
-  const int64_t ntile = w / a.descriptors, d = w % a.descriptors;
-  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true, GPW>(a, ntile, d, lds_dyn);
-  else grouped_gemm_body<MODE, false, GPW>(a, ntile, d, lds_dyn);
+  const int64_t ntile = w / D;
+  int64_t d = w % D;
+  const bool dense = d >= a.descriptors;  // an item of the dense problem
+  if (dense) d -= a.descriptors;
+  ItemSource src;
+  src.a_hi = dense ? a.x_a_hi : a.a_hi;
+  src.a_lo = dense ? a.x_a_lo : a.a_lo;
+  src.a_scale = dense ? a.x_a_scale : a.a_scale;
+  src.a_row_index = dense ? nullptr : a.a_row_index;
+  src.routes = dense ? a.x_routes : a.routes;
+  src.tile_expert = dense ? nullptr : a.tile_expert;
+  src.tile_start = a.tile_start;
+  src.tile_len = a.tile_len;
+  src.experts = dense ? 1 : a.experts;
+  src.weight = dense ? a.x_weight : a.weight;
+  src.weight_up = dense ? a.x_weight_up : a.weight_up;
+  src.scale = dense ? a.x_scale : a.scale;
+  src.scale_up = dense ? a.x_scale_up : a.scale_up;
+  src.out = dense ? a.x_out : a.out;
+  src.out_row_stride = dense ? a.x_out_row_stride : a.out_row_stride;
+  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true, GPW>(a, src, ntile, d, lds_dyn);
+  else grouped_gemm_body<MODE, false, GPW>(a, src, ntile, d, lds_dyn);
 }
 
 // Sets *flag (pre-cleared by clear_flag_kernel) when any byte of codes is
@@ -622,11 +663,11 @@ hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st) {
-  if (descriptors == 0) return hipSuccess;
+  if (descriptors == 0 && a.x_descriptors == 0) return hipSuccess;
   GroupedGemmArgs g = a;
   g.n_tiles = mode == GEMM_PLAIN ? (a.N + 127) / 128 : (a.N + 63) / 64;
   g.descriptors = descriptors;
-  const int64_t items = g.n_tiles * descriptors;
+  const int64_t items = g.n_tiles * (descriptors + g.x_descriptors);
   const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
   if (a.tile_rows != 0 && a.tile_rows != kGemmMinTileRows && a.tile_rows != kGemmTileRows)
     return hipErrorInvalidValue;

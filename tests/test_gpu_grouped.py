@@ -242,3 +242,21 @@ def test_skewed_routing_many_descriptors_matches_oracle(M, O, dev, reduction):
         assert_parity(to_bits(y).reshape(T, -1), want_g, O, exact_fraction=0.75)
     else:
         assert stats["bit_exact_fraction"] >= 0.75, stats
+
+
+@pytest.mark.parametrize("shared_experts", [1, 2])
+def test_prefill_shared_expert_merged_or_separate_matches_oracle(M, O, dev, shared_experts):
+    """A shared expert of the routed width runs as extra dense descriptors
+    inside the routed GEMM launches; two shared experts (width 2 I) take the
+    separate dense GEMM pair.  Both against the oracle's Direct MoE."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0, shared=shared_experts)
+    bank, shared, gate = syn.synth_layer(cfg, seed=51 + shared_experts, device=dev)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    T = 96
+    x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(51, shared_experts), device=dev)
+    y = moe(x)
+    ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
+    xb = to_bits(x).reshape(T, -1)
+    want = O.direct_moe(xb, host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
