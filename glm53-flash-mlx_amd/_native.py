@@ -95,6 +95,7 @@ _SIGNATURES = {
     "glm53_sigmoid_bf16": (ctypes.c_int, [P, I64, P, P]),
     "glm53_restore_and_reduce": (ctypes.c_int, [P, P, P, I64, I64, I64, P, P, P]),
     "glm53_direct_order_reduce": (ctypes.c_int, [P, P, P, P, I64, I64, I64, P, P, P]),
+    "glm53_split_activations": (ctypes.c_int, [P, I64, I64, I64, P, P, P, P]),
     "glm53_prefill_plan_create": (ctypes.c_int, [I64, I64, I64, I64, I64, I64, F32, P]),
     "glm53_prefill_plan_destroy": (None, [P]),
     "glm53_prefill_moe": (ctypes.c_int, [P, P, P, P, P, I64, P, P, I32, P, P]),

@@ -1061,6 +1061,27 @@ int glm53_route_plan(const int32_t* expert_ids, const float* scores, int64_t rou
                          capacity, status, workspace, S(stream));
 }
 
+int glm53_split_activations(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, uint8_t* hi, uint8_t* lo,
+                            float* scale, void* stream) {
+  CHECK_ARG(rows >= 0 && cols > 0 && cols % 128 == 0 && x_row_stride >= cols,
+            "split needs cols a positive multiple of 128 and x_row_stride >= cols; got cols=%lld, stride=%lld",
+            (long long)cols, (long long)x_row_stride);
+  if (rows == 0) return GLM53_OK;
+  CHECK_ARG(x && hi && lo && scale, "null pointer argument");
+  CHECK_ARG(aligned(x, 2) && aligned(hi, 8) && aligned(lo, 8) && aligned(scale, 4),
+            "x must be 2-byte, hi and lo 8-byte, scale 4-byte aligned");
+  SplitArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.x_row_stride = x_row_stride;
+  a.rows = rows;
+  a.cols = cols;
+  a.hi = hi;
+  a.lo = lo;
+  a.scale = scale;
+  HIP_TRY(launch_split_activations(a, S(stream)), "split launch");
+  return GLM53_OK;
+}
+
 size_t glm53_grouped_linear_workspace_bytes(int64_t act_rows, int64_t K) {
   if (K % 128 != 0) return 0;
   return split_bytes(act_rows, K) + 256;

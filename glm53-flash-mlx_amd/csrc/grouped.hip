@@ -167,19 +167,90 @@ __device__ __forceinline__ float e4m3_value(uint32_t code) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h)) * 256.0f;
 }
 
-// One wavefront per (row, 128-column block): two elements per lane.
+// Hardware E4M3 conversion of a pair (q0, q1), both |q| <= 448, into bytes
+// 0-1 (kUpper false) or 2-3 of hi_word, and of their residuals 16 (q - hi)
+// into the same bytes of lo_word; the other bytes are kept.
+template <bool kUpper>
+__device__ __forceinline__ void encode_pair_e4m3(float q0, float q1, uint32_t& hi_word, uint32_t& lo_word) {
+  const int h = __builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, static_cast<int>(hi_word), kUpper);
+  hi_word = static_cast<uint32_t>(h);
+  const float r0 = (q0 - __builtin_amdgcn_cvt_f32_fp8(h, kUpper ? 2 : 0)) * 16.0f;
+  const float r1 = (q1 - __builtin_amdgcn_cvt_f32_fp8(h, kUpper ? 3 : 1)) * 16.0f;
+  lo_word = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, static_cast<int>(lo_word), kUpper));
+}
+
+// V consecutive BF16 values as raw words: V = 8 is one 16-byte load (the
+// pointer 16-byte aligned), V = 1 or 2 are 2-byte loads.
+template <int V>
+struct Bf16Run {
+  uint32_t w[(V + 1) / 2];
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    if constexpr (V == 8) {
+      const uint4 r = *reinterpret_cast<const uint4*>(p);
+      w[0] = r.x, w[1] = r.y, w[2] = r.z, w[3] = r.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < (V + 1) / 2; ++i) w[i] = 0u;
+#pragma unroll
+      for (int i = 0; i < V; ++i) w[i >> 1] |= static_cast<uint32_t>(p[i]) << (16 * (i & 1));
+    }
+  }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int i = 0; i < (V + 1) / 2; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ float get(int i) const {
+    return __uint_as_float(i & 1 ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+  }
+};
+
+// Rounds V floats to BF16 and stores them (one 16-byte store for V = 8).
+template <int V>
+__device__ __forceinline__ void store_bf16_run(uint16_t* p, const float* v) {
+  if constexpr (V == 8) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(o[0], o[1], o[2], o[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) p[i] = f32_to_bf16(v[i]);
+  }
+}
+
+// Wavefront = one row x (V / 2) consecutive 128-column blocks; lane l holds
+// V columns of block l / (128 / V).  V = 8 (16-byte loads, each block's amax
+// a reduction over one 16-lane DPP row) when the rows are 16-byte aligned,
+// V = 2 (one block per wavefront) otherwise.
+template <int V>
 __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
+  constexpr int kLanesPerBlock = kBlock / V;
+  constexpr int kBlocksPerWave = 64 / kLanesPerBlock;
   const int lane = threadIdx.x & 63;
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t blocks_per_row = a.cols / kBlock;
-  if (unit >= a.rows * blocks_per_row) return;
-  const int64_t row = unit / blocks_per_row;
-  const int64_t blk = unit % blocks_per_row;
-  const uint16_t* src = a.x + row * a.x_row_stride + blk * kBlock + 2 * lane;
-  uint32_t pair = *reinterpret_cast<const uint32_t*>(src);
-  float v0 = __uint_as_float(pair << 16);
-  float v1 = __uint_as_float(pair & 0xffff0000u);
-  float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+  const int64_t groups = (blocks_per_row + kBlocksPerWave - 1) / kBlocksPerWave;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (unit >= a.rows * groups) return;
+  const int64_t row = unit / groups;
+  const int64_t blk = (unit % groups) * kBlocksPerWave + lane / kLanesPerBlock;
+  const bool valid = blk < blocks_per_row;
+  const int64_t col = blk * kBlock + V * (lane % kLanesPerBlock);
+  Bf16Run<V> x;
+  x.clear();
+  if (valid) x.load(a.x + row * a.x_row_stride + col);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) amax = fmaxf(amax, fabsf(x.get(i)));
+  if constexpr (kLanesPerBlock == 64) {
+    amax = wave_max(amax);
+  } else {
+    static_assert(kLanesPerBlock == 16, "a block spans one DPP row or the whole wavefront");
+    amax = fmaxf(amax, dpp_f32<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f32<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_f32<0x141>(amax));  // row_half_mirror
+    amax = fmaxf(amax, dpp_f32<0x140>(amax));  // row_mirror: the block's amax in all 16 lanes
+  }
   // s = 2^ceil(log2(amax / 448)): amax / s lies in (224, 448].
   float s = 1.0f;
   if (amax > 0.0f && isfinite(amax)) {
@@ -189,14 +260,43 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
     if (amax / s > 448.0f) s = ldexpf(1.0f, e + 1);
   }
   const float inv = 1.0f / s;
-  float q0 = v0 * inv, q1 = v1 * inv;
-  uint32_t h0 = encode_e4m3(q0), h1 = encode_e4m3(q1);
-  uint32_t l0 = encode_e4m3((q0 - e4m3_value(h0)) * 16.0f);
-  uint32_t l1 = encode_e4m3((q1 - e4m3_value(h1)) * 16.0f);
-  const int64_t off = row * a.cols + blk * kBlock + 2 * lane;
-  *reinterpret_cast<uint16_t*>(a.hi + off) = static_cast<uint16_t>(h0 | (h1 << 8));
-  *reinterpret_cast<uint16_t*>(a.lo + off) = static_cast<uint16_t>(l0 | (l1 << 8));
-  if (lane == 0) a.scale[row * blocks_per_row + blk] = s;
+  float q[V];
+  bool in_range = true;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    q[i] = x.get(i) * inv;
+    in_range = in_range && fabsf(q[i]) <= 448.0f;
+  }
+  uint32_t hi[(V + 3) / 4] = {}, lo[(V + 3) / 4] = {};
+  if (in_range) {
+    // Every |q| <= 448 is on the E4M3 range, where the hardware conversion
+    // (OCP E4M3, round to nearest even) is encode_e4m3; the residual
+    // |q - hi| <= 16 makes 16 (q - hi) lie within +-256.
+#pragma unroll
+    for (int w = 0; w < (V + 3) / 4; ++w) {
+      encode_pair_e4m3<false>(q[4 * w], q[4 * w + 1], hi[w], lo[w]);
+      if constexpr (V >= 4) encode_pair_e4m3<true>(q[4 * w + 2], q[4 * w + 3], hi[w], lo[w]);
+    }
+  } else {  // a non-finite or saturating value in this lane
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const uint32_t h = encode_e4m3(q[i]);
+      const uint32_t l = encode_e4m3((q[i] - e4m3_value(h)) * 16.0f);
+      hi[i >> 2] |= h << (8 * (i & 3));
+      lo[i >> 2] |= l << (8 * (i & 3));
+    }
+  }
+  if (!valid) return;
+  const int64_t off = row * a.cols + col;
+  if constexpr (V == 8) {
+    *reinterpret_cast<uint2*>(a.hi + off) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2*>(a.lo + off) = make_uint2(lo[0], lo[1]);
+  } else {
+    static_assert(V == 2, "narrow split handles two columns per lane");
+    *reinterpret_cast<uint16_t*>(a.hi + off) = static_cast<uint16_t>(hi[0]);
+    *reinterpret_cast<uint16_t*>(a.lo + off) = static_cast<uint16_t>(lo[0]);
+  }
+  if (lane % kLanesPerBlock == 0) a.scale[row * blocks_per_row + blk] = s;
 }
 
 // --------------------------------------------------------- grouped GEMM --
@@ -593,27 +693,61 @@ __global__ __launch_bounds__(256) void scan_480_kernel(const uint8_t* codes, int
 
 // grouped_fp8.py:273-276: y[t] = T(sum_slot float(down[inv[t*k+slot]]) *
 // score), FP32 products summed in slot order, optional BF16 shared add.
+// Thread = V consecutive columns of one token (V = 8: 16-byte loads and
+// stores, when H and the row pointers allow it; V = 1 otherwise).  The
+// token's positions and scores are read first (uniform across the
+// workgroup), then every slot's row is requested before the first is summed,
+// so the row loads overlap instead of each waiting behind the last.
+template <int V, int K>
 __global__ __launch_bounds__(256) void restore_reduce_kernel(ReduceArgs a) {
+  constexpr int kSlots = K > 0 ? K : kMaxReduceTopK;  // K = 0: top_k known only at run time
+  const int k = K > 0 ? K : a.top_k;
   const int64_t t = blockIdx.y;
-  const int64_t h = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (h >= a.H) return;
-  float total = 0.0f;
-  for (int s = 0; s < a.top_k; ++s) {
-    const int32_t pos = a.inverse[t * a.top_k + s];
-    const float v = pos < 0 ? __builtin_nanf("") : bf16_to_f32(a.route_out[static_cast<int64_t>(pos) * a.H + h]);
-    total = __fadd_rn(total, __fmul_rn(v, a.sorted_score[pos < 0 ? 0 : pos]));
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * V;
+  if (h0 >= a.H) return;
+  int32_t pos[kSlots];
+  float score[kSlots];
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) pos[s] = s < k ? a.inverse[t * k + s] : 0;
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) score[s] = s < k ? a.sorted_score[pos[s] < 0 ? 0 : pos[s]] : 0.0f;
+  Bf16Run<V> row[kSlots];
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {  // a missing route (pos < 0) reads row 0 and sums NaN
+    row[s].clear();
+    if (s < k) row[s].load(a.route_out + static_cast<int64_t>(pos[s] < 0 ? 0 : pos[s]) * a.H + h0);
   }
-  float r = bf16_round(total);
-  if (a.shared != nullptr) r = __fadd_rn(r, bf16_to_f32(a.shared[t * a.H + h]));
-  a.out[t * a.H + h] = f32_to_bf16(r);
+  float total[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) total[i] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    if (s >= k) continue;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float v = pos[s] < 0 ? __builtin_nanf("") : row[s].get(i);
+      total[i] = __fadd_rn(total[i], __fmul_rn(v, score[s]));
+    }
+  }
+  Bf16Run<V> sh;
+  sh.clear();
+  if (a.shared != nullptr) sh.load(a.shared + t * a.H + h0);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    total[i] = bf16_round(total[i]);
+    if (a.shared != nullptr) total[i] = __fadd_rn(total[i], sh.get(i));
+  }
+  store_bf16_run<V>(a.out + t * a.H + h0, total);
 }
 
 // native_indexer_plan.metal:2174-2207 (fp8.py:384-397 order): per token,
 // ascending expert id; contribution = T(down * score); total = T(total + c).
+// Thread = V consecutive columns; loads are issued as above, in sorted order.
+template <int V>
 __global__ __launch_bounds__(256) void direct_order_reduce_kernel(ReduceArgs a) {
   const int64_t t = blockIdx.y;
-  const int64_t h = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (h >= a.H) return;
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * V;
+  if (h0 >= a.H) return;
   int32_t slot_ids[kMaxReduceTopK];
   int order[kMaxReduceTopK];
   for (int s = 0; s < a.top_k; ++s) {
@@ -629,17 +763,38 @@ __global__ __launch_bounds__(256) void direct_order_reduce_kernel(ReduceArgs a) 
     }
     order[j + 1] = v;
   }
-  float total = 0.0f;
-  for (int r = 0; r < a.top_k; ++r) {
-    const int64_t route = t * a.top_k + order[r];
-    const int32_t pos = a.inverse[route];
-    const float v = pos < 0 ? __builtin_nanf("") : bf16_to_f32(a.route_out[static_cast<int64_t>(pos) * a.H + h]);
-    const float c = bf16_round(__fmul_rn(v, a.route_score[route]));
-    total = bf16_round(__fadd_rn(total, c));
+  int32_t pos[kMaxReduceTopK];
+  float score[kMaxReduceTopK];
+#pragma unroll
+  for (int r = 0; r < kMaxReduceTopK; ++r) pos[r] = a.inverse[t * a.top_k + (r < a.top_k ? order[r] : 0)];
+#pragma unroll
+  for (int r = 0; r < kMaxReduceTopK; ++r) score[r] = a.route_score[t * a.top_k + (r < a.top_k ? order[r] : 0)];
+  Bf16Run<V> row[kMaxReduceTopK];
+#pragma unroll
+  for (int r = 0; r < kMaxReduceTopK; ++r) {
+    row[r].clear();
+    if (r < a.top_k) row[r].load(a.route_out + static_cast<int64_t>(pos[r] < 0 ? 0 : pos[r]) * a.H + h0);
   }
-  float r = total;
-  if (a.shared != nullptr) r = __fadd_rn(r, bf16_to_f32(a.shared[t * a.H + h]));
-  a.out[t * a.H + h] = f32_to_bf16(r);
+  float total[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) total[i] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kMaxReduceTopK; ++r) {
+    if (r >= a.top_k) continue;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float v = pos[r] < 0 ? __builtin_nanf("") : row[r].get(i);
+      const float c = bf16_round(__fmul_rn(v, score[r]));
+      total[i] = bf16_round(__fadd_rn(total[i], c));
+    }
+  }
+  Bf16Run<V> sh;
+  sh.clear();
+  if (a.shared != nullptr) sh.load(a.shared + t * a.H + h0);
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    if (a.shared != nullptr) total[i] = __fadd_rn(total[i], sh.get(i));
+  store_bf16_run<V>(a.out + t * a.H + h0, total);
 }
 
 // ------------------------------------------------------------- launchers --
@@ -656,9 +811,14 @@ hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st) {
-  const int64_t units = a.rows * (a.cols / kBlock);
-  if (units == 0) return hipSuccess;
-  hipLaunchKernelGGL(split_activations_kernel, dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256), 0, st, a);
+  if (a.rows == 0) return hipSuccess;
+  if (a.cols % kBlock != 0) return hipErrorInvalidValue;
+  const bool wide = a.x_row_stride % 8 == 0 && reinterpret_cast<uintptr_t>(a.x) % 16 == 0;
+  const int64_t blocks_per_row = a.cols / kBlock;
+  const int64_t units = a.rows * (wide ? (blocks_per_row + 3) / 4 : blocks_per_row);  // wavefronts
+  const dim3 grid(static_cast<unsigned>((units + 3) / 4));
+  if (wide) hipLaunchKernelGGL(split_activations_kernel<8>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(split_activations_kernel<2>, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -704,9 +864,19 @@ hipError_t launch_or_flags(int32_t* dst, const int32_t* a, const int32_t* b, hip
 
 hipError_t launch_reduce(const ReduceArgs& a, bool direct_order, hipStream_t st) {
   if (a.tokens == 0) return hipSuccess;
-  dim3 grid(static_cast<unsigned>((a.H + 255) / 256), static_cast<unsigned>(a.tokens));
-  if (direct_order) hipLaunchKernelGGL(direct_order_reduce_kernel, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(restore_reduce_kernel, grid, dim3(256), 0, st, a);
+  if (a.top_k > kMaxReduceTopK) return hipErrorInvalidValue;
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool wide = a.H % 8 == 0 && a16(a.route_out) && a16(a.out) && a16(a.shared);
+  const int64_t per_thread = wide ? 8 : 1;
+  const dim3 grid(static_cast<unsigned>((a.H / per_thread + 255) / 256), static_cast<unsigned>(a.tokens));
+  if (wide) {
+    if (direct_order) hipLaunchKernelGGL(direct_order_reduce_kernel<8>, grid, dim3(256), 0, st, a);
+    else if (a.top_k == 8) hipLaunchKernelGGL((restore_reduce_kernel<8, 8>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((restore_reduce_kernel<8, 0>), grid, dim3(256), 0, st, a);
+  } else {
+    if (direct_order) hipLaunchKernelGGL(direct_order_reduce_kernel<1>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((restore_reduce_kernel<1, 0>), grid, dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

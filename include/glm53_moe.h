@@ -247,6 +247,19 @@ int glm53_route_plan(const int32_t* expert_ids, const float* scores, int64_t rou
                      int32_t* tile_start, int32_t* tile_len, int64_t capacity, uint32_t* status,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Activation split feeding the grouped FP8 GEMM.  No counterpart in the
+ * reference, which multiplies BF16 activations by the dequantised weights
+ * (grouped_fp8.py:206-262); exported so the encoding can be checked bit for
+ * bit.  Per row and 128-column block: s = 2^ceil(log2(amax / 448)), so
+ * amax / s lies in (224, 448] (s = 1 for an all-zero or non-finite amax);
+ * q = x / s; hi = E4M3(q); lo = E4M3(16 (q - hi)), both round to nearest
+ * even, saturating at +-448 (never the 0x7F / 0xFF codes); x ~= s (hi +
+ * lo / 16).  x bf16 rows of x_row_stride elements (2-byte aligned), hi and
+ * lo u8 [rows, cols] (8-byte aligned), scale f32 [rows, cols / 128].
+ * Requires cols % 128 == 0. */
+int glm53_split_activations(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride, uint8_t* hi,
+                            uint8_t* lo, float* scale, void* stream);
+
 /* grouped_fp8_linear (grouped_fp8.py:206-262): y[r] = T(x[row(r)] .
  * W[e(r)]^T) for sorted routes r, where row(r) = row_index[r] (NULL:
  * identity) and e(r) comes from the 32-route descriptors.  x bf16

@@ -105,6 +105,71 @@ def test_grouped_linear_matches_oracle(M, O, dev):
     assert np.array_equal(to_bits(out), want_out)
 
 
+def _place(bits, offset, dev):
+    """Device BF16 copy of `bits` starting `offset` elements into its buffer
+    (offset 1 leaves the rows 2-byte aligned only)."""
+    import torch
+
+    buf = torch.zeros(bits.size + offset, dtype=torch.bfloat16, device=dev)
+    view = buf[offset:].view(bits.shape)
+    view.copy_(from_bits(bits, dev))
+    return view
+
+
+@pytest.mark.parametrize("hidden,offset", [(256, 0), (256, 1), (200, 0)])
+def test_reductions_at_any_width_and_alignment_match_oracle(M, O, dev, hidden, offset):
+    """Slot-order and ascending-expert reductions with the shared add: 16-byte
+    aligned rows with H % 8 == 0 take the 8-column form, the rest the
+    1-column form; both match the oracle bit for bit."""
+    import torch
+
+    N = submodule("_native")
+    rng = np.random.default_rng(31 + hidden + offset)
+    tokens, k = 37, 8
+    route = O.f32_to_bf16(rng.normal(size=(tokens * k, hidden)).astype(np.float32))
+    shared = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    ids = np.stack([rng.choice(32, size=k, replace=False) for _ in range(tokens)]).astype(np.int32)
+    scores = rng.uniform(size=(tokens, k)).astype(np.float32)
+    route_d, shared_d = _place(route, offset, dev), _place(shared, offset, dev)
+    inverse = torch.arange(tokens * k, dtype=torch.int32, device=dev)
+    scores_d = torch.from_numpy(scores.reshape(-1)).to(dev)
+    ids_d = torch.from_numpy(ids.reshape(-1)).to(dev)
+    lib, st = N.lib(), N.stream_handle(dev)
+    out = _place(np.zeros((tokens, hidden), np.uint16), offset, dev)
+    N.check(lib.glm53_restore_and_reduce(N.ptr(route_d), N.ptr(scores_d), N.ptr(inverse), tokens, k, hidden,
+                                         N.ptr(shared_d), N.ptr(out), st))
+    want = O.add_bf16(O.restore_and_reduce(route, scores.reshape(-1), np.arange(tokens * k), tokens, k), shared)
+    assert np.array_equal(to_bits(out), want)
+    out = _place(np.zeros((tokens, hidden), np.uint16), offset, dev)
+    N.check(lib.glm53_direct_order_reduce(N.ptr(route_d), N.ptr(inverse), N.ptr(ids_d), N.ptr(scores_d), tokens, k,
+                                          hidden, N.ptr(shared_d), N.ptr(out), st))
+    want = O.add_bf16(O.direct_order_reduce(route, ids, scores), shared)
+    assert np.array_equal(to_bits(out), want)
+
+
+def test_grouped_linear_unaligned_activations_split_alike(M, O, dev):
+    """Activation rows that are only 2-byte aligned take the two-column split;
+    the GEMM output equals the aligned run bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(13)
+    bank = _small_bank(M, dev, rng, 8, 384, 128)  # 3 blocks per row: a partial group of 4 in the wide split
+    tokens = 24
+    ids = np.stack([rng.choice(8, size=8, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = from_bits(O.f32_to_bf16(rng.normal(size=(tokens, 384)).astype(np.float32)), dev)
+    sorted_x, sorted_e, _, _ = M.build_route_plan(x, torch.from_numpy(ids).to(dev), torch.ones(ids.shape, device=dev))
+    tile_plan = M.build_grouped_tile_plan(sorted_e, 8)
+    y = M.grouped_fp8_linear(sorted_x, tile_plan, bank.gate_up_weight, bank.gate_up_scale_inv)
+    shifted = _place(to_bits(sorted_x), 1, dev)
+    assert shifted.data_ptr() % 16 != 0
+    y_shifted = M.grouped_fp8_linear(shifted, tile_plan, bank.gate_up_weight, bank.gate_up_scale_inv)
+    assert np.array_equal(to_bits(y_shifted), to_bits(y))
+    plan = O.build_route_plan(ids, np.ones(ids.shape, np.float32))
+    want = O.grouped_linear(to_bits(x)[plan.token_ids], plan.sorted_experts, bank.gate_up_weight.cpu().numpy(),
+                            bank.gate_up_scale_inv.cpu().numpy())
+    assert_parity(to_bits(y), want, O, exact_fraction=0.95)
+
+
 class DeterministicGate:
     """tests/test_fp8_metal.py:160-166 of the reference."""
 
