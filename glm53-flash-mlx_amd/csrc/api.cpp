@@ -1350,18 +1350,19 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     HIP_TRY(launch_scan_480(bank->down_weight, E * H * I, p->flags + 1, true, st), "scan bank");
     bank_flag = p->flags;
   }
-  // shared gate and up share one MFMA call, so their flags are OR-ed
-  const int32_t* shared_gu_flag = nullptr;
+  // shared gate and up share one MFMA call; the GEMM ORs their two flags
+  const int32_t* shared_gate_flag = nullptr;
+  const int32_t* shared_up_flag = nullptr;
   const int32_t* shared_down_flag = nullptr;
   if (shared != nullptr) {
-    int32_t* fgu = p->flags + 2;
     if (shared->gate.code_flags != nullptr && shared->up.code_flags != nullptr) {
-      HIP_TRY(launch_or_flags(fgu, shared->gate.code_flags, shared->up.code_flags, st), "or flags");
+      shared_gate_flag = shared->gate.code_flags;
+      shared_up_flag = shared->up.code_flags;
     } else {
-      HIP_TRY(launch_scan_480(shared->gate.weight, Is * H, fgu, true, st), "scan shared gate");
-      HIP_TRY(launch_scan_480(shared->up.weight, Is * H, fgu, false, st), "scan shared up");
+      HIP_TRY(launch_scan_480(shared->gate.weight, Is * H, p->flags + 2, true, st), "scan shared gate");
+      HIP_TRY(launch_scan_480(shared->up.weight, Is * H, p->flags + 2, false, st), "scan shared up");
+      shared_gate_flag = p->flags + 2;
     }
-    shared_gu_flag = fgu;
     shared_down_flag = shared->down.code_flags;
     if (shared_down_flag == nullptr) {
       HIP_TRY(launch_scan_480(shared->down.weight, H * Is, p->flags + 3, true, st), "scan shared down");
@@ -1420,8 +1421,8 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     g.x_scale_up = shared->up.scale_inv;
     g.x_out = p->hs;
     g.x_out_row_stride = Is;
-    HIP_TRY(launch_or_flags(p->flags + 4, bank_flag, shared_gu_flag, st), "or flags");
-    g.fixup = p->flags + 4;
+    g.x_fixup = shared_gate_flag;
+    g.x_fixup_up = shared_up_flag;
   }
   HIP_TRY(launch_grouped_gemm(g, GEMM_SWIGLU, cap, st), "grouped gate/up launch");
   // 4. hidden -> split, 5. grouped down (+ the shared down when merged)
@@ -1458,8 +1459,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     d.x_scale = shared->down.scale_inv;
     d.x_out = p->shared_out;
     d.x_out_row_stride = H;
-    HIP_TRY(launch_or_flags(p->flags + 5, down_flag, shared_down_flag, st), "or flags");
-    d.fixup = p->flags + 5;
+    d.x_fixup = shared_down_flag;
   }
   HIP_TRY(launch_grouped_gemm(d, GEMM_PLAIN, cap, st), "grouped down launch");
   // 6. a shared expert of another width as its own dense M = T GEMM pair
@@ -1481,7 +1481,8 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
     sg.limit = p->limit;
     sg.out = p->hs;
     sg.out_row_stride = Is;
-    sg.fixup = shared_gu_flag;
+    sg.fixup = shared_gate_flag;
+    sg.fixup_up = shared_up_flag;
     const int stile = T >= 16 * kGemmTileRows ? kGemmTileRows : kGemmMinTileRows;
     sg.tile_rows = stile;
     HIP_TRY(launch_grouped_gemm(sg, GEMM_SWIGLU, cdiv(T, stile), st), "shared gate/up launch");

@@ -69,6 +69,7 @@ struct GroupedGemmArgs {
   uint16_t* out;              // [routes, out_row_stride] bf16
   int64_t out_row_stride;
   const int32_t* fixup;       // device flag: weights hold 0x7F/0xFF codes (or null)
+  const int32_t* fixup_up;    // SwiGLU mode: the up weights' flag when kept apart (or null)
   int tile_rows;                 // routes per descriptor: kGemmMinTileRows, or kGemmTileRows (also 0)
   int64_t n_tiles, descriptors;  // set by the launcher
   // A dense problem run by the same launch after the routed descriptors (the
@@ -86,6 +87,8 @@ struct GroupedGemmArgs {
   const float* x_scale_up;
   uint16_t* x_out;
   int64_t x_out_row_stride;
+  const int32_t* x_fixup;     // the dense problem's weight flags (either may be null)
+  const int32_t* x_fixup_up;
 };
 
 struct ReduceArgs {
@@ -105,6 +108,5 @@ hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st);
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st);
 hipError_t launch_reduce(const ReduceArgs& a, bool direct_order, hipStream_t st);
 hipError_t launch_scan_480(const uint8_t* codes, int64_t n, int32_t* flag, bool clear, hipStream_t st);
-hipError_t launch_or_flags(int32_t* dst, const int32_t* a, const int32_t* b, hipStream_t st);
 
 }  // namespace glm53

@@ -73,7 +73,18 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RoutePlanArgs a) {
   // per-expert running base over blocks (exclusive), totals per expert
   if (t < a.experts) {
     unsigned run = 0;
-    for (int64_t b = 0; b < a.blocks; ++b) {
+    int64_t b = 0;
+    for (; b + 8 <= a.blocks; b += 8) {  // 8 loads in flight per round trip
+      unsigned c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = a.block_counts[(b + j) * a.experts + t];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a.block_counts[(b + j) * a.experts + t] = run;
+        run += c[j];
+      }
+    }
+    for (; b < a.blocks; ++b) {
       unsigned c = a.block_counts[b * a.experts + t];
       a.block_counts[b * a.experts + t] = run;
       run += c;
@@ -661,7 +672,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   src.scale_up = dense ? a.x_scale_up : a.scale_up;
   src.out = dense ? a.x_out : a.out;
   src.out_row_stride = dense ? a.x_out_row_stride : a.out_row_stride;
-  if (a.fixup != nullptr && *a.fixup != 0) grouped_gemm_body<MODE, true, GPW>(a, src, ntile, d, lds_dyn);
+  auto set = [](const int32_t* flag) { return flag != nullptr && *flag != 0; };
+  const bool fix = dense ? set(a.x_fixup) || set(a.x_fixup_up) : set(a.fixup) || set(a.fixup_up);
+  if (fix) grouped_gemm_body<MODE, true, GPW>(a, src, ntile, d, lds_dyn);
   else grouped_gemm_body<MODE, false, GPW>(a, src, ntile, d, lds_dyn);
 }
 
@@ -669,7 +682,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
 // 0x7F or 0xFF.
 __global__ void clear_flag_kernel(int32_t* flag) { *flag = 0; }
 
-__global__ void or_flags_kernel(int32_t* dst, const int32_t* a, const int32_t* b) { *dst = (*a != 0) | (*b != 0); }
 
 __global__ __launch_bounds__(256) void scan_480_kernel(const uint8_t* codes, int64_t n, int32_t* flag) {
   const int64_t words = n / 16;
@@ -854,11 +866,6 @@ hipError_t launch_scan_480(const uint8_t* codes, int64_t n, int32_t* flag, bool 
     if (blocks > 2048) blocks = 2048;
     hipLaunchKernelGGL(scan_480_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, codes, n, flag);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_or_flags(int32_t* dst, const int32_t* a, const int32_t* b, hipStream_t st) {
-  hipLaunchKernelGGL(or_flags_kernel, dim3(1), dim3(1), 0, st, dst, a, b);
   return hipGetLastError();
 }
 

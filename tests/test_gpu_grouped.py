@@ -325,3 +325,25 @@ def test_prefill_shared_expert_merged_or_separate_matches_oracle(M, O, dev, shar
     xb = to_bits(x).reshape(T, -1)
     want = O.direct_moe(xb, host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
     assert_parity(to_bits(y).reshape(T, -1), want, O)
+
+
+@pytest.mark.parametrize("which", ["gate", "up", "down"])
+@pytest.mark.parametrize("shared_experts", [1, 2])
+def test_prefill_480_codes_in_one_shared_weight(M, O, dev, shared_experts, which):
+    """0x7F / 0xFF codes (+-480) in one shared weight only: the routed
+    problem's flag stays clear while the shared items (merged into the routed
+    launches, or the separate pair) must take the fixup path; without it the
+    MFMA would read those codes as NaN."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0, shared=shared_experts)
+    bank, shared, gate = syn.synth_layer(cfg, seed=61 + shared_experts, device=dev)
+    w = getattr(shared, f"{which}_proj").weight
+    w[::7, ::13] = 0x7F
+    w[3::11, 5::17] = 0xFF
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    T = 80
+    x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(61, shared_experts), device=dev)
+    y = moe(x)
+    ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
+    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
