@@ -2,8 +2,8 @@
 
 Every translation unit is compiled for gfx950 only, with packed-FP32 VALU ops
 disabled (they are not used by any kernel here and are avoided on purpose),
-then linked against the HIP runtime and rocBLAS (FP32 router GEMM for
-prefill).  Objects go to ``_build/`` next to this file; the shared library
+then linked against the HIP runtime and rocBLAS (the FP32 router GEMM for
+prefills above 1024 tokens).  Objects go to ``_build/`` next to this file; the shared library
 is written next to this file so it travels with the source tree.
 """
 
@@ -20,7 +20,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libglm53_moe.so"
 BUILD = PKG / "_build"
-SOURCES = ["decode.hip", "step.hip", "layer.hip", "grouped.hip", "synth.hip", "api.cpp"]
+SOURCES = ["decode.hip", "step.hip", "layer.hip", "grouped.hip", "router.hip", "synth.hip", "api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

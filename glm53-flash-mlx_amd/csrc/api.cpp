@@ -182,9 +182,12 @@ int router_logits(const float* xf, const float* w, float* logits, int64_t T, int
   return GLM53_OK;
 }
 
-int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, float* scores, hipStream_t st) {
+int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, float* scores, hipStream_t st,
+         int splits = 1, int64_t split_stride = 0) {
   TopkArgs a{};
   a.logits = logits;
+  a.splits = splits;
+  a.split_stride = split_stride;
   a.bias = r->bias;
   a.tokens = T;
   a.experts = r->experts;
@@ -195,6 +198,42 @@ int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, fl
   a.scores_out = scores;
   HIP_TRY(launch_topk(a, st), "topk launch");
   return GLM53_OK;
+}
+
+// Router logits and selection for T > 1 tokens.  Up to kRouterMfmaMaxTokens
+// tokens, where the shape allows, the weights' BF16 parts go to `planes`
+// (6 x experts x hidden bytes) and BF16-MFMA partial sums (splits <=
+// hidden / experts planes of T x E) go to `space` (room for T x hidden
+// floats), or to `logits` (T x E) when a single plane is wider than
+// `space`, and the selection adds them.  More tokens and other shapes widen
+// x into `space` and run an FP32 library GEMM into `logits`.  Measured on
+// MI355X at hidden 4096 and 288 experts: 256 tokens 34 us against 47 us for
+// the library path, 2048 tokens 98 us against 75 us.
+constexpr int64_t kRouterMfmaMaxTokens = 1024;
+
+int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, float* logits, uint16_t* planes,
+                 int32_t* ids, float* scores, hipStream_t st) {
+  const int64_t H = r->hidden, E = r->experts;
+  if (T <= kRouterMfmaMaxTokens && router_gemm_supported(H, E, x, r->weight)) {
+    const RouterGemmShape shape = router_gemm_shape(T, H, E);
+    RouterGemmArgs g{};
+    g.x = static_cast<const uint16_t*>(x);
+    g.planes = planes;
+    g.partial = shape.splits * E <= H ? space : logits;
+    g.tokens = T;
+    g.hidden = H;
+    g.experts = E;
+    g.token_groups = shape.token_groups;
+    g.expert_groups = shape.expert_groups;
+    g.k_chunk = shape.k_chunk;
+    g.splits = shape.splits;
+    HIP_TRY(launch_router_logits(g, r->weight, st), "router logits launch");
+    return topk(g.partial, r, T, ids, scores, st, static_cast<int>(shape.splits), T * E);
+  }
+  HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), space, T * H, st), "widen launch");
+  int rc = router_logits(space, r->weight, logits, T, H, E, st);
+  if (rc) return rc;
+  return topk(logits, r, T, ids, scores, st);
 }
 
 }  // namespace
@@ -317,7 +356,8 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
 
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
   if (tokens <= 1) return round_up(sizeof(float) * experts);
-  return round_up(sizeof(float) * tokens * hidden) + round_up(sizeof(float) * tokens * experts);
+  return round_up(sizeof(float) * tokens * hidden) + round_up(sizeof(float) * tokens * experts) +
+         round_up(router_planes_bytes(hidden, experts));
 }
 
 int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids, float* scores,
@@ -344,13 +384,12 @@ int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens,
     HIP_TRY(launch_router(a, st), "router launch");
     return topk(logits, router, 1, ids, scores, st);
   }
-  float* xf = static_cast<float*>(workspace);
-  float* logits = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                           round_up(sizeof(float) * tokens * router->hidden));
-  HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), xf, tokens * router->hidden, st), "widen launch");
-  int rc = router_logits(xf, router->weight, logits, tokens, router->hidden, router->experts, st);
-  if (rc) return rc;
-  return topk(logits, router, tokens, ids, scores, st);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* space = reinterpret_cast<float*>(ws);
+  ws += round_up(sizeof(float) * tokens * router->hidden);
+  float* logits = reinterpret_cast<float*>(ws);
+  ws += round_up(sizeof(float) * tokens * router->experts);
+  return route_tokens(router, x, tokens, space, logits, reinterpret_cast<uint16_t*>(ws), ids, scores, st);
 }
 
 // ------------------------------------------------------------ decode ------
@@ -1199,6 +1238,7 @@ struct glm53_prefill_plan {
   void* arena = nullptr;
   // router
   float* xf = nullptr;
+  uint16_t* router_planes = nullptr;  // [3][E][H] BF16 parts of the router weights
   float* logits = nullptr;
   int32_t* ids = nullptr;
   float* scores = nullptr;
@@ -1249,6 +1289,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
     return o;
   };
   size_t o_xf = take(4 * T * hidden), o_logits = take(4 * T * experts), o_ids = take(4 * R), o_scores = take(4 * R);
+  size_t o_planes = take(router_planes_bytes(hidden, experts));
   size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(R, intermediate)), o_sq = take(split_bytes(T, Ism));
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
   size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
@@ -1269,6 +1310,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   }
   uint8_t* b = static_cast<uint8_t*>(p->arena);
   p->xf = reinterpret_cast<float*>(b + o_xf);
+  p->router_planes = reinterpret_cast<uint16_t*>(b + o_planes);
   p->logits = reinterpret_cast<float*>(b + o_logits);
   p->ids = reinterpret_cast<int32_t*>(b + o_ids);
   p->scores = reinterpret_cast<float*>(b + o_scores);
@@ -1334,9 +1376,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   const int32_t* ids = expert_ids;
   const float* sc = scores;
   if (ids == nullptr) {
-    HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), p->xf, T * H, st), "widen launch");
-    if ((rc = router_logits(p->xf, router->weight, p->logits, T, H, E, st))) return rc;
-    if ((rc = topk(p->logits, router, T, p->ids, p->scores, st))) return rc;
+    if ((rc = route_tokens(router, x, T, p->xf, p->logits, p->router_planes, p->ids, p->scores, st))) return rc;
     ids = p->ids;
     sc = p->scores;
   } else {

@@ -331,12 +331,45 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 }
 
 // ------------------------------------------------------ per-token top-k ----
+// Every partial is requested before the first is added (splits <= 16).
+template <int P>
+__device__ __forceinline__ void topk_token_partials(const TopkArgs& a, int64_t t, int lane) {
+  const int splits = a.splits > 1 ? a.splits : 1;
+  float part[P][kMaxRouterSplits];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int64_t c = lane + 64 * i;
+#pragma unroll
+    for (int s = 0; s < kMaxRouterSplits; ++s)
+      part[i][s] = s < splits && c < a.experts ? a.logits[s * a.split_stride + t * a.experts + c] : 0.0f;
+  }
+  float lg[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    float v = part[i][0];
+#pragma unroll
+    for (int s = 1; s < kMaxRouterSplits; ++s)
+      if (s < splits) v += part[i][s];
+    lg[i] = v;
+  }
+  wave_topk_regs<P>(lg, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane,
+                    a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
+}
+
+// kPartials: logits come as a.splits partial planes; otherwise whole.
+template <bool kPartials>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= a.tokens) return;
-  wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
-            lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
+  if constexpr (kPartials) {
+    if (a.experts <= 128) topk_token_partials<2>(a, t, lane);
+    else if (a.experts <= 320) topk_token_partials<5>(a, t, lane);
+    else topk_token_partials<kMaxRouterExperts / 64>(a, t, lane);
+  } else {
+    wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
+              lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
+  }
 }
 
 // BF16 -> FP32 widening of the router input (patch.py:133 x.astype(float32)).
@@ -528,7 +561,10 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
 
 hipError_t launch_topk(const TopkArgs& a, hipStream_t st) {
   if (a.tokens == 0) return hipSuccess;
-  hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>((a.tokens + 3) / 4)), dim3(256), 0, st, a);
+  if (a.splits > kMaxRouterSplits) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((a.tokens + 3) / 4));
+  if (a.splits > 1) hipLaunchKernelGGL(topk_kernel<true>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(topk_kernel<false>, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -212,9 +212,11 @@ struct GemvArgs {
 };
 
 struct TopkArgs {
-  const float* logits;    // [tokens, experts] FP32
+  const float* logits;    // [splits][tokens, experts] FP32 partial sums, added in split order
   const float* bias;      // [experts]
   int64_t tokens, experts;
+  int splits;             // 0 or 1: logits are whole
+  int64_t split_stride;   // elements between partial planes
   int top_k;
   float routed_scaling_factor;
   int norm_topk_prob;
@@ -233,6 +235,24 @@ hipError_t launch_down(const DownArgs& a, hipStream_t st);
 hipError_t launch_router(const RouterArgs& a, hipStream_t st);
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
 hipError_t launch_topk(const TopkArgs& a, hipStream_t st);
+
+// Router logits for many tokens on BF16 MFMA (exact three-way BF16 split of
+// the FP32 weights): partial sums per K chunk, [splits][tokens][experts].
+struct RouterGemmArgs {
+  const uint16_t* x;      // [tokens, hidden] bf16, 16-byte aligned rows
+  uint16_t* planes;       // [3][experts][hidden] BF16 parts of the FP32 weights (written by the launch)
+  float* partial;         // [splits, tokens, experts]
+  int64_t tokens, hidden, experts;
+  int64_t token_groups, expert_groups, k_chunk, splits;
+};
+constexpr int kMaxRouterSplits = 16;
+struct RouterGemmShape {
+  int64_t token_groups, expert_groups, k_chunk, splits;  // splits <= max(1, min(hidden / experts, 16))
+};
+bool router_gemm_supported(int64_t hidden, int64_t experts, const void* x, const void* weight);
+RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t experts);
+size_t router_planes_bytes(int64_t hidden, int64_t experts);
+hipError_t launch_router_logits(const RouterGemmArgs& a, const float* weight, hipStream_t st);
 hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st);
 hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st);
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st);

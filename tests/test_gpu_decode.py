@@ -124,6 +124,28 @@ def test_router_matches_oracle(O, config2_layer, dev, tokens):
     _router_check(O, gate, to_bits(x).reshape(tokens, -1), ids.cpu().numpy(), scores.cpu().numpy())
 
 
+@pytest.mark.parametrize("tokens,hidden,experts", [(333, 4096, 288), (1024, 4096, 288), (2048, 4096, 288),
+                                                   (100, 1024, 200), (77, 512, 512), (40, 256, 320), (50, 384, 64),
+                                                   (5, 200, 16)])
+def test_router_many_tokens_matches_oracle(M, O, dev, tokens, hidden, experts):
+    """Many-token router: up to 1024 tokens BF16 MFMA over the exact
+    three-way BF16 split of the FP32 weights, K-chunk partial sums added by
+    the selection (hidden a multiple of 128); more tokens (2048) or hidden 200
+    take the FP32 library GEMM.  Shapes cover tail tokens and experts, a last
+    expert group of 2 tiles (288 experts), 512 experts, a single partial
+    plane wider than the activation space (40 x 256 x 320) and few tiles."""
+    import torch
+
+    syn = submodule("synthetic")
+    rng = np.random.default_rng(tokens + hidden + experts)
+    w = torch.from_numpy((rng.normal(size=(experts, hidden)) * 0.02).astype(np.float32)).to(dev)
+    b = torch.from_numpy((rng.normal(size=experts) * 0.01).astype(np.float32)).to(dev)
+    gate = M.Float32Gate(w, b, top_k=8, routed_scaling_factor=2.5, norm_topk_prob=True)
+    x = syn.normal_bf16((tokens, hidden), syn.key(9, tokens), device=dev)
+    ids, scores = gate(x)
+    _router_check(O, gate, to_bits(x).reshape(tokens, -1), ids.cpu().numpy(), scores.cpu().numpy())
+
+
 @pytest.mark.parametrize("tokens", [1, 3])
 def test_router_scores_kat(M, dev, tokens):
     """The weighting formula of tests/test_grouped_divergence.py:181-199
