@@ -15,6 +15,7 @@ from .abi import (
     PACKED_DECODE_KERNEL_ABI,
     PACKED_EXPERT_BANK_ABI,
 )
+from .checkpoint import CheckpointError, load_moe_layer
 from .fp8 import (
     BLOCK_SIZE,
     DECODE_TOP_K,
@@ -40,6 +41,8 @@ from .packed import DecodePlan, PackedFP8ExpertBank, PackedFP8MoE
 from .router import Float32Gate
 
 __all__ = [
+    "CheckpointError",
+    "load_moe_layer",
     "BLOCK_SIZE", "DECODE_TOP_K", "GROUPED_TILE_ROWS", "GROUPED_MIN_ROUTES", "GROUPED_MEASURED_CROSSOVER_ROUTES",
     "KERNEL_ABI_VERSION", "GROUPED_KERNEL_ABI", "PACKED_EXPERT_BANK_ABI", "PACKED_DECODE_KERNEL_ABI",
     "block_fp8_linear", "swiglu", "BlockFP8Linear", "ClampedMLP", "DirectFP8Expert", "DirectFP8MoE",
