@@ -1,0 +1,49 @@
+"""GPU parity at every (hidden, intermediate) shape of the three-launch step
+table, including the real checkpoint's I = 2048 (SURVEY config 2 uses
+I = 1536): batch-1 decode through PackedFP8MoE (packed.py:896-923) and, at
+the I = 2048 shapes, grouped prefill through SortedGroupedFP8MoE
+(grouped_fp8.py:279-328), both against the oracle's Direct MoE.  16 experts
+per bank keep the host copies small; the step kernels' shapes do not depend
+on the expert count."""
+
+from __future__ import annotations
+
+import pytest
+
+from conftest import assert_parity, host_bank, host_shared, submodule, to_bits
+
+pytestmark = pytest.mark.gpu
+
+STEP_SHAPES = [(4096, 1536), (4096, 2048), (7168, 2048), (6144, 2048), (2048, 1024), (2048, 1536), (1024, 512),
+               (1024, 1024)]
+
+
+def _layer(hidden, inter, dev):
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=hidden, intermediate=inter, experts=16, top_k=8, limit=10.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=hidden * 7 + inter, device=dev)
+    return syn, cfg, bank, shared, gate
+
+
+@pytest.mark.parametrize("hidden,inter", STEP_SHAPES)
+def test_decode_at_step_table_shapes_matches_oracle(M, O, dev, hidden, inter):
+    syn, cfg, bank, shared, gate = _layer(hidden, inter, dev)
+    moe = M.PackedFP8MoE(bank, cfg, gate, shared)
+    hb, hs = host_bank(bank), host_shared(shared)
+    for t in range(2):
+        x = syn.normal_bf16((1, 1, hidden), syn.key(hidden, inter, t), device=dev)
+        y = moe(x)
+        ids, sc = (v.reshape(1, 8).cpu().numpy() for v in gate(x))
+        want = O.direct_moe(to_bits(x).reshape(1, -1), hb, ids, sc, cfg.swiglu_limit, hs)
+        assert_parity(to_bits(y).reshape(1, -1), want, O)
+
+
+@pytest.mark.parametrize("hidden,inter", [(4096, 2048), (7168, 2048)])
+def test_prefill_at_checkpoint_width_matches_oracle(M, O, dev, hidden, inter):
+    syn, cfg, bank, shared, gate = _layer(hidden, inter, dev)
+    T = 40  # 320 routes: the grouped path (>= 256 routes)
+    x = syn.normal_bf16((1, T, hidden), syn.key(hidden, inter, "prefill"), device=dev)
+    y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)(x)
+    ids, sc = (v.reshape(T, 8).cpu().numpy() for v in gate(x))
+    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
