@@ -306,6 +306,19 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
     HIP_TRY(launch_gemv(a, st), "gemv launch");
     return GLM53_OK;
   }
+  if (M == 1 && split_width_supported(K) && aligned(x, 16) && aligned(weight, 16)) {
+    GemvArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.weight = weight;
+    a.scale = scale_inv;
+    a.N = N;
+    a.K = K;
+    a.rows_per_wave = 4;  // rows per workgroup of K / 4096 wavefronts
+    a.y = static_cast<uint16_t*>(y);
+    a.flags = code_flags;
+    HIP_TRY(launch_gemv_split(a, st), "split gemv launch");
+    return GLM53_OK;
+  }
   const size_t need = glm53_fp8_linear_workspace_bytes(M, N, K);
   if (need > 0 && aligned(weight, 16) && workspace != nullptr && workspace_bytes >= need) {
     SplitBuf b = carve_split(workspace, M, K);

@@ -330,6 +330,57 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   else gemv_rows<VB, CH, false>(a, n0, n_end, lane);
 }
 
+// Wide rows (K a multiple of 4096 above 8192, e.g. an attention output
+// projection of 16384): the workgroup holds one wavefront per 4096-wide K
+// part; each streams its part of a batch of up to 4 rows exactly as
+// gemv_rows does, lane 0 leaves the part's sums in LDS and the first
+// threads add the parts in part order (deterministic) and store the row.
+// Workgroup g covers rows [rows_per_wave * g, ...).
+template <bool HW>
+__device__ __forceinline__ void gemv_split_rows(const GemvArgs& a, int parts, int lane, int part) {
+  constexpr int VB = 16, CH = 4;
+  __shared__ float sums[kMaxGemvParts][4];
+  const int64_t K = a.K;
+  const int64_t SC = K / kBlock;
+  const int64_t kp = static_cast<int64_t>(part) * 64 * VB * CH;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_wave;
+  const int64_t n_end = n0 + a.rows_per_wave < a.N ? n0 + a.rows_per_wave : a.N;
+  XRaw<VB, CH> raw;
+  load_x_raw<VB, CH>(a.x + kp, lane, raw);
+  XSlice<VB, CH, HW> xs;
+  pack_x_raw<VB, CH, HW>(raw, xs);
+  for (int64_t n = n0; n < n_end; n += 4) {  // uniform across the workgroup: every wave reaches each barrier
+    const int rows = n_end - n < 4 ? static_cast<int>(n_end - n) : 4;
+    WRow<VB, CH> w[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = n + (r < rows ? r : 0);
+      load_wrow<VB, CH>(w[r], a.weight + row * K + kp, a.scale + (row >> 7) * SC + kp / kBlock, lane);
+    }
+    float t[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) t[r] = wave_sum(wrow_partial<VB, CH, HW>(w[r], xs));
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sums[part][r] = t[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < rows) {
+      float total = sums[0][threadIdx.x];
+      for (int q = 1; q < parts; ++q) total += sums[q][threadIdx.x];
+      a.y[n + threadIdx.x] = f32_to_bf16(total);
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(64 * kMaxGemvParts) void gemv_split_kernel(GemvArgs a, int parts) {
+  const int lane = threadIdx.x & 63;
+  const int part = threadIdx.x >> 6;
+  if (hw_decode_ok(a.flags)) gemv_split_rows<true>(a, parts, lane, part);
+  else gemv_split_rows<false>(a, parts, lane, part);
+}
+
 // ------------------------------------------------------ per-token top-k ----
 // Every partial is requested before the first is added (splits <= 16).
 template <int P>
@@ -557,6 +608,16 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t st) {
     case 8192: return launch_gemv_t<16, 8>(a, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool split_width_supported(int64_t K) { return K > 8192 && K % 4096 == 0 && K / 4096 <= kMaxGemvParts; }
+
+hipError_t launch_gemv_split(const GemvArgs& a, hipStream_t st) {
+  if (!split_width_supported(a.K) || a.rows_per_wave < 1) return hipErrorInvalidValue;
+  const int parts = static_cast<int>(a.K / 4096);
+  hipLaunchKernelGGL(gemv_split_kernel, dim3(static_cast<unsigned>((a.N + a.rows_per_wave - 1) / a.rows_per_wave)),
+                     dim3(static_cast<unsigned>(64 * parts)), 0, st, a, parts);
+  return hipGetLastError();
 }
 
 hipError_t launch_topk(const TopkArgs& a, hipStream_t st) {

@@ -234,6 +234,9 @@ hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st);
 hipError_t launch_down(const DownArgs& a, hipStream_t st);
 hipError_t launch_router(const RouterArgs& a, hipStream_t st);
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t st);
+constexpr int kMaxGemvParts = 16;  // split-K GEMV: one wavefront per 4096-wide part, K <= 65536
+bool split_width_supported(int64_t K);
+hipError_t launch_gemv_split(const GemvArgs& a, hipStream_t st);  // rows_per_wave = rows per workgroup
 hipError_t launch_topk(const TopkArgs& a, hipStream_t st);
 
 // Router logits for many tokens on BF16 MFMA (exact three-way BF16 split of

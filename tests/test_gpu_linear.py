@@ -48,6 +48,25 @@ def test_gemv_random_codes_decode_like_reference_lut(M, O, dev, k, n):
     assert_parity(got, want, O, exact_fraction=0.98)
 
 
+@pytest.mark.parametrize("k,n", [(12288, 200), (16384, 130), (65536, 8)])
+@pytest.mark.parametrize("with_480", [False, True])
+def test_wide_gemv_split_k_matches_oracle(M, O, dev, k, n, with_480):
+    """One-row linear with K a multiple of 4096 above 8192 (an attention
+    output projection is 16384 wide): one wavefront per 4096-wide K part,
+    parts added in order.  Codes with 0x7F/0xFF take the exact software
+    decode, codes without them the hardware one."""
+    rng = np.random.default_rng(k + n + with_480)
+    if with_480:
+        codes = random_codes(rng, (n, k))
+    else:
+        codes = (rng.integers(0, 0x7F, size=(n, k)) | (rng.integers(0, 2, size=(n, k)) << 7)).astype(np.uint8)
+    scale = (rng.uniform(size=(-(-n // 128), k // 128)) * 0.002).astype(np.float32)
+    x = O.f32_to_bf16((rng.normal(size=(1, k)) * 2).astype(np.float32))
+    got = _linear(M, dev, x, codes, scale)
+    want = O.fp8_linear(x, codes, scale)
+    assert_parity(got, want, O, exact_fraction=0.98)
+
+
 def test_reference_kat_non_aligned_129x257(M, O, dev):
     """tests/test_fp8_metal.py:23-39: 129 x 257 crosses both block edges;
     error vs the dequantised matmul <= 0.03125."""
