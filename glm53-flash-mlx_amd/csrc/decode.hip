@@ -424,7 +424,19 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 }
 
 // BF16 -> FP32 widening of the router input (patch.py:133 x.astype(float32)).
+// Thread = 8 elements: one 16-byte load, two 16-byte stores (x and y
+// 16-byte aligned, n a multiple of 8); bf16_to_f32_tail_kernel otherwise.
 __global__ void bf16_to_f32_kernel(const uint16_t* x, float* y, int64_t n) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;
+  const uint4 v = *reinterpret_cast<const uint4*>(x + i);
+  *reinterpret_cast<float4*>(y + i) = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                                                  __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+  *reinterpret_cast<float4*>(y + i + 4) = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
+                                                      __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u));
+}
+
+__global__ void bf16_to_f32_tail_kernel(const uint16_t* x, float* y, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) y[i] = bf16_to_f32(x[i]);
 }
@@ -631,7 +643,11 @@ hipError_t launch_topk(const TopkArgs& a, hipStream_t st) {
 
 hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+  if (n % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0)
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0, st, x, y, n);
+  else
+    hipLaunchKernelGGL(bf16_to_f32_tail_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, x, y,
+                       n);
   return hipGetLastError();
 }
 

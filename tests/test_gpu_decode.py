@@ -126,12 +126,13 @@ def test_router_matches_oracle(O, config2_layer, dev, tokens):
 
 @pytest.mark.parametrize("tokens,hidden,experts", [(333, 4096, 288), (1024, 4096, 288), (2048, 4096, 288),
                                                    (100, 1024, 200), (77, 512, 512), (40, 256, 320), (50, 384, 64),
-                                                   (5, 200, 16)])
+                                                   (5, 200, 16), (3, 201, 16)])
 def test_router_many_tokens_matches_oracle(M, O, dev, tokens, hidden, experts):
     """Many-token router: up to 1024 tokens BF16 MFMA over the exact
     three-way BF16 split of the FP32 weights, K-chunk partial sums added by
     the selection (hidden a multiple of 128); more tokens (2048) or hidden 200
-    take the FP32 library GEMM.  Shapes cover tail tokens and experts, a last
+    and 201 take the widened input and the FP32 library GEMM (201: the
+    element-wise widening).  Shapes cover tail tokens and experts, a last
     expert group of 2 tiles (288 experts), 512 experts, a single partial
     plane wider than the activation space (40 x 256 x 320) and few tiles."""
     import torch
