@@ -1,5 +1,5 @@
 """GPU parity at every (hidden, intermediate) shape of the three-launch step
-table, including the real checkpoint's I = 2048 (SURVEY config 2 uses
+table, including the real checkpoint's I = 2048 (the benchmark layer uses
 I = 1536): batch-1 decode through PackedFP8MoE (packed.py:896-923) and, at
 the I = 2048 shapes, grouped prefill through SortedGroupedFP8MoE
 (grouped_fp8.py:279-328), both against the oracle's Direct MoE.  16 experts
