@@ -211,6 +211,10 @@ def main():
     # -------------------------------------------------------------- parity ---
     parity = parity_sample(args, layers, cfg, dev, torch, np)
 
+    # ------------------------------------------------------ config-1 linear ---
+    linear = bench_linear(dev, torch, pkg, syn)
+    log(f"config-1 linear: {linear['us_per_linear']:.2f} us per GEMV in a graph")
+
     # ------------------------------------------------------------- prefill ---
     prefill = {}
     if not args.no_prefill:
@@ -272,6 +276,7 @@ def main():
             "weights_generated_s": round(gen_s, 1),
             "final_state_finite": finite,
         },
+        "linear_config1": linear,
         "prefill": prefill,
         "parity": parity,
         "cpu_baseline": cpu,
@@ -299,6 +304,34 @@ def time_graph(fn, reps, torch):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) * 1000.0 / reps
+
+
+def bench_linear(dev, torch, pkg, syn, copies=24, reps=20):
+    """y = block_fp8_linear(x bf16 [1,4096], W [4096,4096],
+    s [32,32]) (fp8.py:254-299).  One graph replays the GEMV over `copies`
+    distinct weight matrices (403 MB, more than the 256 MB last-level
+    cache), so each launch streams its weights from HBM; the per-GEMV time
+    includes the graph's kernel-to-kernel gaps."""
+    K = N = 4096
+    lins = []
+    for i in range(copies):
+        lin = pkg.BlockFP8Linear(K, N, device=dev)
+        syn.fill_fp8(lin.weight, lin.weight_scale_inv, syn.key(91, i), 0.02)
+        lins.append(lin)
+    x = syn.normal_bf16((1, K), syn.key(91, "x"), device=dev)
+    out = [None] * copies
+
+    def run():
+        for i, lin in enumerate(lins):
+            out[i] = lin(x)
+
+    us = time_graph(run, reps, torch) / copies
+    nbytes = K * N + 4 * (K // 128) * (N // 128) + 2 * K + 2 * N
+    finite = bool(torch.isfinite(out[-1].float()).all().item())
+    del lins
+    return {"us_per_linear": round(us, 3), "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "finite": finite,
+            "note": f"graph of {copies} GEMVs over distinct weights; kernel time in profiles/"}
 
 
 def read_probe(lib, N, bank, dev, torch):
