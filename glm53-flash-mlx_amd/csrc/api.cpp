@@ -1270,7 +1270,8 @@ struct glm53_prefill_plan {
   uint16_t* down = nullptr;      // [R, H]
   uint16_t* hs = nullptr;        // [T, Is]
   uint16_t* shared_out = nullptr;  // [T, H]
-  int32_t* flags = nullptr;        // [4] scanned code flags: bank, shared gate/up/down
+  int32_t* flags = nullptr;        // [4] code flags scanned when the caller has none: bank gate/up, bank
+                                   // down, shared gate + up, shared down
   int64_t last_tokens = 0;
 };
 
