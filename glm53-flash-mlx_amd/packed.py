@@ -248,6 +248,43 @@ class DecodePlan:
                                               ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual), N.ptr(out),
                                               int(stages), N.stream_handle(device)))
 
+    @staticmethod
+    def _bound_tensors(bank, shared, router):
+        tensors = [bank.gate_up_weight, bank.gate_up_scale_inv, bank.down_weight, bank.down_scale_inv]
+        if shared is not None:
+            for proj in (shared.gate_proj, shared.up_proj, shared.down_proj):
+                tensors += [proj.weight, proj.weight_scale_inv]
+        return tensors + [router.weight, router.e_score_correction_bias]
+
+    def bind_weights(self, bank, shared, router) -> None:
+        """Bind one layer's weights once (bindings.cpp:576-583,
+        native_packed_moe_plan.cpp:231-258); binding again raises
+        RuntimeError.  The storage identity of every bound tensor is
+        recorded for execute_bound."""
+        b = bank.as_c_struct()
+        s = shared.as_c_struct() if shared is not None else None
+        r = router.as_c_struct()
+        N.check(self._lib.glm53_decode_plan_bind(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                                 ctypes.byref(r)))
+        flags = [bank.code_flags()]
+        if shared is not None:
+            flags += [shared.gate_proj.code_flags(), shared.up_proj.code_flags(), shared.down_proj.code_flags()]
+        self._bound = (bank, shared, router, flags)  # keeps the scanned flag tensors the plan points at alive
+        self._bound_identity = [(t.data_ptr(), t._version) for t in self._bound_tensors(bank, shared, router)]
+
+    def execute_bound(self, x, out, device) -> None:
+        """Decode x [H] with the bound weights into out [H]
+        (native_packed_moe_plan.cpp:260-280).  Raises RuntimeError when
+        nothing is bound, or when a bound tensor was replaced or modified in
+        place since binding (its 0x7F/0xFF code flags were scanned then)."""
+        bound = getattr(self, "_bound", None)
+        if bound is None:
+            raise RuntimeError("decode plan weights are not bound")
+        now = [(t.data_ptr(), t._version) for t in self._bound_tensors(*bound[:3])]
+        if now != self._bound_identity:
+            raise RuntimeError("decode plan bound weight identity changed")
+        N.check(self._lib.glm53_decode_moe_bound(self.handle, N.ptr(x), N.ptr(out), N.stream_handle(device)))
+
     def tune(self, gate_up_rows_per_wave: int = 8, down_rows_per_wg: int = 16) -> None:
         N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))
 

@@ -411,3 +411,38 @@ def test_decode_rejects_bad_shapes(M, dev, small_layer):
         M.block_fp8_linear(torch.zeros((1, 100), dtype=torch.bfloat16, device=dev),
                            torch.zeros((128, 128), dtype=torch.uint8, device=dev),
                            torch.ones((1, 1), device=dev))
+
+
+def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
+    """bind_weights / execute_bound (native_packed_moe_plan.cpp:231-280):
+    the bound run equals the unbound one bit for bit; executing unbound,
+    binding twice, or executing after a bound tensor was replaced or
+    modified in place raise RuntimeError."""
+    import torch
+
+    syn = submodule("synthetic")
+    packed = submodule("packed")
+    cfg = syn.layer_config(hidden=1024, intermediate=512, experts=32, top_k=8, limit=10.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=81, device=dev)
+    plan = packed.DecodePlan(1024, 512, 512, 32, 8, 10.0)
+    x = syn.normal_bf16((1024,), syn.key(81, "x"), device=dev)
+    want = torch.empty(1024, dtype=torch.bfloat16, device=dev)
+    ids = torch.empty(8, dtype=torch.int32, device=dev)
+    sc = torch.empty(8, dtype=torch.float32, device=dev)
+    plan.full(bank, shared, gate, x, want, ids, sc, dev)
+    out = torch.empty_like(want)
+    with pytest.raises(RuntimeError, match="not bound"):
+        plan.execute_bound(x, out, dev)
+    plan.bind_weights(bank, shared, gate)
+    plan.execute_bound(x, out, dev)
+    assert torch.equal(out, want)
+    with pytest.raises(RuntimeError, match="already bound"):
+        plan.bind_weights(bank, shared, gate)
+    shared.down_proj.weight_scale_inv.mul_(1.0)  # in place: a new version of a bound tensor
+    with pytest.raises(RuntimeError, match="identity changed"):
+        plan.execute_bound(x, out, dev)
+    plan2 = packed.DecodePlan(1024, 512, 512, 32, 8, 10.0)
+    plan2.bind_weights(bank, shared, gate)
+    bank.down_weight = bank.down_weight.clone()  # replaced storage
+    with pytest.raises(RuntimeError, match="identity changed"):
+        plan2.execute_bound(x, out, dev)
