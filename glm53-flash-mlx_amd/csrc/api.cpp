@@ -427,6 +427,7 @@ struct glm53_decode_plan {
   uint16_t* shared_out = nullptr;   // [H]
   uint16_t* moe_out = nullptr;      // [H] before a residual add
   void* arena = nullptr;
+  size_t arena_bytes = 0;
   bool bound = false;
   int gate_up_rows_per_wave = 8;   // launch shape (glm53_decode_plan_tune), swept on MI355X
   int down_rows_per_wg = 16;
@@ -476,6 +477,7 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   size_t o_down = take(2 * top_k * hidden), o_routed = take(2 * hidden);
   size_t o_sg = take(2 * std::max<int64_t>(shared_intermediate, 1)), o_su = take(2 * std::max<int64_t>(shared_intermediate, 1));
   size_t o_so = take(2 * hidden), o_mo = take(2 * hidden), o_rc = take(4);
+  p->arena_bytes = off;
   hipError_t e = hipMalloc(&p->arena, off);
   if (e != hipSuccess) {
     delete p;
@@ -1036,6 +1038,10 @@ int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr
     case 3:
       *ptr = plan->control;
       *bytes = 64;
+      return GLM53_OK;
+    case 4:
+      *ptr = plan->arena;
+      *bytes = plan->arena_bytes;
       return GLM53_OK;
     default:
       return fail(GLM53_INVALID_ARGUMENT, "unknown scratch id %d", which);

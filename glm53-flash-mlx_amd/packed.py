@@ -216,6 +216,8 @@ class DecodePlan:
                                                    float(limit), ctypes.byref(handle)))
         self.handle = handle
         self.top_k = top_k
+        self._dims = (int(hidden), int(intermediate), int(shared_intermediate), int(experts))
+        self._executions = 0
 
     def __del__(self):
         handle = getattr(self, "handle", None)
@@ -223,20 +225,69 @@ class DecodePlan:
             self._lib.glm53_decode_plan_destroy(handle)
             self.handle = None
 
+    def _execute(self, status: int) -> None:
+        N.check(status)
+        self._executions += 1
+
+    # Read-only counters of the reference plan (bindings.cpp:584-632).
+    @property
+    def hidden_size(self) -> int:
+        return self._dims[0]
+
+    @property
+    def intermediate_size(self) -> int:
+        return self._dims[1]
+
+    @property
+    def shared_intermediate_size(self) -> int:
+        return self._dims[2]
+
+    @property
+    def expert_count(self) -> int:
+        return self._dims[3]
+
+    @property
+    def execution_count(self) -> int:
+        return self._executions
+
+    @property
+    def dynamic_allocation_count(self) -> int:
+        return 0  # all device scratch is one arena allocated at creation
+
+    @property
+    def host_synchronization_count(self) -> int:
+        return 0  # every call only enqueues on the caller's stream
+
+    @property
+    def weights_bound(self) -> bool:
+        return getattr(self, "_bound", None) is not None
+
+    @property
+    def bound_weight_identities_stable(self) -> bool:
+        bound = getattr(self, "_bound", None)
+        return bound is not None and [(t.data_ptr(), t._version) for t in self._bound_tensors(*bound[:3])] == \
+            self._bound_identity
+
+    @property
+    def scratch_bytes(self) -> int:
+        ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
+        N.check(self._lib.glm53_decode_plan_scratch(self.handle, 4, ctypes.byref(ptr), ctypes.byref(nbytes)))
+        return int(nbytes.value)
+
     def routed(self, bank, shared, x, ids, scores, out, device):
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
-        N.check(self._lib.glm53_decode_moe_routed(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                                  N.ptr(x), N.ptr(ids), N.ptr(scores), N.ptr(out),
-                                                  N.stream_handle(device)))
+        self._execute(self._lib.glm53_decode_moe_routed(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                                        N.ptr(x), N.ptr(ids), N.ptr(scores), N.ptr(out),
+                                                        N.stream_handle(device)))
 
     def full(self, bank, shared, router, x, out, ids_out, scores_out, device):
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
         r = router.as_c_struct()
-        N.check(self._lib.glm53_decode_moe(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                           ctypes.byref(r), N.ptr(x), N.ptr(out), N.ptr(ids_out), N.ptr(scores_out),
-                                           N.stream_handle(device)))
+        self._execute(self._lib.glm53_decode_moe(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                                 ctypes.byref(r), N.ptr(x), N.ptr(out), N.ptr(ids_out),
+                                                 N.ptr(scores_out), N.stream_handle(device)))
 
     def step(self, bank, shared, router, x, residual, out, stages, device):
         """Decoder-step form: out = T(residual + T(moe(x))) (residual may be
@@ -244,9 +295,9 @@ class DecodePlan:
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
         r = router.as_c_struct() if router is not None else None
-        N.check(self._lib.glm53_decode_moe_ex(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                              ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual), N.ptr(out),
-                                              int(stages), N.stream_handle(device)))
+        self._execute(self._lib.glm53_decode_moe_ex(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                                    ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual),
+                                                    N.ptr(out), int(stages), N.stream_handle(device)))
 
     @staticmethod
     def _bound_tensors(bank, shared, router):
@@ -283,7 +334,7 @@ class DecodePlan:
         now = [(t.data_ptr(), t._version) for t in self._bound_tensors(*bound[:3])]
         if now != self._bound_identity:
             raise RuntimeError("decode plan bound weight identity changed")
-        N.check(self._lib.glm53_decode_moe_bound(self.handle, N.ptr(x), N.ptr(out), N.stream_handle(device)))
+        self._execute(self._lib.glm53_decode_moe_bound(self.handle, N.ptr(x), N.ptr(out), N.stream_handle(device)))
 
     def tune(self, gate_up_rows_per_wave: int = 8, down_rows_per_wg: int = 16) -> None:
         N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))

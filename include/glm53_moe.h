@@ -219,7 +219,9 @@ int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode);
 
 /* Device scratch of the last call (read-only diagnostics): which = 0 hidden
  * bf16 [top_k + 1, I] (routed rows, then shared), 1 expert ids int32
- * [top_k], 2 scores f32 [top_k]. */
+ * [top_k], 2 scores f32 [top_k], 3 the launch control words (64 B), 4 the
+ * plan's whole device arena (allocated once at creation; the reference's
+ * scratch_bytes, native_packed_moe_plan.h:73). */
 int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes);
 
 /* Synchronous: copies the plan's device error flag to *host_value and

@@ -433,14 +433,22 @@ def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
     out = torch.empty_like(want)
     with pytest.raises(RuntimeError, match="not bound"):
         plan.execute_bound(x, out, dev)
+    assert not plan.weights_bound and plan.execution_count == 1
     plan.bind_weights(bank, shared, gate)
     plan.execute_bound(x, out, dev)
     assert torch.equal(out, want)
+    assert plan.weights_bound and plan.bound_weight_identities_stable and plan.execution_count == 2
+    assert (plan.hidden_size, plan.intermediate_size, plan.shared_intermediate_size, plan.expert_count) == \
+        (1024, 512, 512, 32)
+    assert plan.dynamic_allocation_count == 0 and plan.host_synchronization_count == 0
+    assert plan.scratch_bytes >= 2 * 9 * 512 + 4 * 8 + 4 * 8
     with pytest.raises(RuntimeError, match="already bound"):
         plan.bind_weights(bank, shared, gate)
     shared.down_proj.weight_scale_inv.mul_(1.0)  # in place: a new version of a bound tensor
+    assert not plan.bound_weight_identities_stable
     with pytest.raises(RuntimeError, match="identity changed"):
         plan.execute_bound(x, out, dev)
+    assert plan.execution_count == 2
     plan2 = packed.DecodePlan(1024, 512, 512, 32, 8, 10.0)
     plan2.bind_weights(bank, shared, gate)
     bank.down_weight = bank.down_weight.clone()  # replaced storage
