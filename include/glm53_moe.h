@@ -137,6 +137,10 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
  * Router -- replaces patch.py:131-142 `Float32Gate.__call__` (with the
  * selection half of mlx-vlm dsv32.group_expert_select, n_group = 1).
  * x bf16 [tokens, H] -> ids int32 [tokens, top_k], scores f32 [tokens, top_k].
+ * The workspace holds, for several tokens, FP32 activations or BF16-MFMA
+ * partial sums (tokens x H floats), FP32 logits (tokens x experts) and the
+ * weights' three BF16 parts (6 x experts x H bytes); for one token, the
+ * logits.
  * ---------------------------------------------------------------------- */
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts);
 int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids,
