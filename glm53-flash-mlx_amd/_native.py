@@ -99,6 +99,7 @@ _SIGNATURES = {
     "glm53_prefill_plan_create": (ctypes.c_int, [I64, I64, I64, I64, I64, I64, F32, P]),
     "glm53_prefill_plan_destroy": (None, [P]),
     "glm53_prefill_moe": (ctypes.c_int, [P, P, P, P, P, I64, P, P, I32, P, P]),
+    "glm53_prefill_moe_hc": (ctypes.c_int, [P, P, P, P, P, I64, P, P, I32, P, P, P, P, P]),
     "glm53_prefill_plan_status": (ctypes.c_int, [P, P]),
     "glm53_prefill_plan_scratch": (ctypes.c_int, [P, I32, P, P]),
     "glm53_synth_fp8": (ctypes.c_int, [P, P, I64, I64, ctypes.c_uint64, F32, P]),

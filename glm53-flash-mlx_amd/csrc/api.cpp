@@ -1364,9 +1364,12 @@ void glm53_prefill_plan_destroy(glm53_prefill_plan* plan) {
   delete plan;
 }
 
-int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
-                      const glm53_router* router, const void* x, int64_t tokens, const int32_t* expert_ids,
-                      const float* scores, int32_t reduction, void* out, void* stream) {
+// The prefill body; out = the BF16 MoE output, or (hc_out set) the
+// hyper-connection streams built from it in the reduction's epilogue.
+static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                       const glm53_router* router, const void* x, int64_t tokens, const int32_t* expert_ids,
+                       const float* scores, int32_t reduction, void* out, const void* hc_residual, const float* hc_post,
+                       const float* hc_comb, void* hc_out, void* stream) {
   CHECK_ARG(p != nullptr, "plan is null");
   CHECK_ARG(tokens >= 0 && tokens <= p->max_tokens, "tokens %lld outside [0, %lld]", (long long)tokens,
             (long long)p->max_tokens);
@@ -1389,7 +1392,7 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   }
   p->last_tokens = tokens;
   if (tokens == 0) return GLM53_OK;
-  CHECK_ARG(x && out, "null pointer argument");
+  CHECK_ARG(x && (out || hc_out), "null pointer argument");
   hipStream_t st = S(stream);
   const int64_t T = tokens, k = p->k, R = T * k, H = p->H, I = p->I, Is = p->Is, E = p->E;
   const int64_t SC = H / 128, SR = I / 128, SI = I / 128;
@@ -1577,8 +1580,29 @@ int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53
   r.H = H;
   r.top_k = static_cast<int>(k);
   r.out = static_cast<uint16_t*>(out);
+  r.hc_residual = static_cast<const uint16_t*>(hc_residual);
+  r.hc_post = hc_post;
+  r.hc_comb = hc_comb;
+  r.hc_out = static_cast<uint16_t*>(hc_out);
   HIP_TRY(launch_reduce(r, reduction == GLM53_REDUCE_DIRECT, st), "reduce launch");
   return GLM53_OK;
+}
+
+int glm53_prefill_moe(glm53_prefill_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                      const glm53_router* router, const void* x, int64_t tokens, const int32_t* expert_ids,
+                      const float* scores, int32_t reduction, void* out, void* stream) {
+  CHECK_ARG(tokens == 0 || out != nullptr, "null pointer argument");
+  return prefill_run(p, bank, shared, router, x, tokens, expert_ids, scores, reduction, out, nullptr, nullptr, nullptr,
+                     nullptr, stream);
+}
+
+int glm53_prefill_moe_hc(glm53_prefill_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                         const glm53_router* router, const void* x, int64_t tokens, const int32_t* expert_ids,
+                         const float* scores, int32_t reduction, const void* residual, const float* post,
+                         const float* comb, void* out_hc, void* stream) {
+  CHECK_ARG(tokens == 0 || (residual && post && comb && out_hc), "null pointer argument");
+  return prefill_run(p, bank, shared, router, x, tokens, expert_ids, scores, reduction, nullptr, residual, post, comb,
+                     out_hc, stream);
 }
 
 int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes) {

@@ -100,8 +100,16 @@ struct ReduceArgs {
   const uint16_t* shared;     // [tokens, H] or null
   int64_t tokens, H;
   int top_k;
-  uint16_t* out;              // [tokens, H]
+  uint16_t* out;              // [tokens, H] (unused when hc_out is set)
+  // Hyper-connection expand epilogue (metal:2362-2388), kHcBranches streams:
+  // hc_out[t, b, h] = T(post[t, b] * moe[t, h] + fma-chain_s comb[t, s, b] *
+  // residual[t, s, h]), moe = the BF16 MoE output; hc_out null: plain out.
+  const uint16_t* hc_residual;  // [tokens, kHcBranches, H]
+  const float* hc_post;         // [tokens, kHcBranches]
+  const float* hc_comb;         // [tokens, kHcBranches (source), kHcBranches (branch)]
+  uint16_t* hc_out;             // [tokens, kHcBranches, H]
 };
+constexpr int kHcBranches = 4;
 
 hipError_t launch_route_plan(const RoutePlanArgs& a, hipStream_t st);
 hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st);

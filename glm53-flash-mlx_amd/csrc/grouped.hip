@@ -705,6 +705,35 @@ __global__ __launch_bounds__(256) void scan_480_kernel(const uint8_t* codes, int
 
 // grouped_fp8.py:273-276: y[t] = T(sum_slot float(down[inv[t*k+slot]]) *
 // score), FP32 products summed in slot order, optional BF16 shared add.
+// Stores one thread's V MoE outputs (FP32 values already BF16-exact): the
+// plain row, or the kHcBranches hyper-connection streams built from them
+// (native_indexer_plan.metal:2362-2388: mixed = fma(comb[s][b], residual[s],
+// mixed) over s in order from 0, then T(post[b] * moe + mixed)).
+template <int V>
+__device__ __forceinline__ void store_moe_row(const ReduceArgs& a, int64_t t, int64_t h0, const float (&moe)[V]) {
+  if (a.hc_out == nullptr) {
+    store_bf16_run<V>(a.out + t * a.H + h0, moe);
+    return;
+  }
+  Bf16Run<V> res[kHcBranches];
+#pragma unroll
+  for (int s = 0; s < kHcBranches; ++s) res[s].load(a.hc_residual + (t * kHcBranches + s) * a.H + h0);
+#pragma unroll
+  for (int b = 0; b < kHcBranches; ++b) {
+    const float post = a.hc_post[t * kHcBranches + b];
+    float y[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float mixed = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kHcBranches; ++s)
+        mixed = __builtin_fmaf(a.hc_comb[(t * kHcBranches + s) * kHcBranches + b], res[s].get(i), mixed);
+      y[i] = __fadd_rn(__fmul_rn(post, moe[i]), mixed);
+    }
+    store_bf16_run<V>(a.hc_out + (t * kHcBranches + b) * a.H + h0, y);
+  }
+}
+
 // Thread = V consecutive columns of one token (V = 8: 16-byte loads and
 // stores, when H and the row pointers allow it; V = 1 otherwise).  The
 // token's positions and scores are read first (uniform across the
@@ -747,9 +776,9 @@ __global__ __launch_bounds__(256) void restore_reduce_kernel(ReduceArgs a) {
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     total[i] = bf16_round(total[i]);
-    if (a.shared != nullptr) total[i] = __fadd_rn(total[i], sh.get(i));
+    if (a.shared != nullptr) total[i] = bf16_round(__fadd_rn(total[i], sh.get(i)));
   }
-  store_bf16_run<V>(a.out + t * a.H + h0, total);
+  store_moe_row<V>(a, t, h0, total);
 }
 
 // native_indexer_plan.metal:2174-2207 (fp8.py:384-397 order): per token,
@@ -805,8 +834,8 @@ __global__ __launch_bounds__(256) void direct_order_reduce_kernel(ReduceArgs a) 
   if (a.shared != nullptr) sh.load(a.shared + t * a.H + h0);
 #pragma unroll
   for (int i = 0; i < V; ++i)
-    if (a.shared != nullptr) total[i] = __fadd_rn(total[i], sh.get(i));
-  store_bf16_run<V>(a.out + t * a.H + h0, total);
+    if (a.shared != nullptr) total[i] = bf16_round(__fadd_rn(total[i], sh.get(i)));
+  store_moe_row<V>(a, t, h0, total);
 }
 
 // ------------------------------------------------------------- launchers --
@@ -873,7 +902,8 @@ hipError_t launch_reduce(const ReduceArgs& a, bool direct_order, hipStream_t st)
   if (a.tokens == 0) return hipSuccess;
   if (a.top_k > kMaxReduceTopK) return hipErrorInvalidValue;
   auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool wide = a.H % 8 == 0 && a16(a.route_out) && a16(a.out) && a16(a.shared);
+  const bool wide = a.H % 8 == 0 && a16(a.route_out) && a16(a.out) && a16(a.shared) && a16(a.hc_residual) &&
+                    a16(a.hc_out);
   const int64_t per_thread = wide ? 8 : 1;
   const dim3 grid(static_cast<unsigned>((a.H / per_thread + 255) / 256), static_cast<unsigned>(a.tokens));
   if (wide) {

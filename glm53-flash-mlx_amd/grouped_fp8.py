@@ -179,6 +179,19 @@ class PrefillPlan:
                                             ctypes.byref(r) if r else None, N.ptr(x), tokens, N.ptr(ids),
                                             N.ptr(scores), reduction, N.ptr(out), N.stream_handle(device)))
 
+    def run_hc(self, bank, shared, router, x, tokens, ids, scores, reduction, residual, post, comb, out, device):
+        """execute_indirect_hc (native_prefill_moe_plan.cpp:101-119): the MoE
+        of `run` followed by the hyper-connection expand, fused into the
+        reduction: out bf16 [tokens, 4, H] from residual bf16 [tokens, 4, H],
+        post f32 [tokens, 4] and comb f32 [tokens, 4, 4]."""
+        b = bank.as_c_struct()
+        s = shared.as_c_struct() if shared is not None else None
+        r = router.as_c_struct() if router is not None else None
+        N.check(self._lib.glm53_prefill_moe_hc(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                               ctypes.byref(r) if r else None, N.ptr(x), tokens, N.ptr(ids),
+                                               N.ptr(scores), reduction, N.ptr(residual), N.ptr(post), N.ptr(comb),
+                                               N.ptr(out), N.stream_handle(device)))
+
     def invalid_routes(self) -> int:
         value = ctypes.c_uint32()
         N.check(self._lib.glm53_prefill_plan_status(self.handle, ctypes.byref(value)))

@@ -325,6 +325,20 @@ int glm53_prefill_moe(glm53_prefill_plan* plan, const glm53_bank* bank,
                       int64_t tokens, const int32_t* expert_ids, const float* scores,
                       int32_t reduction, void* out, void* stream);
 
+/* NativePrefillMoEPlan.execute_indirect_hc (native_prefill_moe_plan.cpp:
+ * 101-119, finish_hc 136-161; kernel native_indexer_plan.metal:2362-2388):
+ * the MoE of glm53_prefill_moe followed by the hyper-connection expand,
+ * fused into the reduction (the MoE output is never written):
+ * out_hc[t, b, h] = T(post[t, b] * moe[t, h] + mixed), mixed = fma chain
+ * over s = 0..3 of comb[t, s, b] * residual[t, s, h], starting from 0.
+ * residual bf16 [tokens, 4, H], post f32 [tokens, 4], comb f32
+ * [tokens, 4, 4], out_hc bf16 [tokens, 4, H]. */
+int glm53_prefill_moe_hc(glm53_prefill_plan* plan, const glm53_bank* bank,
+                         const glm53_shared_expert* shared, const glm53_router* router,
+                         const void* x, int64_t tokens, const int32_t* expert_ids,
+                         const float* scores, int32_t reduction, const void* residual,
+                         const float* post, const float* comb, void* out_hc, void* stream);
+
 /* Synchronous: invalid route count of the last glm53_prefill_moe. */
 int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes);
 

@@ -280,6 +280,22 @@ void glm53o_weighted_reduction(const uint16_t* down, const float* scores, int64_
 }
 
 /* BF16 + BF16 -> BF16 (packed.py:922; native_indexer_plan.metal:525-535). */
+/* native_indexer_plan.metal:2362-2388 (finish_hc of native_prefill_moe_plan.cpp:136-161):
+ * out[r, b, d] = T(post[r, b] * moe[r, d] + mixed), mixed = fma chain over
+ * s = 0..3 of comb[r, s, b] * residual[r, s, d] from 0 (4 streams). */
+void glm53o_hc_expand(const uint16_t* moe, const uint16_t* residual, const float* post, const float* comb,
+                      int64_t rows, int64_t hidden, uint16_t* out) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int b = 0; b < 4; ++b)
+            for (int64_t d = 0; d < hidden; ++d) {
+                float mixed = 0.0f;
+                for (int src = 0; src < 4; ++src)
+                    mixed = fmaf(comb[(r * 4 + src) * 4 + b], bf16_to_f32(residual[(r * 4 + src) * hidden + d]), mixed);
+                const float branch = post[r * 4 + b] * bf16_to_f32(moe[r * hidden + d]);
+                out[(r * 4 + b) * hidden + d] = f32_to_bf16(branch + mixed);
+            }
+}
+
 void glm53o_add_bf16(const uint16_t* a, const uint16_t* b, int64_t n, uint16_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(bf16_to_f32(a[i]) + bf16_to_f32(b[i]));
 }

@@ -76,6 +76,7 @@ def _declare(L):
     L.glm53o_router.argtypes = [P, I64, I64, P, P, I64, I64, ctypes.c_float, ctypes.c_int, P, P, P]
     L.glm53o_weighted_reduction.argtypes = [P, P, I64, I64, P]
     L.glm53o_add_bf16.argtypes = [P, P, I64, P]
+    L.glm53o_hc_expand.argtypes = [P, P, P, P, I64, I64, P]
     L.glm53o_direct_order_reduce.argtypes = [P, P, P, I64, I64, I64, P]
     L.glm53o_restore_and_reduce.argtypes = [P, P, P, I64, I64, I64, P]
     L.glm53o_num_threads.restype = ctypes.c_int
@@ -293,6 +294,19 @@ def _weighted_reduction(down_bits, scores):
     s = np.ascontiguousarray(scores, dtype=np.float32)
     out = np.zeros(d.shape[1], dtype=np.uint16)
     lib().glm53o_weighted_reduction(_p(d), _p(s), d.shape[0], d.shape[1], _p(out))
+    return out
+
+
+def hc_expand(moe, residual, post, comb):
+    """native_indexer_plan.metal:2362-2388: moe bf16 [T, H], residual bf16
+    [T, 4, H], post f32 [T, 4], comb f32 [T, 4, 4] -> bf16 [T, 4, H]."""
+    m = np.ascontiguousarray(moe, dtype=np.uint16)
+    r = np.ascontiguousarray(residual, dtype=np.uint16)
+    po = np.ascontiguousarray(post, dtype=np.float32)
+    co = np.ascontiguousarray(comb, dtype=np.float32)
+    t, h = m.shape
+    out = np.zeros((t, 4, h), dtype=np.uint16)
+    lib().glm53o_hc_expand(_p(m), _p(r), _p(po), _p(co), t, h, _p(out))
     return out
 
 

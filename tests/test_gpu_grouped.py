@@ -347,3 +347,30 @@ def test_prefill_480_codes_in_one_shared_weight(M, O, dev, shared_experts, which
     ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
     want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
     assert_parity(to_bits(y).reshape(T, -1), want, O)
+
+
+@pytest.mark.parametrize("reduction", ["grouped", "direct"])
+def test_prefill_hc_expand_epilogue_matches_plain_then_oracle(M, O, dev, reduction):
+    """glm53_prefill_moe_hc: the hyper-connection expand fused into the
+    reduction equals the oracle's expand (metal:2362-2388) applied to the
+    plain prefill output, bit for bit."""
+    import torch
+
+    N = submodule("_native")
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=91, device=dev)
+    T = 70
+    x = syn.normal_bf16((T, 512), syn.key(91, "x"), device=dev)
+    rng = np.random.default_rng(91)
+    residual = from_bits(O.f32_to_bf16(rng.normal(size=(T, 4, 512)).astype(np.float32)), dev)
+    post = torch.from_numpy(rng.normal(size=(T, 4)).astype(np.float32)).to(dev)
+    comb = torch.from_numpy(rng.normal(size=(T, 4, 4)).astype(np.float32)).to(dev)
+    plan = M.PrefillPlan(512, 256, 256, 32, 8, T, 7.0)
+    red = N.REDUCE_DIRECT if reduction == "direct" else N.REDUCE_GROUPED
+    plain = torch.empty((T, 512), dtype=torch.bfloat16, device=dev)
+    plan.run(bank, shared, gate, x, T, None, None, red, plain, dev)
+    hc = torch.empty((T, 4, 512), dtype=torch.bfloat16, device=dev)
+    plan.run_hc(bank, shared, gate, x, T, None, None, red, residual, post, comb, hc, dev)
+    want = O.hc_expand(to_bits(plain), to_bits(residual), post.cpu().numpy(), comb.cpu().numpy())
+    assert np.array_equal(to_bits(hc), want)

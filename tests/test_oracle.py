@@ -443,3 +443,30 @@ def test_grouped_equals_direct_and_decode_fallback(O):
     assert np.allclose(a, e, rtol=0.02, atol=0.02)
     one = O.direct_moe(x[:1], bank, routes[:1], scores[:1], L)
     assert np.array_equal(one[0], O.decode_moe(x[0], bank, routes[0], scores[0], L))
+
+
+def test_hc_expand_special_cases_and_float64_restatement(O):
+    """Hyper-connection expand (metal:2362-2388): comb = identity with post =
+    0 returns the residual streams bit for bit; comb = 0 with post = 1
+    returns the MoE output; random inputs match a float64 restatement that
+    rounds the FMA chain and the product to FP32 where the kernel does."""
+    rng = np.random.default_rng(21)
+    T, H = 5, 64
+    moe = O.f32_to_bf16(rng.normal(size=(T, H)).astype(np.float32))
+    res = O.f32_to_bf16(rng.normal(size=(T, 4, H)).astype(np.float32))
+    eye = np.broadcast_to(np.eye(4, dtype=np.float32), (T, 4, 4)).copy()
+    assert np.array_equal(O.hc_expand(moe, res, np.zeros((T, 4), np.float32), eye), res)
+    got = O.hc_expand(moe, res, np.ones((T, 4), np.float32), np.zeros((T, 4, 4), np.float32))
+    assert np.array_equal(got, np.repeat(moe[:, None, :], 4, axis=1))
+    post = rng.normal(size=(T, 4)).astype(np.float32)
+    comb = rng.normal(size=(T, 4, 4)).astype(np.float32)
+    m = O.bf16_to_f32(moe).astype(np.float64)
+    r = O.bf16_to_f32(res).astype(np.float64)
+    want = np.zeros((T, 4, H), np.uint16)
+    for b in range(4):
+        mixed = np.zeros((T, H), np.float32)
+        for src in range(4):  # one rounding per FMA: at these magnitudes the product-sum is exact in float64
+            mixed = (comb[:, src, b, None].astype(np.float64) * r[:, src] + mixed.astype(np.float64)).astype(np.float32)
+        branch = (post[:, b, None].astype(np.float64) * m).astype(np.float32)
+        want[:, b] = O.f32_to_bf16((branch.astype(np.float64) + mixed.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(O.hc_expand(moe, res, post, comb), want)
