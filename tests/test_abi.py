@@ -106,6 +106,33 @@ def test_struct_layouts_match_header(N, tmp_path):
             assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
 
 
+def test_invalid_arguments_fail_before_any_device_work(N, libso):
+    """Status 1 (invalid argument, -> ValueError) with a message from
+    glm53_last_error, for argument checks that run before any device call
+    (the reference raises ValueError / std::invalid_argument for shape and
+    layout errors)."""
+    P = ctypes.c_void_p
+    h = ctypes.c_void_p()
+    cases = [
+        (lambda: libso.glm53_prefill_plan_create(100, 256, 0, 32, 8, 64, 10.0, ctypes.byref(h)), "block-aligned"),
+        (lambda: libso.glm53_prefill_plan_create(4096, 1536, 100, 32, 8, 64, 10.0, ctypes.byref(h)), "multiple of 128"),
+        (lambda: libso.glm53_prefill_plan_create(512, 256, 0, 32, 40, 64, 10.0, ctypes.byref(h)), "top_k"),
+        (lambda: libso.glm53_decode_plan_create(4096, 1536, 1536, 288, 0, 10.0, ctypes.byref(h)), "top_k"),
+        (lambda: libso.glm53_decode_plan_create(4096, 1536, 1536, 288, 8, 10.0, None), "out is null"),
+        (lambda: libso.glm53_split_activations(P(16), 4, 100, 100, P(16), P(16), P(16), None), "multiple of 128"),
+        (lambda: libso.glm53_restore_and_reduce(P(16), P(16), P(16), 4, 0, 256, None, P(16), None), "dimensions"),
+        (lambda: libso.glm53_router_topk(None, P(16), 4, P(16), P(16), P(16), 1 << 20, None), "router is null"),
+        (lambda: libso.glm53_grouped_linear(P(16), 8, None, 8, 100, P(16), P(16), P(16), 1, P(16), P(16), None, 1,
+                                            128, P(16), P(16), 1 << 20, None), "block-aligned"),
+    ]
+    for call, fragment in cases:
+        assert call() == N.INVALID_ARGUMENT, fragment
+        assert fragment in libso.glm53_last_error().decode(), (fragment, libso.glm53_last_error())
+        with pytest.raises(ValueError):
+            N.check(N.INVALID_ARGUMENT)
+    assert libso.glm53_split_activations(P(16), 0, 128, 128, P(16), P(16), P(16), None) == N.OK  # empty: no work
+
+
 def test_product_refuses_cpu_tensors():
     """No CPU fallback: a product op on host tensors raises."""
     torch = pytest.importorskip("torch")
