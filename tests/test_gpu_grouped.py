@@ -374,3 +374,18 @@ def test_prefill_hc_expand_epilogue_matches_plain_then_oracle(M, O, dev, reducti
     plan.run_hc(bank, shared, gate, x, T, None, None, red, residual, post, comb, hc, dev)
     want = O.hc_expand(to_bits(plain), to_bits(residual), post.cpu().numpy(), comb.cpu().numpy())
     assert np.array_equal(to_bits(hc), want)
+
+
+def test_prefill_4096_tokens_matches_oracle(M, O, dev):
+    """A long prompt on a small layer: 32,768 routes (128 route-count blocks,
+    the library FP32 router above 1,024 tokens, 64-route descriptors)
+    against the oracle's Direct MoE."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=101, device=dev)
+    T = 4096
+    x = syn.normal_bf16((1, T, 512), syn.key(101, "x"), device=dev)
+    y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)(x)
+    ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
+    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
