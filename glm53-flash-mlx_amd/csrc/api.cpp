@@ -202,14 +202,19 @@ int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, fl
 
 // Router logits and selection for T > 1 tokens.  Up to kRouterMfmaMaxTokens
 // tokens, where the shape allows, the weights' BF16 parts go to `planes`
-// (6 x experts x hidden bytes) and BF16-MFMA partial sums (splits <=
-// hidden / experts planes of T x E) go to `space` (room for T x hidden
-// floats), or to `logits` (T x E) when a single plane is wider than
-// `space`, and the selection adds them.  More tokens and other shapes widen
-// x into `space` and run an FP32 library GEMM into `logits`.  Measured on
+// (6 x experts x hidden bytes) and BF16-MFMA partial sums (up to
+// kMaxRouterSplits planes of T x E) go to `space` (room for T x max(hidden,
+// kMaxRouterSplits x experts) floats), and the selection adds them.  More
+// tokens and other shapes widen x into `space` and run an FP32 library GEMM
+// into `logits`.  Measured on
 // MI355X at hidden 4096 and 288 experts: 256 tokens 34 us against 47 us for
 // the library path, 2048 tokens 98 us against 75 us.
 constexpr int64_t kRouterMfmaMaxTokens = 1024;
+
+// FP32 widened router input (T x H) or router partial sums (T x E per split).
+size_t router_space_bytes(int64_t T, int64_t H, int64_t E) {
+  return sizeof(float) * static_cast<size_t>(T) * static_cast<size_t>(std::max<int64_t>(H, kMaxRouterSplits * E));
+}
 
 int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, float* logits, uint16_t* planes,
                  int32_t* ids, float* scores, hipStream_t st) {
@@ -219,7 +224,7 @@ int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, 
     RouterGemmArgs g{};
     g.x = static_cast<const uint16_t*>(x);
     g.planes = planes;
-    g.partial = shape.splits * E <= H ? space : logits;
+    g.partial = space;
     g.tokens = T;
     g.hidden = H;
     g.experts = E;
@@ -369,7 +374,7 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
 
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
   if (tokens <= 1) return round_up(sizeof(float) * experts);
-  return round_up(sizeof(float) * tokens * hidden) + round_up(sizeof(float) * tokens * experts) +
+  return round_up(router_space_bytes(tokens, hidden, experts)) + round_up(sizeof(float) * tokens * experts) +
          round_up(router_planes_bytes(hidden, experts));
 }
 
@@ -399,7 +404,7 @@ int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens,
   }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   float* space = reinterpret_cast<float*>(ws);
-  ws += round_up(sizeof(float) * tokens * router->hidden);
+  ws += round_up(router_space_bytes(tokens, router->hidden, router->experts));
   float* logits = reinterpret_cast<float*>(ws);
   ws += round_up(sizeof(float) * tokens * router->experts);
   return route_tokens(router, x, tokens, space, logits, reinterpret_cast<uint16_t*>(ws), ids, scores, st);
@@ -1308,7 +1313,8 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
     off += round_up(bytes);
     return o;
   };
-  size_t o_xf = take(4 * T * hidden), o_logits = take(4 * T * experts), o_ids = take(4 * R), o_scores = take(4 * R);
+  size_t o_xf = take(router_space_bytes(T, hidden, experts)), o_logits = take(4 * T * experts), o_ids = take(4 * R),
+         o_scores = take(4 * R);
   size_t o_planes = take(router_planes_bytes(hidden, experts));
   size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(R, intermediate)), o_sq = take(split_bytes(T, Ism));
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));

@@ -250,7 +250,7 @@ struct RouterGemmArgs {
 };
 constexpr int kMaxRouterSplits = 16;
 struct RouterGemmShape {
-  int64_t token_groups, expert_groups, k_chunk, splits;  // splits <= max(1, min(hidden / experts, 16))
+  int64_t token_groups, expert_groups, k_chunk, splits;  // splits <= kMaxRouterSplits
 };
 bool router_gemm_supported(int64_t hidden, int64_t experts, const void* x, const void* weight);
 RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t experts);

@@ -177,13 +177,9 @@ RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t expert
   s.expert_groups = (tiles + 4 * kRouterTilesPerWave - 1) / (4 * kRouterTilesPerWave);
   const int64_t groups = s.token_groups * s.expert_groups;
   const int64_t blocks = hidden / 128;
-  // Two work items per CU where K allows, while the partial planes fit in
-  // the space of an FP32 copy of x (splits <= hidden / experts, <= 16).
+  // Two work items per CU where K allows, at most kMaxRouterSplits partial planes.
   int64_t want = (512 + groups - 1) / groups;
-  int64_t cap = hidden / experts;
-  if (cap > kMaxRouterSplits) cap = kMaxRouterSplits;
-  if (cap < 1) cap = 1;
-  if (want > cap) want = cap;
+  if (want > kMaxRouterSplits) want = kMaxRouterSplits;
   if (want > blocks) want = blocks;
   if (want < 1) want = 1;
   const int64_t chunk_blocks = (blocks + want - 1) / want;

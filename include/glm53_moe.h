@@ -138,7 +138,8 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
  * selection half of mlx-vlm dsv32.group_expert_select, n_group = 1).
  * x bf16 [tokens, H] -> ids int32 [tokens, top_k], scores f32 [tokens, top_k].
  * The workspace holds, for several tokens, FP32 activations or BF16-MFMA
- * partial sums (tokens x H floats), FP32 logits (tokens x experts) and the
+ * partial sums (tokens x max(H, 16 x experts) floats), FP32 logits
+ * (tokens x experts) and the
  * weights' three BF16 parts (6 x experts x H bytes); for one token, the
  * logits.
  * ---------------------------------------------------------------------- */
