@@ -389,3 +389,33 @@ def test_prefill_4096_tokens_matches_oracle(M, O, dev):
     ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
     want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
     assert_parity(to_bits(y).reshape(T, -1), want, O)
+
+
+def test_prefill_graph_replays_match_eager(M, dev):
+    """A 300-token prefill (BF16-MFMA router, route plan, grouped GEMMs,
+    reduction) captured in a HIP graph: every replay, with eager work and
+    synchronisations between replays, equals the eager output bit for bit."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=111, device=dev)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    x = syn.normal_bf16((1, 300, 512), syn.key(111, "x"), device=dev)
+    eager = moe(x).clone()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        moe(x)  # warm the capture stream's plan (plans are per stream) and the cached code flags
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = moe(x)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out, eager), i
+        noise = syn.normal_bf16((1, 300, 512), syn.key(111, "noise", i), device=dev)
+        moe(noise)  # eager work on the same plan between replays
+        torch.cuda.synchronize(dev)
