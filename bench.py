@@ -9,8 +9,7 @@ seeded input every step.  One step (42 x 3 launches + the input draw) is
 captured once as a HIP graph and replayed; `value` = microseconds per MoE
 layer = step time / 42.  The dominant kernel (top-k prologue, routed
 gate/up/SwiGLU, shared down) is the `roofline` entry, timed with
-HIP events on its stream against the HBM roofline.  The one-launch form
-(decode_layer_kernel) is timed beside it for comparison.
+HIP events on its stream against the HBM roofline.
 
 Also reported: the grouped prefill configs 4 (256 tokens, near-uniform) and 5 (2,048 tokens, Zipf
 router bias) as routes/s with HBM and FP8-MFMA roofline fractions, a parity
@@ -53,7 +52,6 @@ def parse():
     p.add_argument("--prefill-only", action="store_true",
                    help="one synthetic layer, configs 4 and 5 prefill only (for profiling the grouped GEMM)")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--no-single", action="store_true", help="skip timing the one-launch decode form")
     p.add_argument("--json-out", type=str, default="")
     p.add_argument("--traffic-run", action="store_true", help="short eager program for rocprofv3 --pmc passes")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -135,10 +133,6 @@ def main():
     counter = torch.zeros(1, dtype=torch.int32, device=dev)
     lib = N.lib()
 
-    def set_mode(mode):
-        for l in layers:
-            l.plan.set_mode(mode)
-
     def step():
         N.check(lib.glm53_synth_step_input(N.ptr(x), H, SEED, 1.0, N.ptr(counter), N.stream_handle(dev)))
         for l in layers:
@@ -164,7 +158,6 @@ def main():
         torch.cuda.synchronize()
         return start.elapsed_time(end) / args.steps, time.perf_counter() - wall0
 
-    set_mode(N.DECODE_THREE_LAUNCH)
     ms_step, wall = time_steps()
     us_layer = ms_step * 1000.0 / L
     finite = bool(torch.isfinite(x.float()).all().item())
@@ -198,15 +191,9 @@ def main():
     log(f"launches: router+shared {router_us:.2f} us, gate/up {gate_up_us:.2f} us ({gu_gbs:.0f} GB/s), "
         f"down {down_us:.2f} us ({down_bytes / (down_us * 1e-6) / 1e9:.0f} GB/s)")
 
-    # The one-launch form (decode_layer_kernel), for comparison.
-    single = None
-    if not args.no_single:
-        set_mode(N.DECODE_SINGLE_LAUNCH)
-        ms_single, _ = time_steps()
-        layer_us = time_graph(run_stage(N.STAGE_ALL), args.kernel_steps * 2, torch) / L
-        set_mode(N.DECODE_THREE_LAUNCH)
-        single = {"us_per_layer": round(ms_single * 1000.0 / L, 3), "launch_us": round(layer_us, 3)}
-        log(f"one-launch form: {ms_single * 1000.0 / L:.2f} us/layer")
+    errors = [l.plan.error_flag() for l in layers]  # synchronous; after every timed replay
+    if any(errors):
+        raise RuntimeError(f"decode error flags after the timed replays: {errors}")
 
     # -------------------------------------------------------------- parity ---
     parity = parity_sample(args, layers, cfg, dev, torch, np)
@@ -272,7 +259,7 @@ def main():
             "launch_note": "stage-only graphs of one launch kind; kernel durations in profiles/",
             "achievable_read_GBps": probe,
             "copy_GBps": copy,
-            "one_launch_form": single,
+            "error_flags_clear": True,
             "weights_generated_s": round(gen_s, 1),
             "final_state_finite": finite,
         },
@@ -519,11 +506,6 @@ def traffic_run(args):
     torch.cuda.synchronize()
     for _ in range(4):
         for l in layers:
-            l.plan.set_mode(N.DECODE_SINGLE_LAUNCH)
-            l.plan.step(l.bank, l.shared, l.gate, x, None, x, N.STAGE_ALL, dev)
-    for _ in range(4):
-        for l in layers:
-            l.plan.set_mode(N.DECODE_THREE_LAUNCH)
             for mask in (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN):
                 l.plan.step(l.bank, l.shared, l.gate, x, None, x, mask, dev)
     lib = N.lib()
@@ -570,8 +552,7 @@ def summarize_traffic(fetch_csv, write_csv):
     copy_kw = pick(write, "copyBuffer") or pick(write, "elementwise_kernel")
     fetch_scale = 4 * probe_bytes / (fetch[probe_k][2] * 1024.0)
     write_scale = 4 * copy_bytes / (write[copy_kw][2] * 1024.0)
-    keys = ("step_router_shared_kernel", "step_gate_up_kernel", "step_down_kernel", "decode_layer_kernel",
-            "probe_read_kernel")
+    keys = ("step_router_shared_kernel", "step_gate_up_kernel", "step_down_kernel", "probe_read_kernel")
     print("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (calibrated) | written B (calibrated) |")
     print("|---|---|---|---|---|---|")
     out = {}

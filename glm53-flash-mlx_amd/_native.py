@@ -22,7 +22,6 @@ LIB_PATH = Path(os.environ.get("GLM53_MOE_LIB", _PKG / "libglm53_moe.so"))
 OK, INVALID_ARGUMENT, BAD_STATE, DEVICE_ERROR = 0, 1, 2, 3
 REDUCE_GROUPED, REDUCE_DIRECT = 0, 1
 STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 4, 7
-DECODE_THREE_LAUNCH, DECODE_SINGLE_LAUNCH = 0, 1
 
 _lib = None
 
@@ -66,6 +65,19 @@ class Router(ctypes.Structure):
     ]
 
 
+class PlanCounters(ctypes.Structure):
+    _fields_ = [
+        ("execution_count", ctypes.c_uint64),
+        ("dynamic_allocation_count", ctypes.c_uint64),
+        ("host_synchronization_count", ctypes.c_uint64),
+        ("static_input_validation_count", ctypes.c_uint64),
+        ("dynamic_input_validation_count", ctypes.c_uint64),
+        ("scratch_bytes", ctypes.c_uint64),
+        ("weights_bound", I32),
+        ("router_bound", I32),
+    ]
+
+
 _SIGNATURES = {
     "glm53_last_error": (ctypes.c_char_p, []),
     "glm53_abi_version": (ctypes.c_int, []),
@@ -83,10 +95,12 @@ _SIGNATURES = {
     "glm53_decode_moe_ex": (ctypes.c_int, [P, P, P, P, P, P, P, I32, P]),
     "glm53_decode_plan_bind": (ctypes.c_int, [P, P, P, P]),
     "glm53_decode_moe_bound": (ctypes.c_int, [P, P, P, P]),
+    "glm53_decode_moe_bound_routed": (ctypes.c_int, [P, P, P, P, P, P]),
     "glm53_decode_plan_tune": (ctypes.c_int, [P, I32, I32]),
-    "glm53_decode_plan_set_mode": (ctypes.c_int, [P, I32]),
     "glm53_decode_plan_scratch": (ctypes.c_int, [P, I32, P, P]),
     "glm53_decode_plan_error_flag": (ctypes.c_int, [P, P]),
+    "glm53_decode_plan_counters": (ctypes.c_int, [P, P]),
+    "glm53_decode_plan_identities": (ctypes.c_int, [P, I32, P, I32, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),
     "glm53_route_plan": (ctypes.c_int, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, I64, P, P, SZ, P]),
     "glm53_grouped_linear_workspace_bytes": (SZ, [I64, I64]),
@@ -102,6 +116,8 @@ _SIGNATURES = {
     "glm53_prefill_moe_hc": (ctypes.c_int, [P, P, P, P, P, I64, P, P, I32, P, P, P, P, P]),
     "glm53_prefill_plan_status": (ctypes.c_int, [P, P]),
     "glm53_prefill_plan_scratch": (ctypes.c_int, [P, I32, P, P]),
+    "glm53_prefill_plan_counters": (ctypes.c_int, [P, P]),
+    "glm53_prefill_plan_identities": (ctypes.c_int, [P, P, I32, P]),
     "glm53_synth_fp8": (ctypes.c_int, [P, P, I64, I64, ctypes.c_uint64, F32, P]),
     "glm53_synth_f32": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, F32, F32, I32, P]),
     "glm53_synth_bf16": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, P]),

@@ -2,8 +2,7 @@
 
 Every translation unit is compiled for gfx950 only, with packed-FP32 VALU ops
 disabled (they are not used by any kernel here and are avoided on purpose),
-then linked against the HIP runtime and rocBLAS (the FP32 router GEMM for
-prefills above 1024 tokens).  Objects go to ``_build/`` next to this file; the shared library
+then linked against the HIP runtime only (no vendor math library).  Objects go to ``_build/`` next to this file; the shared library
 is written next to this file so it travels with the source tree.
 """
 
@@ -20,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libglm53_moe.so"
 BUILD = PKG / "_build"
-SOURCES = ["decode.hip", "step.hip", "layer.hip", "grouped.hip", "router.hip", "synth.hip", "api.cpp"]
+SOURCES = ["decode.hip", "step.hip", "grouped.hip", "router.hip", "synth.hip", "api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -54,8 +53,7 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as pool:
         objs = list(pool.map(_compile, SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
-           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)

@@ -34,6 +34,7 @@ import torch
 
 from . import _native as N
 from .fp8 import ClampedMLP
+from .ownership import TensorLayout, owned_tensor
 from .packed import PackedFP8ExpertBank
 from .router import Float32Gate
 
@@ -255,7 +256,9 @@ def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = No
         put(gate_up_s[e, sr:], proj["up"] + "_scale_inv")
         put(down[e], proj["down"])
         put(down_s[e], proj["down"] + "_scale_inv")
-    bank = PackedFP8ExpertBank(gate_up, gate_up_s, down, down_s, intermediate_size=I)
+    rm = TensorLayout.ROW_MAJOR_CONTIGUOUS
+    bank = PackedFP8ExpertBank(owned_tensor(gate_up, layout=rm), owned_tensor(gate_up_s, layout=rm),
+                               owned_tensor(down, layout=rm), owned_tensor(down_s, layout=rm), intermediate_size=I)
     shared = None
     if keys.shared is not None:
         Is = tensors[keys.shared["gate"]].shape[0]

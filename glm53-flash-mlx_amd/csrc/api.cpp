@@ -6,8 +6,7 @@
 // thread-local message for glm53_last_error().
 #include <glm53_moe.h>
 
-#include <rocblas/rocblas.h>
-
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -115,73 +114,6 @@ int check_router(const glm53_router* r, int64_t H, int64_t E, int64_t k) {
   return GLM53_OK;
 }
 
-// Exchange words and counters of the one-launch decode kernel live in
-// uncached device memory: its workgroups on different XCDs (each with its
-// own L2) read each other's words while the kernel runs, and consecutive
-// launches hand the ticket, exit count and epoch on to each other; uncached
-// memory keeps every such access at the memory itself.  Uncached blocks are never freed (a freed
-// uncached block has been seen to corrupt later allocations), so a destroyed
-// plan returns its block to this per-process pool for the next plan.
-struct UncachedBlock {
-  int device;
-  size_t bytes;
-  void* ptr;
-};
-std::mutex g_uncached_mutex;
-std::vector<UncachedBlock> g_uncached_free;
-
-hipError_t uncached_take(size_t bytes, void** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  {
-    std::lock_guard<std::mutex> lock(g_uncached_mutex);
-    for (size_t i = 0; i < g_uncached_free.size(); ++i) {
-      if (g_uncached_free[i].device == dev && g_uncached_free[i].bytes >= bytes) {
-        *out = g_uncached_free[i].ptr;
-        g_uncached_free.erase(g_uncached_free.begin() + static_cast<std::ptrdiff_t>(i));
-        return hipSuccess;
-      }
-    }
-  }
-  return hipExtMallocWithFlags(out, bytes, hipDeviceMallocUncached);
-}
-
-void uncached_give(void* ptr, size_t bytes) {
-  int dev = 0;
-  if (ptr == nullptr || hipGetDevice(&dev) != hipSuccess) return;
-  std::lock_guard<std::mutex> lock(g_uncached_mutex);
-  g_uncached_free.push_back({dev, bytes, ptr});
-}
-
-std::mutex g_blas_mutex;
-rocblas_handle g_blas = nullptr;
-
-int blas_handle(rocblas_handle* out) {
-  std::lock_guard<std::mutex> lock(g_blas_mutex);
-  if (g_blas == nullptr) {
-    if (rocblas_create_handle(&g_blas) != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_create_handle failed");
-  }
-  *out = g_blas;
-  return GLM53_OK;
-}
-
-// logits[T, E] = x_f32[T, H] . W[E, H]^T in FP32 (column-major view: C' = W'^T X').
-int router_logits(const float* xf, const float* w, float* logits, int64_t T, int64_t H, int64_t E, hipStream_t st) {
-  rocblas_handle h;
-  int rc = blas_handle(&h);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lock(g_blas_mutex);
-  if (rocblas_set_stream(h, st) != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_set_stream failed");
-  const float one = 1.0f, zero = 0.0f;
-  rocblas_status s = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(E),
-                                   static_cast<rocblas_int>(T), static_cast<rocblas_int>(H), &one, w,
-                                   static_cast<rocblas_int>(H), xf, static_cast<rocblas_int>(H), &zero, logits,
-                                   static_cast<rocblas_int>(E));
-  if (s != rocblas_status_success) return fail(GLM53_DEVICE_ERROR, "rocblas_sgemm failed (%d)", (int)s);
-  return GLM53_OK;
-}
-
 int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, float* scores, hipStream_t st,
          int splits = 1, int64_t split_stride = 0) {
   TopkArgs a{};
@@ -200,30 +132,22 @@ int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, fl
   return GLM53_OK;
 }
 
-// Router logits and selection for T > 1 tokens.  Up to kRouterMfmaMaxTokens
-// tokens, where the shape allows, the weights' BF16 parts go to `planes`
-// (6 x experts x hidden bytes) and BF16-MFMA partial sums (up to
-// kMaxRouterSplits planes of T x E) go to `space` (room for T x max(hidden,
-// kMaxRouterSplits x experts) floats), and the selection adds them.  More
-// tokens and other shapes widen x into `space` and run an FP32 library GEMM
-// into `logits`.  Measured on
-// MI355X at hidden 4096 and 288 experts: 256 tokens 34 us against 47 us for
-// the library path, 2048 tokens 98 us against 75 us.
-constexpr int64_t kRouterMfmaMaxTokens = 1024;
-
-// FP32 widened router input (T x H) or router partial sums (T x E per split).
-size_t router_space_bytes(int64_t T, int64_t H, int64_t E) {
-  return sizeof(float) * static_cast<size_t>(T) * static_cast<size_t>(std::max<int64_t>(H, kMaxRouterSplits * E));
+// Router logits and selection for T > 1 tokens.  Where the shape allows
+// (hidden % 128 == 0, 16-byte aligned rows) the BF16-MFMA tile kernel writes
+// FP32 partial sums per K chunk (up to kMaxRouterSplits planes of T x E) to
+// `space` and the selection adds them in chunk order; other shapes compute
+// the FP32 logits per (expert, token) into `logits`.
+size_t router_space_bytes(int64_t T, int64_t E) {
+  return sizeof(float) * static_cast<size_t>(T) * static_cast<size_t>(kMaxRouterSplits * E);
 }
 
-int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, float* logits, uint16_t* planes,
-                 int32_t* ids, float* scores, hipStream_t st) {
+int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, float* logits, int32_t* ids,
+                 float* scores, hipStream_t st) {
   const int64_t H = r->hidden, E = r->experts;
-  if (T <= kRouterMfmaMaxTokens && router_gemm_supported(H, E, x, r->weight)) {
+  if (router_gemm_supported(H, E, x, r->weight)) {
     const RouterGemmShape shape = router_gemm_shape(T, H, E);
     RouterGemmArgs g{};
     g.x = static_cast<const uint16_t*>(x);
-    g.planes = planes;
     g.partial = space;
     g.tokens = T;
     g.hidden = H;
@@ -235,9 +159,14 @@ int route_tokens(const glm53_router* r, const void* x, int64_t T, float* space, 
     HIP_TRY(launch_router_logits(g, r->weight, st), "router logits launch");
     return topk(g.partial, r, T, ids, scores, st, static_cast<int>(shape.splits), T * E);
   }
-  HIP_TRY(launch_bf16_to_f32(static_cast<const uint16_t*>(x), space, T * H, st), "widen launch");
-  int rc = router_logits(space, r->weight, logits, T, H, E, st);
-  if (rc) return rc;
+  RouterArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.weight = r->weight;
+  a.experts = E;
+  a.hidden = H;
+  a.tokens = T;
+  a.logits_out = logits;
+  HIP_TRY(launch_router(a, st), "router launch");
   return topk(logits, r, T, ids, scores, st);
 }
 
@@ -374,8 +303,7 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
 
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
   if (tokens <= 1) return round_up(sizeof(float) * experts);
-  return round_up(router_space_bytes(tokens, hidden, experts)) + round_up(sizeof(float) * tokens * experts) +
-         round_up(router_planes_bytes(hidden, experts));
+  return round_up(router_space_bytes(tokens, experts)) + round_up(sizeof(float) * tokens * experts);
 }
 
 int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids, float* scores,
@@ -404,21 +332,40 @@ int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens,
   }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   float* space = reinterpret_cast<float*>(ws);
-  ws += round_up(router_space_bytes(tokens, router->hidden, router->experts));
-  float* logits = reinterpret_cast<float*>(ws);
-  ws += round_up(sizeof(float) * tokens * router->experts);
-  return route_tokens(router, x, tokens, space, logits, reinterpret_cast<uint16_t*>(ws), ids, scores, st);
+  float* logits = reinterpret_cast<float*>(ws + round_up(router_space_bytes(tokens, router->experts)));
+  return route_tokens(router, x, tokens, space, logits, ids, scores, st);
 }
 
 // ------------------------------------------------------------ decode ------
 
+namespace {
+
+// What one three-launch decode step reads and writes besides its inputs and
+// outputs: the plan's arena, or the library's static scratch for callers
+// that cannot allocate (glm53_decode_moe_static).
+struct StepContext {
+  int64_t H, I, Is, E, k;
+  float limit;
+  uint16_t* hidden;                  // [(k + 1) * max(I, Is)] SwiGLU rows: routed slots, then shared
+  unsigned long long* route_words;   // [E] launch-1 router words
+  uint32_t* router_count;            // launch-1 arrival counter (reset by the last arriver)
+  int32_t* ids;                      // [k]
+  float* scores;                     // [k]
+  int* err;                          // bit 0: an expert id was out of range
+  uint16_t* shared_out;              // [H] T(shared down)
+  int* step_slots;                   // cached CUs x resident workgroups of the gate/up launch (0: unknown)
+};
+
+}  // namespace
+
 struct glm53_decode_plan {
   int64_t H, I, Is, E, k;
   float limit;
-  // fixed scratch (allocated once)
+  // fixed scratch (one arena, allocated at creation)
   uint16_t* hidden = nullptr;  // [(k + 1) * max(I, Is)]
   float* sig = nullptr;        // [E] router logits
-  unsigned long long* route_words = nullptr;  // [E] three-launch step's router exchange
+  unsigned long long* route_words = nullptr;  // [E] three-launch step's router words
+  uint32_t* router_count = nullptr;           // arrival counter of the step's router launch
   int32_t* ids = nullptr;      // [k]
   float* scores = nullptr;     // [k]
   int* err = nullptr;
@@ -433,25 +380,25 @@ struct glm53_decode_plan {
   uint16_t* moe_out = nullptr;      // [H] before a residual add
   void* arena = nullptr;
   size_t arena_bytes = 0;
-  bool bound = false;
   int gate_up_rows_per_wave = 8;   // launch shape (glm53_decode_plan_tune), swept on MI355X
   int down_rows_per_wg = 16;
-  // one-launch layer kernel (layer.hip): epoch-tagged exchange words
-  int mode = GLM53_DECODE_THREE_LAUNCH;
-  uint64_t* logit_words = nullptr;   // [E]
-  uint64_t* hidden_words = nullptr;  // [(k + 1) * max(I, Is) / 2]
-  uint64_t* shared_words = nullptr;  // [H / 2]
-  uint32_t* control = nullptr;       // [4]: ticket, exits, epoch, last stale tag seen
-  int layer_grid = 0;                // persistent grid (CUs x resident workgroups), found on first use
-  int step_slots = 0;                // CUs x resident workgroups of the routed gate/up launch
-  uint32_t* router_count = nullptr;  // arrival counter of the step's router launch
-  void* exchange = nullptr;          // uncached block holding the three word arrays
-  size_t exchange_bytes = 0;
+  int step_slots = 0;              // CUs x resident workgroups of the routed gate/up launch
+  // bound weights (glm53_decode_plan_bind)
+  bool bound = false;
   glm53_bank bank{};
   glm53_shared_expert shared{};
   bool has_shared = false;
   glm53_router router{};
   bool has_router = false;
+  // read-only counters (glm53_decode_plan_counters)
+  uint64_t executions = 0;
+  uint64_t static_validations = 0;
+  uint64_t dynamic_validations = 0;
+  uint64_t host_syncs = 0;
+
+  StepContext step() {
+    return {H, I, Is, E, k, limit, hidden, route_words, router_count, ids, scores, err, shared_out, &step_slots};
+  }
 };
 
 int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate, int64_t experts,
@@ -510,39 +457,6 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
   p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
   p->moe_out = reinterpret_cast<uint16_t*>(b + o_mo);
   p->router_count = reinterpret_cast<uint32_t*>(b + o_rc);
-  {
-    size_t xo = 0;
-    auto xtake = [&](size_t bytes) {
-      size_t o = xo;
-      xo += round_up(bytes);
-      return o;
-    };
-    const size_t o_lw = xtake(8 * experts), o_hw = xtake(8 * ((top_k + 1) * Imax / 2 + 1));
-    const size_t o_sw = xtake(8 * (hidden / 2 + 1)), o_ctl = xtake(64);
-    p->exchange_bytes = xo;
-    e = uncached_take(xo, &p->exchange);
-    if (e == hipSuccess) e = hipMemset(p->exchange, 0, xo);  // tag 0: no launch's epoch
-    if (e != hipSuccess) {
-      if (p->exchange) uncached_give(p->exchange, xo);
-      (void)hipFree(p->arena);
-      delete p;
-      return hip_fail(e, "decode plan exchange words");
-    }
-    uint8_t* xb = static_cast<uint8_t*>(p->exchange);
-    p->logit_words = reinterpret_cast<uint64_t*>(xb + o_lw);
-    p->hidden_words = reinterpret_cast<uint64_t*>(xb + o_hw);
-    p->shared_words = reinterpret_cast<uint64_t*>(xb + o_sw);
-    p->control = reinterpret_cast<uint32_t*>(xb + o_ctl);
-  }
-  // epoch 1 for the first launch: the zeroed exchange words carry epoch 0
-  const uint32_t control0[16] = {0u, 0u, 1u, 0u};
-  e = hipMemcpy(p->control, control0, sizeof(control0), hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    uncached_give(p->exchange, p->exchange_bytes);
-    (void)hipFree(p->arena);
-    delete p;
-    return hip_fail(e, "decode plan control init");
-  }
   *out = p;
   return GLM53_OK;
 }
@@ -550,11 +464,11 @@ int glm53_decode_plan_create(int64_t hidden, int64_t intermediate, int64_t share
 void glm53_decode_plan_destroy(glm53_decode_plan* plan) {
   if (plan == nullptr) return;
   if (plan->arena) (void)hipFree(plan->arena);
-  uncached_give(plan->exchange, plan->exchange_bytes);
   delete plan;
 }
 
 namespace {
+
 
 int check_decode_inputs(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared) {
   CHECK_ARG(p != nullptr, "plan is null");
@@ -569,11 +483,11 @@ int check_decode_inputs(glm53_decode_plan* p, const glm53_bank* bank, const glm5
   return GLM53_OK;
 }
 
-bool decode_fast_ok(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+bool decode_fast_ok(int64_t H, int64_t I, int64_t Is, const glm53_bank* bank, const glm53_shared_expert* shared,
                     const void* x) {
-  if (!fast_width_supported(p->H) || !fast_width_supported(p->I)) return false;
-  if (p->H / 128 * 128 != p->H) return false;
-  if (shared != nullptr && p->Is != p->I) return false;
+  if (!fast_width_supported(H) || !fast_width_supported(I)) return false;
+  if (H / 128 * 128 != H) return false;
+  if (shared != nullptr && Is != I) return false;
   if (!aligned(x, 16) || !aligned(bank->gate_up_weight, 16) || !aligned(bank->down_weight, 16)) return false;
   if (shared != nullptr && (!aligned(shared->gate.weight, 16) || !aligned(shared->up.weight, 16) ||
                             !aligned(shared->down.weight, 16)))
@@ -625,7 +539,7 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
     ids = p->ids;
     scores = p->scores;
   }
-  if (decode_fast_ok(p, bank, shared, x)) {
+  if (decode_fast_ok(p->H, p->I, p->Is, bank, shared, x)) {
     GateUpArgs g{};
     g.x = static_cast<const uint16_t*>(x);
     g.expert_ids = ids;
@@ -756,128 +670,49 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
   return GLM53_OK;
 }
 
-// One launch for the whole layer when the plan allows it and the shape has
-// an instantiated kernel; returns -1 (nothing launched) otherwise.  With a
-// router the selection is computed in the launch (ids / scores land in the
-// plan); otherwise `ids` / `scores` are used.  out may alias x or residual:
-// an output row is written only after every reader of x has finished (each
-// output row waits for all SwiGLU rows, which are produced after their
-// readers' loads of x).
-int run_layer(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
-              const glm53_router* router, const void* x, const int32_t* ids, const float* scores,
-              const void* residual, void* out, hipStream_t st) {
-  if (p->mode != GLM53_DECODE_SINGLE_LAUNCH) return -1;
-  if (!decode_fast_ok(p, bank, shared, x) || !layer_shape_supported(p->H, p->I)) return -1;
-  if (router != nullptr && (router->experts > 320 || !aligned(router->weight, 16))) return -1;
-  if (p->layer_grid == 0) {
-    int dev = 0, cus = 0;
-    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
-    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
-    const int occ = layer_occupancy(p->H, p->I);
-    if (occ <= 0 || cus <= 0) return -1;
-    p->layer_grid = cus * occ;
-  }
-  const int64_t H = p->H, I = p->I;
-  const int k = static_cast<int>(p->k);
-  const int rpw = std::max(2, p->gate_up_rows_per_wave & ~1);
-  const int sdr = 16;
-  LayerArgs a{};
-  a.x = static_cast<const uint16_t*>(x);
-  a.residual = static_cast<const uint16_t*>(residual);
-  a.out = static_cast<uint16_t*>(out);
-  a.hidden = H;
-  a.intermediate = I;
-  a.experts = p->E;
-  a.top_k = k;
-  a.limit = p->limit;
-  if (router != nullptr) {
-    a.router_weight = router->weight;
-    a.router_bias = router->bias;
-    a.routed_scaling_factor = router->routed_scaling_factor;
-    a.norm_topk_prob = router->norm_topk_prob;
-  } else {
-    a.given_ids = ids;
-    a.given_scores = scores;
-  }
-  a.gate_up_weight = bank->gate_up_weight;
-  a.gate_up_scale = bank->gate_up_scale_inv;
-  a.down_weight = bank->down_weight;
-  a.down_scale = bank->down_scale_inv;
-  a.routed_flags = bank->code_flags;
-  if (shared != nullptr) {
-    a.shared_gate_weight = shared->gate.weight;
-    a.shared_gate_scale = shared->gate.scale_inv;
-    a.shared_up_weight = shared->up.weight;
-    a.shared_up_scale = shared->up.scale_inv;
-    a.shared_down_weight = shared->down.weight;
-    a.shared_down_scale = shared->down.scale_inv;
-    a.shared_gate_flags = shared->gate.code_flags;
-    a.shared_up_flags = shared->up.code_flags;
-    a.shared_down_flags = shared->down.code_flags;
-  }
-  a.logits = p->logit_words;
-  a.hidden_words = p->hidden_words;
-  a.hidden_plain = p->hidden;
-  a.shared_words = p->shared_words;
-  a.control = p->control;
-  a.ids_out = p->ids;
-  a.scores_out = p->scores;
-  a.error_flag = p->err;
-  const int gu_items = static_cast<int>(cdiv(I, 4 * rpw));
-  a.n_router = router != nullptr ? static_cast<int>(cdiv(p->E, 4)) : 0;
-  a.n_shared_gu = shared != nullptr ? gu_items : 0;
-  a.n_routed_gu = k * gu_items;
-  a.n_shared_down = shared != nullptr ? static_cast<int>(cdiv(H, 4 * sdr)) : 0;
-  a.n_down = static_cast<int>(cdiv(H, kLayerDownRows));
-  a.gu_rows_per_wave = rpw;
-  a.shared_down_rows_per_wave = sdr;
-  const int items = a.n_router + a.n_shared_gu + a.n_routed_gu + a.n_shared_down + a.n_down;
-  const int grid = std::min(items, p->layer_grid);
-  HIP_TRY(launch_decode_layer(a, grid, st), "decode layer launch");
-  return GLM53_OK;
-}
-
 // The three-launch step (step.hip) when the shape is instantiated; returns
 // -1 (nothing launched) otherwise.  router != NULL: launch 1 computes the
-// logits and the selection into the plan's ids / scores; else `ids` /
-// `scores` are the caller's.
-int run_step(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+// logits and the selection into the context's ids / scores; else the
+// routed launches read `ids` / `scores`, or the context's when those are
+// NULL (the selection of an earlier router stage).
+int run_step(const StepContext& c, const glm53_bank* bank, const glm53_shared_expert* shared,
              const glm53_router* router, const void* x, const int32_t* ids, const float* scores,
-             const void* residual, void* out, int stages, hipStream_t st) {
-  if (!decode_fast_ok(p, bank, shared, x) || !step_shape_supported(p->H, p->I)) return -1;
+             const void* residual, void* out, int stages, int gate_up_rows_per_wave, hipStream_t st) {
+  (void)gate_up_rows_per_wave;
+  if (!decode_fast_ok(c.H, c.I, c.Is, bank, shared, x) || !step_shape_supported(c.H, c.I)) return -1;
   if (router != nullptr && (router->experts > 320 || !aligned(router->weight, 16))) return -1;
   if (!aligned(out, 4)) return -1;
-  if (p->step_slots == 0) {
+  if (*c.step_slots == 0) {
     int dev = 0, cus = 0;
     HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
-    const int occ = step_gate_up_occupancy(p->H, p->I);
+    const int occ = step_gate_up_occupancy(c.H, c.I);
     if (occ <= 0 || cus <= 0) return -1;
-    p->step_slots = cus * occ;
+    *c.step_slots = cus * occ;
   }
   StepArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.residual = static_cast<const uint16_t*>(residual);
   a.out = static_cast<uint16_t*>(out);
-  a.hidden = p->H;
-  a.intermediate = p->I;
-  a.experts = p->E;
-  a.top_k = static_cast<int>(p->k);
-  a.limit = p->limit;
+  a.hidden = c.H;
+  a.intermediate = c.I;
+  a.experts = c.E;
+  a.top_k = static_cast<int>(c.k);
+  a.limit = c.limit;
   if (router != nullptr) {
     a.router_weight = router->weight;
     a.router_bias = router->bias;
     a.routed_scaling_factor = router->routed_scaling_factor;
     a.norm_topk_prob = router->norm_topk_prob;
-    a.ids = p->ids;
-    a.scores = p->scores;
-    a.router_wgs = static_cast<int>(cdiv(p->E, 4));
+    a.ids = c.ids;
+    a.scores = c.scores;
+    a.router_wgs = static_cast<int>(cdiv(c.E, 4));
   } else {
-    a.ids = const_cast<int32_t*>(ids);
-    a.scores = const_cast<float*>(scores);
+    a.ids = ids != nullptr ? const_cast<int32_t*>(ids) : c.ids;
+    a.scores = scores != nullptr ? const_cast<float*>(scores) : c.scores;
   }
-  a.route_words = p->route_words;
-  a.router_count = p->router_count;
+  a.route_words = c.route_words;
+  a.router_count = c.router_count;
   a.gate_up_weight = bank->gate_up_weight;
   a.gate_up_scale = bank->gate_up_scale_inv;
   a.down_weight = bank->down_weight;
@@ -894,13 +729,13 @@ int run_step(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_ex
     a.shared_up_flags = shared->up.code_flags;
     a.shared_down_flags = shared->down.code_flags;
   }
-  a.hidden_act = p->hidden;
-  a.shared_out = p->shared_out;
-  a.error_flag = p->err;
+  a.hidden_act = c.hidden;
+  a.shared_out = c.shared_out;
+  a.error_flag = c.err;
   a.shared_rows_per_wave = 2;
   a.shared_delay = kStepSharedDelay;
-  const int sd_wgs = shared != nullptr ? static_cast<int>(cdiv(p->H, 64)) : 0;
-  a.routed_wgs = std::max(64, p->step_slots - sd_wgs);
+  const int sd_wgs = shared != nullptr ? static_cast<int>(cdiv(c.H, 64)) : 0;
+  a.routed_wgs = std::max(64, *c.step_slots - sd_wgs);
   HIP_TRY(launch_step(a, stages, st), "decode step launch");
   return GLM53_OK;
 }
@@ -916,18 +751,40 @@ int run_router_decode(glm53_decode_plan* p, const glm53_router* r, const void* x
   return GLM53_OK;
 }
 
+// Routed + shared decode with caller-chosen (ids, scores): the step kernels
+// when the shape has them, else the any-shape composition.
+int decode_routed_impl(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                       const void* x, const int32_t* ids, const float* scores, void* out, hipStream_t st) {
+  int rc = run_step(p->step(), bank, shared, nullptr, x, ids, scores, nullptr, out, GLM53_STAGE_ALL,
+                    p->gate_up_rows_per_wave, st);
+  if (rc < 0) rc = run_decode(p, bank, shared, x, ids, scores, nullptr, nullptr, out, GLM53_STAGE_ALL, st);
+  if (rc == GLM53_OK) ++p->executions;
+  return rc;
+}
+
+// Router + routed + shared decode; ids / scores land in the plan.
+int decode_full_impl(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_expert* shared,
+                     const glm53_router* router, const void* x, void* out, hipStream_t st) {
+  int rc = run_step(p->step(), bank, shared, router, x, nullptr, nullptr, nullptr, out, GLM53_STAGE_ALL,
+                    p->gate_up_rows_per_wave, st);
+  if (rc < 0) {
+    if ((rc = run_router_decode(p, router, x, st))) return rc;
+    rc = run_decode(p, bank, shared, x, p->ids, p->scores, router, nullptr, out, GLM53_STAGE_ALL, st);
+  }
+  if (rc == GLM53_OK) ++p->executions;
+  return rc;
+}
+
 }  // namespace
 
 int glm53_decode_moe_routed(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
                             const void* x, const int32_t* expert_ids, const float* scores, void* out, void* stream) {
   int rc = check_decode_inputs(plan, bank, shared);
   if (rc) return rc;
+  ++plan->static_validations;
   CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
-  rc = run_layer(plan, bank, shared, nullptr, x, expert_ids, scores, nullptr, out, S(stream));
-  if (rc >= 0) return rc;
-  rc = run_step(plan, bank, shared, nullptr, x, expert_ids, scores, nullptr, out, GLM53_STAGE_ALL, S(stream));
-  if (rc >= 0) return rc;
-  return run_decode(plan, bank, shared, x, expert_ids, scores, nullptr, nullptr, out, GLM53_STAGE_ALL, S(stream));
+  ++plan->dynamic_validations;
+  return decode_routed_impl(plan, bank, shared, x, expert_ids, scores, out, S(stream));
 }
 
 int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
@@ -936,16 +793,11 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank, const glm5
   int rc = check_decode_inputs(plan, bank, shared);
   if (rc) return rc;
   if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  ++plan->static_validations;
   CHECK_ARG(x && out, "null pointer argument");
+  ++plan->dynamic_validations;
   hipStream_t st = S(stream);
-  rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, nullptr, out, st);
-  if (rc < 0) rc = run_step(plan, bank, shared, router, x, nullptr, nullptr, nullptr, out, GLM53_STAGE_ALL, st);
-  if (rc > 0) return rc;
-  if (rc < 0) {
-    if ((rc = run_router_decode(plan, router, x, st))) return rc;
-    if ((rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, nullptr, out, GLM53_STAGE_ALL, st)))
-      return rc;
-  }
+  if ((rc = decode_full_impl(plan, bank, shared, router, x, out, st))) return rc;
   if (ids_out) HIP_TRY(hipMemcpyAsync(ids_out, plan->ids, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy ids");
   if (scores_out)
     HIP_TRY(hipMemcpyAsync(scores_out, plan->scores, 4 * plan->k, hipMemcpyDeviceToDevice, st), "copy scores");
@@ -958,12 +810,13 @@ int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank, cons
   if (plan->bound) return fail(GLM53_BAD_STATE, "decode plan weights are already bound");
   int rc = check_decode_inputs(plan, bank, shared);
   if (rc) return rc;
-  if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  if (router != nullptr && (rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
+  ++plan->static_validations;
   plan->bank = *bank;
   plan->has_shared = shared != nullptr;
   if (shared) plan->shared = *shared;
-  plan->router = *router;
-  plan->has_router = true;
+  plan->has_router = router != nullptr;
+  if (router) plan->router = *router;
   plan->bound = true;
   return GLM53_OK;
 }
@@ -971,16 +824,21 @@ int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank, cons
 int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, void* stream) {
   CHECK_ARG(plan != nullptr, "plan is null");
   if (!plan->bound) return fail(GLM53_BAD_STATE, "decode plan has no bound weights");
+  if (!plan->has_router) return fail(GLM53_BAD_STATE, "decode plan was bound without a router");
   CHECK_ARG(x && out, "null pointer argument");
-  hipStream_t st = S(stream);
-  const glm53_shared_expert* shared = plan->has_shared ? &plan->shared : nullptr;
-  int rc = run_layer(plan, &plan->bank, shared, &plan->router, x, nullptr, nullptr, nullptr, out, st);
-  if (rc >= 0) return rc;
-  rc = run_step(plan, &plan->bank, shared, &plan->router, x, nullptr, nullptr, nullptr, out, GLM53_STAGE_ALL, st);
-  if (rc >= 0) return rc;
-  if ((rc = run_router_decode(plan, &plan->router, x, st))) return rc;
-  return run_decode(plan, &plan->bank, shared, x, plan->ids, plan->scores, &plan->router, nullptr, out,
-                    GLM53_STAGE_ALL, st);
+  ++plan->dynamic_validations;
+  return decode_full_impl(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, &plan->router, x, out,
+                          S(stream));
+}
+
+int glm53_decode_moe_bound_routed(glm53_decode_plan* plan, const void* x, const int32_t* expert_ids,
+                                  const float* scores, void* out, void* stream) {
+  CHECK_ARG(plan != nullptr, "plan is null");
+  if (!plan->bound) return fail(GLM53_BAD_STATE, "decode plan has no bound weights");
+  CHECK_ARG(x && expert_ids && scores && out, "null pointer argument");
+  ++plan->dynamic_validations;
+  return decode_routed_impl(plan, &plan->bank, plan->has_shared ? &plan->shared : nullptr, x, expert_ids, scores,
+                            out, S(stream));
 }
 
 int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const glm53_shared_expert* shared,
@@ -990,22 +848,26 @@ int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank, const g
   if (rc) return rc;
   CHECK_ARG(x && out, "null pointer argument");
   CHECK_ARG(stages > 0 && (stages & ~GLM53_STAGE_ALL) == 0, "invalid stage mask %d", stages);
-  hipStream_t st = S(stream);
-  if (stages & (GLM53_STAGE_ROUTER | GLM53_STAGE_GATE_UP)) {
+  if (stages & GLM53_STAGE_ROUTER) {
     if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
   }
-  if (stages == GLM53_STAGE_ALL) {
-    rc = run_layer(plan, bank, shared, router, x, nullptr, nullptr, residual, out, st);
-    if (rc >= 0) return rc;
-  }
-  rc = run_step(plan, bank, shared, router, x, nullptr, nullptr, residual, out, stages, st);
-  if (rc >= 0) return rc;
-  if (stages & GLM53_STAGE_ROUTER) {
+  ++plan->static_validations;
+  ++plan->dynamic_validations;
+  hipStream_t st = S(stream);
+  // Without the router stage the routed launches read the selection the
+  // plan holds (written by an earlier call's router stage).
+  const glm53_router* stage_router = (stages & GLM53_STAGE_ROUTER) ? router : nullptr;
+  rc = run_step(plan->step(), bank, shared, stage_router, x, nullptr, nullptr, residual, out, stages,
+                plan->gate_up_rows_per_wave, st);
+  if (rc < 0) {
+    CHECK_ARG(stages == GLM53_STAGE_ALL && router != nullptr,
+              "partial stage masks need the fused step shapes (aligned pointers, instantiated widths)");
+    if ((rc = check_router(router, plan->H, plan->E, plan->k))) return rc;
     if ((rc = run_router_decode(plan, router, x, st))) return rc;
+    rc = run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, residual, out, GLM53_STAGE_ALL, st);
   }
-  if (stages & (GLM53_STAGE_GATE_UP | GLM53_STAGE_DOWN))
-    return run_decode(plan, bank, shared, x, plan->ids, plan->scores, router, residual, out, stages, st);
-  return GLM53_OK;
+  if (rc == GLM53_OK) ++plan->executions;
+  return rc;
 }
 
 int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wave, int32_t down_rows_per_wg) {
@@ -1015,13 +877,6 @@ int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wav
             kMaxDownRowsPerWg);
   plan->gate_up_rows_per_wave = gate_up_rows_per_wave;
   plan->down_rows_per_wg = down_rows_per_wg;
-  return GLM53_OK;
-}
-
-int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode) {
-  CHECK_ARG(plan != nullptr, "plan is null");
-  CHECK_ARG(mode == GLM53_DECODE_THREE_LAUNCH || mode == GLM53_DECODE_SINGLE_LAUNCH, "unknown decode mode %d", mode);
-  plan->mode = mode;
   return GLM53_OK;
 }
 
@@ -1041,12 +896,16 @@ int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr
       *bytes = 4 * plan->k;
       return GLM53_OK;
     case 3:
-      *ptr = plan->control;
-      *bytes = 64;
+      *ptr = plan->route_words;
+      *bytes = 8 * plan->E;
       return GLM53_OK;
     case 4:
       *ptr = plan->arena;
       *bytes = plan->arena_bytes;
+      return GLM53_OK;
+    case 5:
+      *ptr = plan->shared_out;
+      *bytes = 2 * plan->H;
       return GLM53_OK;
     default:
       return fail(GLM53_INVALID_ARGUMENT, "unknown scratch id %d", which);
@@ -1057,8 +916,60 @@ int glm53_decode_plan_error_flag(glm53_decode_plan* plan, int32_t* host_value) {
   CHECK_ARG(plan && host_value, "null pointer argument");
   HIP_TRY(hipMemcpy(host_value, plan->err, sizeof(int32_t), hipMemcpyDeviceToHost), "read error flag");
   HIP_TRY(hipMemset(plan->err, 0, sizeof(int32_t)), "clear error flag");
+  ++plan->host_syncs;
   return GLM53_OK;
 }
+
+int glm53_decode_plan_counters(const glm53_decode_plan* plan, glm53_plan_counters* out) {
+  CHECK_ARG(plan && out, "null pointer argument");
+  *out = glm53_plan_counters{};
+  out->execution_count = plan->executions;
+  out->dynamic_allocation_count = 0;
+  out->host_synchronization_count = plan->host_syncs;
+  out->static_input_validation_count = plan->static_validations;
+  out->dynamic_input_validation_count = plan->dynamic_validations;
+  out->scratch_bytes = plan->arena_bytes;
+  out->weights_bound = plan->bound ? 1 : 0;
+  out->router_bound = plan->has_router ? 1 : 0;
+  return GLM53_OK;
+}
+
+int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, uint64_t* out, int32_t capacity,
+                                 int32_t* count) {
+  CHECK_ARG(plan && count && (capacity == 0 || out), "null pointer argument");
+  uint64_t ids[16];
+  int n = 0;
+  auto put = [&](const void* q) { ids[n++] = reinterpret_cast<uint64_t>(q); };
+  if (which == 0) {
+    for (const void* q : {static_cast<const void*>(plan->hidden), static_cast<const void*>(plan->sig),
+                          static_cast<const void*>(plan->route_words), static_cast<const void*>(plan->ids),
+                          static_cast<const void*>(plan->scores), static_cast<const void*>(plan->err),
+                          static_cast<const void*>(plan->shared_out), static_cast<const void*>(plan->router_count)})
+      put(q);
+  } else if (which == 1) {
+    if (!plan->bound) return fail(GLM53_BAD_STATE, "decode plan has no bound weights");
+    put(plan->bank.gate_up_weight);
+    put(plan->bank.gate_up_scale_inv);
+    put(plan->bank.down_weight);
+    put(plan->bank.down_scale_inv);
+    if (plan->has_shared) {
+      for (const glm53_linear* l : {&plan->shared.gate, &plan->shared.up, &plan->shared.down}) {
+        put(l->weight);
+        put(l->scale_inv);
+      }
+    }
+    if (plan->has_router) {
+      put(plan->router.weight);
+      put(plan->router.bias);
+    }
+  } else {
+    return fail(GLM53_INVALID_ARGUMENT, "unknown identity set %d", which);
+  }
+  *count = n;
+  for (int i = 0; i < n && i < capacity; ++i) out[i] = ids[i];
+  return GLM53_OK;
+}
+
 
 // ---------------------------------------------------- prefill pieces ------
 
@@ -1261,8 +1172,7 @@ struct glm53_prefill_plan {
   int64_t capacity_max;
   void* arena = nullptr;
   // router
-  float* xf = nullptr;
-  uint16_t* router_planes = nullptr;  // [3][E][H] BF16 parts of the router weights
+  float* router_partial = nullptr;  // [kMaxRouterSplits, T, E] router partial sums
   float* logits = nullptr;
   int32_t* ids = nullptr;
   float* scores = nullptr;
@@ -1284,6 +1194,12 @@ struct glm53_prefill_plan {
   int32_t* flags = nullptr;        // [4] code flags scanned when the caller has none: bank gate/up, bank
                                    // down, shared gate + up, shared down
   int64_t last_tokens = 0;
+  size_t arena_bytes = 0;
+  // read-only counters (glm53_prefill_plan_counters)
+  uint64_t executions = 0;
+  uint64_t static_validations = 0;
+  uint64_t dynamic_validations = 0;
+  uint64_t host_syncs = 0;
 };
 
 int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shared_intermediate, int64_t experts,
@@ -1313,9 +1229,8 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
     off += round_up(bytes);
     return o;
   };
-  size_t o_xf = take(router_space_bytes(T, hidden, experts)), o_logits = take(4 * T * experts), o_ids = take(4 * R),
+  size_t o_xf = take(router_space_bytes(T, experts)), o_logits = take(4 * T * experts), o_ids = take(4 * R),
          o_scores = take(4 * R);
-  size_t o_planes = take(router_planes_bytes(hidden, experts));
   size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(R, intermediate)), o_sq = take(split_bytes(T, Ism));
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
   size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
@@ -1323,6 +1238,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   size_t o_te = take(4 * p->capacity_max), o_ts = take(4 * p->capacity_max), o_tl = take(4 * p->capacity_max);
   size_t o_h = take(2 * R * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
   size_t o_so = take(2 * T * hidden), o_flags = take(32);
+  p->arena_bytes = off;
   hipError_t e = hipMalloc(&p->arena, off);
   if (e != hipSuccess) {
     delete p;
@@ -1335,8 +1251,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
     return hip_fail(e, "prefill plan hipMemset");
   }
   uint8_t* b = static_cast<uint8_t*>(p->arena);
-  p->xf = reinterpret_cast<float*>(b + o_xf);
-  p->router_planes = reinterpret_cast<uint16_t*>(b + o_planes);
+  p->router_partial = reinterpret_cast<float*>(b + o_xf);
   p->logits = reinterpret_cast<float*>(b + o_logits);
   p->ids = reinterpret_cast<int32_t*>(b + o_ids);
   p->scores = reinterpret_cast<float*>(b + o_scores);
@@ -1396,16 +1311,18 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   } else {
     CHECK_ARG(scores != nullptr, "scores are required with expert_ids");
   }
+  ++p->static_validations;
   p->last_tokens = tokens;
   if (tokens == 0) return GLM53_OK;
   CHECK_ARG(x && (out || hc_out), "null pointer argument");
+  ++p->dynamic_validations;
   hipStream_t st = S(stream);
   const int64_t T = tokens, k = p->k, R = T * k, H = p->H, I = p->I, Is = p->Is, E = p->E;
   const int64_t SC = H / 128, SR = I / 128, SI = I / 128;
   const int32_t* ids = expert_ids;
   const float* sc = scores;
   if (ids == nullptr) {
-    if ((rc = route_tokens(router, x, T, p->xf, p->logits, p->router_planes, p->ids, p->scores, st))) return rc;
+    if ((rc = route_tokens(router, x, T, p->router_partial, p->logits, p->ids, p->scores, st))) return rc;
     ids = p->ids;
     sc = p->scores;
   } else {
@@ -1591,6 +1508,7 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   r.hc_comb = hc_comb;
   r.hc_out = static_cast<uint16_t*>(hc_out);
   HIP_TRY(launch_reduce(r, reduction == GLM53_REDUCE_DIRECT, st), "reduce launch");
+  ++p->executions;
   return GLM53_OK;
 }
 
@@ -1618,6 +1536,30 @@ int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes
     return GLM53_OK;
   }
   HIP_TRY(hipMemcpy(invalid_routes, plan->status, sizeof(uint32_t), hipMemcpyDeviceToHost), "read status");
+  ++plan->host_syncs;
+  return GLM53_OK;
+}
+
+int glm53_prefill_plan_counters(const glm53_prefill_plan* plan, glm53_plan_counters* out) {
+  CHECK_ARG(plan && out, "null pointer argument");
+  *out = glm53_plan_counters{};
+  out->execution_count = plan->executions;
+  out->dynamic_allocation_count = 0;
+  out->host_synchronization_count = plan->host_syncs;
+  out->static_input_validation_count = plan->static_validations;
+  out->dynamic_input_validation_count = plan->dynamic_validations;
+  out->scratch_bytes = plan->arena_bytes;
+  return GLM53_OK;
+}
+
+int glm53_prefill_plan_identities(const glm53_prefill_plan* plan, uint64_t* out, int32_t capacity, int32_t* count) {
+  CHECK_ARG(plan && count && (capacity == 0 || out), "null pointer argument");
+  const void* bufs[] = {plan->router_partial, plan->logits, plan->ids, plan->scores, plan->xq.hi,
+                        plan->hq.hi, plan->sq.hi, plan->plan_ws, plan->sorted_route, plan->inverse,
+                        plan->tile_expert, plan->h, plan->down, plan->hs, plan->shared_out, plan->flags};
+  const int n = static_cast<int>(sizeof(bufs) / sizeof(bufs[0]));
+  *count = n;
+  for (int i = 0; i < n && i < capacity; ++i) out[i] = reinterpret_cast<uint64_t>(bufs[i]);
   return GLM53_OK;
 }
 

@@ -242,32 +242,36 @@ __global__ __launch_bounds__(64 * (kMaxTopK + 1)) void down_reduce_kernel(DownAr
 
 // ----------------------------------------------------------------- router --
 //
-// patch.py:133: logits = x_f32 . W_f32^T in FP32, one workgroup per expert
-// row (16 KB for H = 4096), no cross-workgroup traffic; selection runs in the
-// consumer (gate/up prologue or topk_kernel).
+// patch.py:133: logits = x_f32 . W_f32^T in FP32, one workgroup per (expert
+// row, token) (16 KB of weights for H = 4096), no cross-workgroup traffic;
+// selection runs in the consumer (topk_kernel).  The one-token router, and
+// the many-token router for shapes the BF16-MFMA form does not take.
 __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
   __shared__ float partial[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t e = blockIdx.x;
+  const int64_t tok = blockIdx.y;
   const float* w = a.weight + e * a.hidden;
+  const uint16_t* x = a.x + tok * a.hidden;
   float acc = 0.0f;
-  if ((a.hidden & 3) == 0) {
+  if ((a.hidden & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 7) == 0 &&
+      (reinterpret_cast<uintptr_t>(a.weight) & 15) == 0) {
     for (int64_t k = 4 * static_cast<int64_t>(threadIdx.x); k < a.hidden; k += 1024) {
       float4 wv = *reinterpret_cast<const float4*>(w + k);
-      uint2 xv = *reinterpret_cast<const uint2*>(a.x + k);
+      uint2 xv = *reinterpret_cast<const uint2*>(x + k);
       acc = fmaf(__uint_as_float(xv.x << 16), wv.x, acc);
       acc = fmaf(__uint_as_float(xv.x & 0xffff0000u), wv.y, acc);
       acc = fmaf(__uint_as_float(xv.y << 16), wv.z, acc);
       acc = fmaf(__uint_as_float(xv.y & 0xffff0000u), wv.w, acc);
     }
   } else {
-    for (int64_t k = threadIdx.x; k < a.hidden; k += 256) acc = fmaf(bf16_to_f32(a.x[k]), w[k], acc);
+    for (int64_t k = threadIdx.x; k < a.hidden; k += 256) acc = fmaf(bf16_to_f32(x[k]), w[k], acc);
   }
   acc = wave_sum(acc);
   if (lane == 0) partial[wave] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) a.logits_out[e] = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+  if (threadIdx.x == 0) a.logits_out[tok * a.experts + e] = (partial[0] + partial[1]) + (partial[2] + partial[3]);
 }
 
 // ---------------------------------------------------------- plain GEMV ----
@@ -421,24 +425,6 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
               lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
   }
-}
-
-// BF16 -> FP32 widening of the router input (patch.py:133 x.astype(float32)).
-// Thread = 8 elements: one 16-byte load, two 16-byte stores (x and y
-// 16-byte aligned, n a multiple of 8); bf16_to_f32_tail_kernel otherwise.
-__global__ void bf16_to_f32_kernel(const uint16_t* x, float* y, int64_t n) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-  if (i >= n) return;
-  const uint4 v = *reinterpret_cast<const uint4*>(x + i);
-  *reinterpret_cast<float4*>(y + i) = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                                                  __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
-  *reinterpret_cast<float4*>(y + i + 4) = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xffff0000u),
-                                                      __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xffff0000u));
-}
-
-__global__ void bf16_to_f32_tail_kernel(const uint16_t* x, float* y, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = bf16_to_f32(x[i]);
 }
 
 // ------------------------------------------------------- generic path ----
@@ -641,18 +627,9 @@ hipError_t launch_topk(const TopkArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st) {
-  if (n == 0) return hipSuccess;
-  if (n % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0)
-    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0, st, x, y, n);
-  else
-    hipLaunchKernelGGL(bf16_to_f32_tail_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, x, y,
-                       n);
-  return hipGetLastError();
-}
-
 hipError_t launch_router(const RouterArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(router_logits_kernel, dim3(static_cast<unsigned>(a.experts)), dim3(256), 0, st, a);
+  const unsigned tokens = a.tokens > 1 ? static_cast<unsigned>(a.tokens) : 1u;
+  hipLaunchKernelGGL(router_logits_kernel, dim3(static_cast<unsigned>(a.experts), tokens), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

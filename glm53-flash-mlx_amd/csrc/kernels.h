@@ -110,59 +110,12 @@ bool step_shape_supported(int64_t H, int64_t I);
 int step_gate_up_occupancy(int64_t H, int64_t I);
 hipError_t launch_step(const StepArgs& a, int stages, hipStream_t st);
 
-// One-launch decode layer (layer.hip).
-constexpr int kLayerDownRows = 16;  // output rows of one routed down item
-
-struct LayerArgs {
-  const uint16_t* x;              // [H] bf16
-  const uint16_t* residual;       // [H] bf16 or null
-  uint16_t* out;                  // [H] bf16
-  int64_t hidden, intermediate;   // H, I (shared expert width == I)
-  int64_t experts;
-  int top_k;
-  float limit;
-  // routing: router (weight non-null) or given ids / scores
-  const float* router_weight;     // [E, H]
-  const float* router_bias;       // [E]
-  float routed_scaling_factor;
-  int norm_topk_prob;
-  const int32_t* given_ids;       // [top_k] or null
-  const float* given_scores;      // [top_k]
-  // packed bank and shared expert (shared pointers null when absent)
-  const uint8_t* gate_up_weight;
-  const float* gate_up_scale;
-  const uint8_t* down_weight;
-  const float* down_scale;
-  const uint8_t* shared_gate_weight;
-  const float* shared_gate_scale;
-  const uint8_t* shared_up_weight;
-  const float* shared_up_scale;
-  const uint8_t* shared_down_weight;
-  const float* shared_down_scale;
-  const int32_t* routed_flags;
-  const int32_t* shared_gate_flags;
-  const int32_t* shared_up_flags;
-  const int32_t* shared_down_flags;
-  // plan scratch
-  uint64_t* logits;               // [E] epoch-tagged FP32
-  uint64_t* hidden_words;         // [(top_k + 1) * I / 2] epoch-tagged BF16 pairs
-  uint16_t* hidden_plain;         // [(top_k + 1) * I] bf16 copy (diagnostics)
-  uint64_t* shared_words;         // [H / 2] epoch-tagged BF16 pairs (shared down)
-  uint32_t* control;              // [0] ticket, [1] exits, [2] epoch
-  int32_t* ids_out;               // [top_k]
-  float* scores_out;              // [top_k]
-  int* error_flag;
-  // work items, in ticket order
-  int n_router, n_shared_gu, n_routed_gu, n_shared_down, n_down;
-  int gu_rows_per_wave;           // even
-  int shared_down_rows_per_wave;  // even
-};
-
 struct RouterArgs {
-  const uint16_t* x;       // [H] bf16
+  const uint16_t* x;       // [tokens, H] bf16
   const float* weight;     // [E, H]
   int64_t experts, hidden;
-  float* logits_out;       // [E] FP32
+  int64_t tokens;          // 0 or 1: one token
+  float* logits_out;       // [tokens, E] FP32
 };
 
 struct GenericLinearArgs {
@@ -227,9 +180,6 @@ struct TopkArgs {
 constexpr int kGenericRows = 8;
 
 bool fast_width_supported(int64_t K);
-bool layer_shape_supported(int64_t H, int64_t I);
-int layer_occupancy(int64_t H, int64_t I);
-hipError_t launch_decode_layer(const LayerArgs& a, int grid, hipStream_t st);
 hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st);
 hipError_t launch_down(const DownArgs& a, hipStream_t st);
 hipError_t launch_router(const RouterArgs& a, hipStream_t st);
@@ -240,10 +190,10 @@ hipError_t launch_gemv_split(const GemvArgs& a, hipStream_t st);  // rows_per_wa
 hipError_t launch_topk(const TopkArgs& a, hipStream_t st);
 
 // Router logits for many tokens on BF16 MFMA (exact three-way BF16 split of
-// the FP32 weights): partial sums per K chunk, [splits][tokens][experts].
+// the FP32 weights, done as the weights go into LDS): partial sums per K
+// chunk, [splits][tokens][experts].
 struct RouterGemmArgs {
   const uint16_t* x;      // [tokens, hidden] bf16, 16-byte aligned rows
-  uint16_t* planes;       // [3][experts][hidden] BF16 parts of the FP32 weights (written by the launch)
   float* partial;         // [splits, tokens, experts]
   int64_t tokens, hidden, experts;
   int64_t token_groups, expert_groups, k_chunk, splits;
@@ -254,9 +204,7 @@ struct RouterGemmShape {
 };
 bool router_gemm_supported(int64_t hidden, int64_t experts, const void* x, const void* weight);
 RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t experts);
-size_t router_planes_bytes(int64_t hidden, int64_t experts);
 hipError_t launch_router_logits(const RouterGemmArgs& a, const float* weight, hipStream_t st);
-hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, int64_t n, hipStream_t st);
 hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st);
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st);
 hipError_t launch_weighted_reduction(const WeightedReductionArgs& a, hipStream_t st);

@@ -7,18 +7,18 @@
 // w = hi + mid + lo.  A BF16 activation times a BF16 part is exact in FP32,
 // so three v_mfma_f32_16x16x32_bf16 per operand pair accumulate x . w in
 // FP32 like an FP32 GEMM; only the order of the FP32 additions differs.
-// router_planes_kernel writes the three parts once per call as BF16 planes
-// [3][experts][hidden]; the GEMM then only loads and multiplies.
 //
-// GEMM work item = 64 tokens (four 16-row MFMA tiles) x 4 NT expert tiles of
-// 16 x one K chunk; wavefront w owns expert tiles w, w + 4, ... of the item.
-// Each lane reads its operands straight from global memory as 16-byte BF16
-// runs (row lane % 16, K run 8 (lane / 16) of each 32-deep step; any K
-// order works as long as both operands use the same one), double-buffered
-// one step ahead.  K chunks ("splits") write FP32 partial sums [split]
-// [token][expert]; topk_kernel adds them in split order.  Items run
+// Work item = 128 tokens x 96 experts x one K chunk, 4 wavefronts in a 2 x 2
+// grid (64 tokens x 48 experts each: 4 x 3 MFMA tiles).  Per 32-deep K step
+// the workgroup loads the tokens' BF16 rows (8 KB) and the experts' FP32 rows
+// (12 KB) once from global memory into registers, one step ahead, splits
+// the weights into their three BF16 parts on the way into LDS (18 KB), and
+// every wavefront reads its MFMA operands from LDS: each operand byte leaves
+// L2 once per workgroup (the register-operand form read the token rows once
+// per wavefront).  K chunks ("splits") write FP32 partial sums
+// [split][token][expert]; topk_kernel adds them in split order.  Items run
 // split-major in contiguous runs per XCD, so the items of one split share
-// that chunk's weight planes in one L2.
+// that chunk's weight rows in one L2.
 
 #include "common.h"
 #include "kernels.h"
@@ -30,135 +30,148 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRouterTileTokens = 64;
-constexpr int kRouterTilesPerWave = 2;  // NT: 8 expert tiles (128 experts) per work item
+constexpr int kTileTokens = 128;
+constexpr int kTileExperts = 96;
+constexpr int kStep = 32;                       // K per step: one v_mfma_f32_16x16x32_bf16
+constexpr int kRowBytes = kStep * 2;            // 64 B: one BF16 row of a step in LDS
+constexpr int kXBytes = kTileTokens * kRowBytes;   // 8 KB
+constexpr int kPlaneBytes = kTileExperts * kRowBytes;  // 6 KB per BF16 part
+constexpr int kStageBytes = kXBytes + 3 * kPlaneBytes;  // 26 KB
 
-// Thread = 8 consecutive weights: two 16-byte FP32 loads, three 16-byte BF16 stores.
-__global__ __launch_bounds__(256) void router_planes_kernel(const float* w, uint16_t* planes, int64_t n) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
-  if (i >= n) return;
-  const float4 a = *reinterpret_cast<const float4*>(w + i);
-  const float4 b = *reinterpret_cast<const float4*>(w + i + 4);
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+// Octet q (8 BF16 = 16 B) of LDS row r sits at slot q ^ ((r >> 2) & 3): the
+// 16 lanes reading octet q of rows r .. r + 15 then spread over all banks.
+__device__ __forceinline__ int slot_offset(int r, int q) { return r * kRowBytes + 16 * (q ^ ((r >> 2) & 3)); }
+
+// The three BF16 parts of four FP32 weights, packed two per word.
+__device__ __forceinline__ void split3(const float4& v, uint2& hi, uint2& mid, uint2& lo) {
+  const float in[4] = {v.x, v.y, v.z, v.w};
   uint32_t h[4], m[4], l[4];
 #pragma unroll
-  for (int k = 0; k < 8; k += 2) {
-    uint32_t hb[2], mb[2], lb[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t b0 = __float_as_uint(v[k + j]) & 0xffff0000u;
-      const float r1 = v[k + j] - __uint_as_float(b0);
-      const uint32_t b1 = __float_as_uint(r1) & 0xffff0000u;
-      const float r2 = r1 - __uint_as_float(b1);
-      hb[j] = b0;
-      mb[j] = b1;
-      lb[j] = __float_as_uint(r2) & 0xffff0000u;  // r2 already fits in BF16
-    }
-    h[k >> 1] = (hb[0] >> 16) | hb[1];
-    m[k >> 1] = (mb[0] >> 16) | mb[1];
-    l[k >> 1] = (lb[0] >> 16) | lb[1];
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t b0 = __float_as_uint(in[j]) & 0xffff0000u;
+    const float r1 = in[j] - __uint_as_float(b0);
+    const uint32_t b1 = __float_as_uint(r1) & 0xffff0000u;
+    const float r2 = r1 - __uint_as_float(b1);
+    h[j] = b0;
+    m[j] = b1;
+    l[j] = __float_as_uint(r2) & 0xffff0000u;  // r2 already fits in BF16
   }
-  *reinterpret_cast<uint4*>(planes + i) = make_uint4(h[0], h[1], h[2], h[3]);
-  *reinterpret_cast<uint4*>(planes + n + i) = make_uint4(m[0], m[1], m[2], m[3]);
-  *reinterpret_cast<uint4*>(planes + 2 * n + i) = make_uint4(l[0], l[1], l[2], l[3]);
+  hi = make_uint2((h[0] >> 16) | h[1], (h[2] >> 16) | h[3]);
+  mid = make_uint2((m[0] >> 16) | m[1], (m[2] >> 16) | m[3]);
+  lo = make_uint2((l[0] >> 16) | l[1], (l[2] >> 16) | l[3]);
 }
 
-template <int NT>
-struct Fragments {
-  uint4 x[4];      // 4 token tiles
-  uint4 w[NT][3];  // NT expert tiles x (hi, mid, lo)
+// One step's global operands held by a thread: token rows (two 16-byte BF16
+// octets) and expert rows (three 16-byte FP32 quads).
+struct StepRegs {
+  uint4 x[2];
+  float4 w[3];
 };
 
-template <int NT>
-__device__ __forceinline__ void load_fragments(Fragments<NT>& f, const uint16_t* const (&xrow)[4],
-                                               const uint16_t* const (&wrow)[NT], int64_t plane, int64_t k) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) f.x[m] = *reinterpret_cast<const uint4*>(xrow[m] + k);
-#pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int p = 0; p < 3; ++p) f.w[j][p] = *reinterpret_cast<const uint4*>(wrow[j] + p * plane + k);
-}
-
-template <int NT>
-__device__ __forceinline__ void multiply(f32x4_t (&acc)[4][NT], const Fragments<NT>& f, const bool (&live)[NT]) {
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    if (!live[j]) continue;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, f.x[m]);
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-        acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8_t, f.w[j][p]), acc[m][j],
-                                                            0, 0, 0);
-    }
-  }
-}
-
-template <int NT>
-__global__ __launch_bounds__(256) void router_gemm_kernel(RouterGemmArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: tile tests branch on scalars
+__global__ __launch_bounds__(256, 2) void router_tile_kernel(RouterGemmArgs a, const float* __restrict__ weight) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // 2 stages
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t groups = a.token_groups * a.expert_groups;
   const int64_t items = groups * a.splits;
   const int64_t per_xcd = (items + 7) / 8;
   const int64_t item = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (item >= items) return;
   const int64_t split = item / groups;
-  const int64_t t0 = (item % groups / a.expert_groups) * kRouterTileTokens;
-  const int64_t tile0 = (item % a.expert_groups) * 4 * NT;
+  const int64_t t0 = (item % groups / a.expert_groups) * kTileTokens;
+  const int64_t e0 = (item % a.expert_groups) * kTileExperts;
   const int64_t k_begin = split * a.k_chunk;
   const int64_t k_end = k_begin + a.k_chunk < a.hidden ? k_begin + a.k_chunk : a.hidden;
-  const int64_t tiles = (a.experts + 15) / 16;
-  const int64_t plane = a.experts * a.hidden;
-  const int r = lane & 15;
-  const int q = lane >> 4;
-  // Rows past the last token or expert read the last one; their sums are dropped.
-  const uint16_t* xrow[4];
+  const int64_t H = a.hidden;
+
+  // ---- global load assignment (rows past the last token / expert re-read
+  // the last one; their sums are never stored)
+  // tokens: thread t loads octets 2 (t % 2) and 2 (t % 2) + 1 of row t / 2
+  const int xr = t >> 1, xq = 2 * (t & 1);
+  const uint16_t* xsrc = a.x + (t0 + xr < a.tokens ? t0 + xr : a.tokens - 1) * H + 8 * xq;
+  // experts: 96 rows x 8 quads of 4 FP32 = 768 quads, quad i = t + 256 j -> row i / 8, quad i % 8
+  const float* wsrc[3];
+  int wr[3], wq[3];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int64_t t = t0 + 16 * m + r;
-    xrow[m] = a.x + (t < a.tokens ? t : a.tokens - 1) * a.hidden + 8 * q;
+  for (int j = 0; j < 3; ++j) {
+    const int i = t + 256 * j;
+    wr[j] = i >> 3;
+    wq[j] = i & 7;
+    const int64_t e = e0 + wr[j];
+    wsrc[j] = weight + (e < a.experts ? e : a.experts - 1) * H + 4 * wq[j];
   }
-  const uint16_t* wrow[NT];
-  bool live[NT];
+  auto load = [&](StepRegs& r, int64_t k) {
+    r.x[0] = *reinterpret_cast<const uint4*>(xsrc + k);
+    r.x[1] = *reinterpret_cast<const uint4*>(xsrc + k + 8);
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int64_t tile = tile0 + wave + 4 * j;
-    const int64_t e = 16 * tile + r;
-    live[j] = tile < tiles;
-    wrow[j] = a.planes + (e < a.experts ? e : a.experts - 1) * a.hidden + 8 * q;
-  }
-  f32x4_t acc[4][NT];
+    for (int j = 0; j < 3; ++j) r.w[j] = *reinterpret_cast<const float4*>(wsrc[j] + k);
+  };
+  auto store = [&](const StepRegs& r, uint8_t* stage) {
+    *reinterpret_cast<uint4*>(stage + slot_offset(xr, xq)) = r.x[0];
+    *reinterpret_cast<uint4*>(stage + slot_offset(xr, xq + 1)) = r.x[1];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      uint2 hi, mid, lo;
+      split3(r.w[j], hi, mid, lo);
+      // quad wq holds K 4 wq .. 4 wq + 3: half (wq & 1) of octet wq / 2
+      const int off = slot_offset(wr[j], wq[j] >> 1) + 8 * (wq[j] & 1);
+      uint8_t* planes = stage + kXBytes;
+      *reinterpret_cast<uint2*>(planes + off) = hi;
+      *reinterpret_cast<uint2*>(planes + kPlaneBytes + off) = mid;
+      *reinterpret_cast<uint2*>(planes + 2 * kPlaneBytes + off) = lo;
+    }
+  };
+
+  // ---- MFMA operand reads: lane reads row 16 tile + lane % 16, octet lane / 16
+  const int wm = wave >> 1, wn = wave & 1;  // 64-token half, 48-expert half
+  const int r16 = lane & 15, q = lane >> 4;
+  f32x4_t acc[4][3];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int j = 0; j < NT; ++j) acc[m][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  // The chunk holds an even number of 32-deep steps (K chunks are multiples
-  // of 128).  Loads are never conditional (the last prefetch re-reads the
-  // first step and is not used), so the compiler's counted waits keep the
-  // next step's loads in flight across each step's MFMAs.
-  Fragments<NT> f0, f1;
-  load_fragments(f0, xrow, wrow, plane, k_begin);
-  for (int64_t k = k_begin; k < k_end; k += 64) {
-    load_fragments(f1, xrow, wrow, plane, k + 32);
-    multiply(acc, f0, live);
-    load_fragments(f0, xrow, wrow, plane, k + 64 < k_end ? k + 64 : k_begin);
-    multiply(acc, f1, live);
+    for (int n = 0; n < 3; ++n) acc[m][n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  StepRegs regs;
+  load(regs, k_begin);
+  int s = 0;
+  for (int64_t k = k_begin; k < k_end; k += kStep) {
+    uint8_t* stage = lds + s * kStageBytes;
+    store(regs, stage);
+    __syncthreads();  // the stage is complete; the other stage's readers are done
+    if (k + kStep < k_end) load(regs, k + kStep);  // next step's loads fly during the MFMAs
+    bf16x8_t xa[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      xa[m] = __builtin_bit_cast(bf16x8_t,
+                                 *reinterpret_cast<const uint4*>(stage + slot_offset(64 * wm + 16 * m + r16, q)));
+#pragma unroll
+    for (int n = 0; n < 3; ++n) {
+      const int row = 48 * wn + 16 * n + r16;
+      bf16x8_t wb[3];
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        wb[p] = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const uint4*>(stage + kXBytes + p * kPlaneBytes + slot_offset(row, q)));
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int p = 0; p < 3; ++p) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[m], wb[p], acc[m][n], 0, 0, 0);
+    }
+    s ^= 1;
   }
   // D layout of the 16x16 MFMA: lane holds rows 4 (lane / 16) + i, column lane % 16.
   float* out = a.partial + split * a.tokens * a.experts;
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int64_t e = 16 * (tile0 + wave + 4 * j) + r;
-    if (!live[j] || e >= a.experts) continue;
+  for (int n = 0; n < 3; ++n) {
+    const int64_t e = e0 + 48 * wn + 16 * n + r16;
+    if (e >= a.experts) continue;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t t = t0 + 16 * m + 4 * q + i;
-        if (t < a.tokens) out[t * a.experts + e] = acc[m][j][i];
+        const int64_t tok = t0 + 64 * wm + 16 * m + 4 * q + i;
+        if (tok < a.tokens) out[tok * a.experts + e] = acc[m][n][i];
       }
   }
 }
@@ -172,9 +185,8 @@ bool router_gemm_supported(int64_t hidden, int64_t experts, const void* x, const
 
 RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t experts) {
   RouterGemmShape s{};
-  s.token_groups = (tokens + kRouterTileTokens - 1) / kRouterTileTokens;
-  const int64_t tiles = (experts + 15) / 16;
-  s.expert_groups = (tiles + 4 * kRouterTilesPerWave - 1) / (4 * kRouterTilesPerWave);
+  s.token_groups = (tokens + kTileTokens - 1) / kTileTokens;
+  s.expert_groups = (experts + kTileExperts - 1) / kTileExperts;
   const int64_t groups = s.token_groups * s.expert_groups;
   const int64_t blocks = hidden / 128;
   // Two work items per CU where K allows, at most kMaxRouterSplits partial planes.
@@ -188,22 +200,15 @@ RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t expert
   return s;
 }
 
-size_t router_planes_bytes(int64_t hidden, int64_t experts) {
-  return static_cast<size_t>(3 * 2) * static_cast<size_t>(hidden * experts);
-}
-
 hipError_t launch_router_logits(const RouterGemmArgs& a, const float* weight, hipStream_t st) {
   if (a.tokens == 0) return hipSuccess;
   if (!router_gemm_supported(a.hidden, a.experts, a.x, weight) || a.k_chunk % 128 != 0 || a.splits < 1 ||
-      a.splits > kMaxRouterSplits || reinterpret_cast<uintptr_t>(a.planes) % 16 != 0)
+      a.splits > kMaxRouterSplits)
     return hipErrorInvalidValue;
-  const int64_t n = a.experts * a.hidden;
-  hipLaunchKernelGGL(router_planes_kernel, dim3(static_cast<unsigned>((n / 8 + 255) / 256)), dim3(256), 0, st, weight,
-                     a.planes, n);
   // item(b) = (b % 8) * ceil(items / 8) + b / 8 covers every item only over 8 * ceil(items / 8) workgroups
   const int64_t items = a.token_groups * a.expert_groups * a.splits;
-  hipLaunchKernelGGL(router_gemm_kernel<kRouterTilesPerWave>, dim3(static_cast<unsigned>((items + 7) / 8 * 8)),
-                     dim3(256), 0, st, a);
+  hipLaunchKernelGGL(router_tile_kernel, dim3(static_cast<unsigned>((items + 7) / 8 * 8)), dim3(256),
+                     2 * kStageBytes, st, a, weight);
   return hipGetLastError();
 }
 

@@ -161,13 +161,28 @@ def _restore_and_reduce_rows(route_out: torch.Tensor, scores: torch.Tensor, toke
     return out
 
 
+def _bucket_forward(expert, rows: torch.Tensor) -> torch.Tensor:
+    """One expert over a prefill bucket of token rows on the FP8 MFMA
+    contraction tree, whatever the bucket size: a one-row bucket runs as a
+    two-row problem (its row twice; rows never mix), so every route of a
+    prefill -- here and in the grouped plan -- takes the same per-row
+    arithmetic and the Direct-order grouped prefill equals this loop bit
+    for bit."""
+    n = rows.shape[0]
+    x = rows if n > 1 else rows.expand(2, rows.shape[-1])
+    h = swiglu(expert.gate_proj(x), expert.up_proj(x), expert.limit)
+    return expert.down_proj(h)[:n]
+
+
 class DirectFP8MoE(torch.nn.Module):
     """Bucketed top-k MoE over separate canonical expert tensors.
 
     Direct semantics (fp8.py:343-400): routing is a phase boundary with one
     host readback of the expert ids.  Decode (one row, k = 8) evaluates the
     selected experts and the ordered FP32 slot reduction; prefill visits
-    experts in ascending id and accumulates T(out * weight) in BF16.
+    experts in ascending id, runs each bucket on the FP8 MFMA contraction
+    tree (one-row buckets included) and accumulates T(out * weight) in BF16,
+    which SortedGroupedFP8MoE(reduction="direct") reproduces bit for bit.
     """
 
     def __init__(self, config, gate, shared_experts, device=None):
@@ -206,7 +221,7 @@ class DirectFP8MoE(torch.nn.Module):
                 rows_np, slots_np = np.nonzero(routes == expert_id)
                 rows = torch.as_tensor(rows_np, device=x.device)
                 flat_pos = torch.as_tensor(rows_np * k + slots_np, device=x.device)
-                route_out[flat_pos] = self._expert(int(expert_id))(flat_x[rows])
+                route_out[flat_pos] = _bucket_forward(self._expert(int(expert_id)), flat_x[rows])
             result = _restore_and_reduce_rows(route_out, flat_scores, tokens, k, shared, indices)
         # result = T(T(routed) + shared) (packed.py:922): the add is fused
         # into the reduction kernel.

@@ -25,6 +25,7 @@ from .packed import PackedFP8MoE, _c_shared
 from .router import Float32Gate
 
 GROUPED_TILE_ROWS = 32
+PLAN_MAX_EXPERTS = 1024  # the route plan's expert bound (kPlanMaxExperts)
 GROUPED_OUTPUT_COLS = 16
 GROUPED_K_TILE = 128
 
@@ -37,12 +38,14 @@ def _route_plan(expert_ids: torch.Tensor, scores: torch.Tensor | None, top_k: in
     sc = scores.reshape(-1).to(torch.float32).contiguous() if scores is not None else None
     capacity = (routes + tile_rows - 1) // tile_rows + expert_count
     i32 = dict(dtype=torch.int32, device=dev)
+    # sorted positions past the valid routes are never written: zeros keep
+    # them in range for gathers
     out = {
-        "order": torch.empty(routes, **i32),
+        "order": torch.zeros(routes, **i32),
         "inverse": torch.empty(routes, **i32),
-        "sorted_experts": torch.empty(routes, **i32),
-        "token_ids": torch.empty(routes, **i32),
-        "sorted_scores": torch.empty(routes, dtype=torch.float32, device=dev),
+        "sorted_experts": torch.zeros(routes, **i32),
+        "token_ids": torch.zeros(routes, **i32),
+        "sorted_scores": torch.zeros(routes, dtype=torch.float32, device=dev),
         "route_offsets": torch.empty(expert_count + 1, **i32),
         "tile_offsets": torch.empty(expert_count + 1, **i32),
         "tile_experts": torch.empty(capacity, **i32),
@@ -62,32 +65,37 @@ def _route_plan(expert_ids: torch.Tensor, scores: torch.Tensor | None, top_k: in
     return out
 
 
-def build_route_plan(x, topk_indices, topk_scores):
+def build_route_plan(x, topk_indices, topk_scores, *, expert_count: int | None = None):
     """Return the expert-sorted route plan (grouped_fp8.py:157-170):
     (sorted_x, sorted expert ids, sorted scores, inverse order).
 
-    The order is a stable sort of the flat (token-major) routes by expert.
-    ``sorted_x`` is materialised here only for API parity; the fused prefill
-    gathers token rows in the GEMM instead.
+    The order is a stable sort of the flat (token-major) routes by expert,
+    computed on the device with no host synchronisation.  Expert ids are
+    histogrammed over ``expert_count`` bins (default: the plan bound of
+    1024); a route outside that range is counted as invalid by the device
+    plan, gets inverse -1 and no sorted position (the sorted arrays end with
+    one zero entry per invalid route).  ``sorted_x`` is materialised
+    here only for API parity; the fused prefill gathers token rows in the
+    GEMM instead.
     """
     N.require_device(x, topk_indices, topk_scores)
     flat_x = x.reshape(-1, x.shape[-1])
     top_k = topk_indices.shape[-1]
-    experts = int(topk_indices.max().item()) + 1 if topk_indices.numel() else 1
-    plan = _route_plan(topk_indices, topk_scores, top_k, max(experts, 1))
-    if int(plan["status"][0].item()) != 0:
-        raise ValueError("expert ids must be non-negative")
+    experts = int(expert_count) if expert_count is not None else PLAN_MAX_EXPERTS
+    plan = _route_plan(topk_indices, topk_scores, top_k, experts)
     sorted_x = flat_x.index_select(0, plan["token_ids"].long())
     return sorted_x, plan["sorted_experts"], plan["sorted_scores"], plan["inverse"]
 
 
-def build_grouped_tile_plan(sorted_experts, expert_count: int):
+def build_grouped_tile_plan(sorted_experts, expert_count: int, *, check: bool = False):
     """Expert-aligned fixed-capacity tile descriptors (grouped_fp8.py:173-203):
     (tile_experts, tile_starts, tile_lengths, route_offsets, tile_offsets);
-    capacity ceil(R/32) + E, unused slots start at R with length 0."""
+    capacity ceil(R/32) + E, unused slots start at R with length 0.  No host
+    synchronisation unless ``check`` asks for a ValueError on ids outside
+    [0, expert_count)."""
     N.require_device(sorted_experts)
     plan = _route_plan(sorted_experts, None, 1, int(expert_count))
-    if int(plan["status"][0].item()) != 0:
+    if check and int(plan["status"][0].item()) != 0:
         raise ValueError(f"expert ids must lie in [0, {expert_count})")
     return (plan["tile_experts"], plan["tile_starts"], plan["tile_lengths"], plan["route_offsets"],
             plan["tile_offsets"])
@@ -193,9 +201,49 @@ class PrefillPlan:
                                                N.ptr(out), N.stream_handle(device)))
 
     def invalid_routes(self) -> int:
+        """Synchronous: routes of the last call whose expert id was out of range."""
         value = ctypes.c_uint32()
         N.check(self._lib.glm53_prefill_plan_status(self.handle, ctypes.byref(value)))
         return int(value.value)
+
+    # ---- read-only state of the reference plan (bindings.cpp:389-407)
+    def _counters(self) -> N.PlanCounters:
+        c = N.PlanCounters()
+        N.check(self._lib.glm53_prefill_plan_counters(self.handle, ctypes.byref(c)))
+        return c
+
+    @property
+    def execution_count(self) -> int:
+        return int(self._counters().execution_count)
+
+    @property
+    def dynamic_allocation_count(self) -> int:
+        return int(self._counters().dynamic_allocation_count)
+
+    @property
+    def host_synchronization_count(self) -> int:
+        return int(self._counters().host_synchronization_count)
+
+    @property
+    def static_input_validation_count(self) -> int:
+        return int(self._counters().static_input_validation_count)
+
+    @property
+    def dynamic_input_validation_count(self) -> int:
+        return int(self._counters().dynamic_input_validation_count)
+
+    @property
+    def scratch_bytes(self) -> int:
+        return int(self._counters().scratch_bytes)
+
+    @property
+    def buffer_identities(self) -> list[int]:
+        """Device addresses of the plan's scratch buffers: fixed at creation."""
+        cap = 32
+        buf = (ctypes.c_uint64 * cap)()
+        count = ctypes.c_int32()
+        N.check(self._lib.glm53_prefill_plan_identities(self.handle, buf, cap, ctypes.byref(count)))
+        return [int(buf[i]) for i in range(count.value)]
 
 
 class SortedGroupedFP8MoE(PackedFP8MoE):
@@ -215,6 +263,9 @@ class SortedGroupedFP8MoE(PackedFP8MoE):
         self.min_routes = int(min_routes)
         self.reduction = reduction
         self._prefill_plans: dict = {}
+        # Plans replaced by a larger one stay alive with the module: a HIP
+        # graph captured with an older plan keeps pointing at its arena.
+        self._retired_prefill_plans: list = []
 
     def _prefill_plan(self, device, tokens: int) -> PrefillPlan:
         key = (device.index, torch.cuda.current_stream(device).cuda_stream)
@@ -224,6 +275,8 @@ class SortedGroupedFP8MoE(PackedFP8MoE):
             if self.shared_experts is not None:
                 shared_inter = int(self.shared_experts.gate_proj.weight.shape[0])
             capacity = max(tokens, plan.max_tokens * 2 if plan is not None else 256)
+            if plan is not None:
+                self._retired_prefill_plans.append(plan)
             plan = PrefillPlan(self.bank.hidden_size, self.bank.intermediate_size, shared_inter,
                                self.bank.expert_count, self.config.num_experts_per_tok, capacity,
                                self.config.swiglu_limit)

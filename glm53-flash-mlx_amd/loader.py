@@ -1,16 +1,23 @@
-"""Layer-by-layer installation of the packed MoE modules.
+"""Installing the bank-backed MoE modules into a model, layer by layer.
 
-Counterpart of the reference's loader.py:167-254 (``install_packed_moe``,
-``install_packed_grouped_moe``, ``install_packed_decode_moe``): every
-``DirectFP8MoE`` layer is packed into a ``PackedFP8ExpertBank``, swapped for
-the packed (or grouped) module, and its separate expert modules are released
-before the next layer is packed, so two full copies never coexist.
+Counterpart of ``install_packed_moe`` / ``install_packed_grouped_moe`` /
+``install_packed_decode_moe`` (reference loader.py:167-254).  The model
+shape it walks is the reference's (``model.language_model.model.layers``,
+each layer with an ``mlp`` and a ``compile_ffn`` flag), and the report keys
+are the ones the reference's tests assert (tests/test_fp8_metal.py:274-284,
+319-329).
+
+Memory discipline: a layer's separate expert modules are released (and the
+caching allocator's blocks returned) before the next layer is packed, so
+at most one layer's experts are ever held twice -- at the BASELINE shapes a
+layer's bank is 5.4 GB, the whole model 229 GB of the 288 GB of HBM.
 """
 
 from __future__ import annotations
 
 import gc
 import logging
+from dataclasses import dataclass
 
 import torch
 
@@ -18,74 +25,110 @@ from .fp8 import DirectFP8MoE
 from .grouped_fp8 import SortedGroupedFP8MoE
 from .packed import PackedFP8ExpertBank, PackedFP8MoE
 
+_log = logging.getLogger(__name__)
 
-def _memory(device) -> int:
-    if device is not None and device.type == "cuda":
-        return int(torch.cuda.memory_allocated(device))
-    return 0
+
+@dataclass(frozen=True)
+class _Policy:
+    """Which module a layer should end up as."""
+
+    target: type
+    backend: str
+    grouped: bool
+
+    @classmethod
+    def of(cls, grouped: bool) -> "_Policy":
+        if grouped:
+            return cls(SortedGroupedFP8MoE, "packed-grouped", True)
+        return cls(PackedFP8MoE, "packed-decode", False)
+
+    def action(self, mlp) -> str:
+        """'keep' (already this policy), 'convert' (a Direct layer), 'skip'
+        (not a MoE layer this installer handles); raises for a packed layer
+        of the other policy, which cannot be re-packed in place."""
+        if isinstance(mlp, PackedFP8MoE):
+            installed_grouped = isinstance(mlp, SortedGroupedFP8MoE)
+            if installed_grouped == self.grouped:
+                return "keep"
+            raise ValueError(f"cannot convert existing {type(mlp).__name__} to {self.backend} in place")
+        return "convert" if isinstance(mlp, DirectFP8MoE) else "skip"
+
+
+class _DeviceMemory:
+    """Allocated-bytes readings of the device holding a layer's experts
+    (zeros for a host-resident layer)."""
+
+    def __init__(self, direct: DirectFP8MoE):
+        dev = direct.experts[0].gate_proj.weight.device if len(direct.experts) else torch.device("cpu")
+        self.device = dev if dev.type == "cuda" else None
+
+    def allocated(self) -> int:
+        return int(torch.cuda.memory_allocated(self.device)) if self.device is not None else 0
+
+    def peak(self) -> int:
+        return int(torch.cuda.max_memory_allocated(self.device)) if self.device is not None else 0
+
+    def release(self) -> None:
+        gc.collect()
+        if self.device is not None:
+            torch.cuda.synchronize(self.device)
+            torch.cuda.empty_cache()
+
+
+def _swap(index: int, layer, policy: _Policy) -> dict:
+    direct = layer.mlp
+    memory = _DeviceMemory(direct)
+    before = memory.allocated()
+    bank = PackedFP8ExpertBank.pack(direct.experts)
+    with_bank = memory.allocated()
+    layer.mlp = policy.target(bank, direct.config, direct.gate, direct.shared_experts)
+    layer.compile_ffn = False
+    expert_count = len(direct.experts)
+    del direct  # the only remaining reference to the separate experts
+    memory.release()
+    row = {
+        "layer": index,
+        "old_expert_count": expert_count,
+        "bank_bytes": bank.nbytes,
+        "active_before_bytes": before,
+        "active_materialized_bytes": with_bank,
+        "active_after_clear_bytes": memory.allocated(),
+        "peak_bytes": memory.peak(),
+        "old_expert_modules_detached": not hasattr(layer.mlp, "experts"),
+    }
+    _log.info("%s MoE layer=%d bank=%.3f GB active=%.3f GB", policy.backend, index, bank.nbytes / 1e9,
+              row["active_after_clear_bytes"] / 1e9)
+    return row
 
 
 def install_packed_moe(model, *, grouped: bool) -> dict:
-    """Pack routed experts layerwise and select the requested execution policy."""
-    logger = logging.getLogger(__name__)
-    module_type = SortedGroupedFP8MoE if grouped else PackedFP8MoE
-    backend = "packed-grouped" if grouped else "packed-decode"
-    converted = []
+    """Give every Direct MoE layer a packed bank and the requested execution
+    policy; layers already on that policy are left alone.  Returns the
+    conversion report, also stored on the model."""
+    policy = _Policy.of(grouped)
     layers = model.language_model.model.layers
-    for layer_id, layer in enumerate(layers):
-        direct = layer.mlp
-        if isinstance(direct, module_type) and (grouped or not isinstance(direct, SortedGroupedFP8MoE)):
-            continue
-        if isinstance(direct, PackedFP8MoE):
-            raise ValueError(f"cannot convert existing {type(direct).__name__} to {backend} in place")
-        if not isinstance(direct, DirectFP8MoE):
-            continue
-        device = direct.experts[0].gate_proj.weight.device if len(direct.experts) else None
-        active_before = _memory(device)
-        bank = PackedFP8ExpertBank.pack(direct.experts)
-        active_materialized = _memory(device)
-        layer.mlp = module_type(bank, direct.config, direct.gate, direct.shared_experts)
-        layer.compile_ffn = False
-        old_expert_count = len(direct.experts)
-        del direct
-        gc.collect()
-        if device is not None and device.type == "cuda":
-            torch.cuda.empty_cache()
-        active_after_clear = _memory(device)
-        converted.append({
-            "layer": layer_id,
-            "old_expert_count": old_expert_count,
-            "bank_bytes": bank.nbytes,
-            "active_before_bytes": active_before,
-            "active_materialized_bytes": active_materialized,
-            "active_after_clear_bytes": active_after_clear,
-            "old_expert_modules_detached": not hasattr(layer.mlp, "experts"),
-        })
-        logger.info("%s MoE layer=%d bank=%.3f GB", backend, layer_id, bank.nbytes / 1e9)
-
-    remaining_direct = [
-        layer_id for layer_id, layer in enumerate(layers)
-        if isinstance(layer.mlp, DirectFP8MoE) and not isinstance(layer.mlp, PackedFP8MoE)
-    ]
+    rows = [_swap(i, layer, policy) for i, layer in enumerate(layers) if policy.action(layer.mlp) == "convert"]
+    still_direct = [i for i, layer in enumerate(layers)
+                    if isinstance(layer.mlp, DirectFP8MoE) and not isinstance(layer.mlp, PackedFP8MoE)]
     report = {
-        "converted_layers": [row["layer"] for row in converted],
-        "converted_count": len(converted),
-        "remaining_direct_layers": remaining_direct,
-        "all_old_expert_modules_detached": all(row["old_expert_modules_detached"] for row in converted),
-        "layers": converted,
-        "backend": backend,
-        "grouped_enabled": grouped,
+        "backend": policy.backend,
+        "grouped_enabled": policy.grouped,
+        "converted_layers": [row["layer"] for row in rows],
+        "converted_count": len(rows),
+        "remaining_direct_layers": still_direct,
+        "all_old_expert_modules_detached": all(row["old_expert_modules_detached"] for row in rows),
+        "layers": rows,
     }
-    model._glm53_moe_backend = backend
-    setattr(model, f"_glm53_{backend.replace('-', '_')}_report", report)
+    model._glm53_moe_backend = policy.backend
+    setattr(model, "_glm53_" + policy.backend.replace("-", "_") + "_report", report)
     return report
 
 
 def install_packed_grouped_moe(model) -> dict:
-    """Install the grouped-prefill policy."""
+    """Grouped prefill above the route threshold, packed decode below it."""
     return install_packed_moe(model, grouped=True)
 
 
 def install_packed_decode_moe(model) -> dict:
-    """Install packed selected decode while retaining Direct prefill semantics."""
+    """Packed batch-1 decode; prefill keeps the Direct semantics."""
     return install_packed_moe(model, grouped=False)

@@ -19,6 +19,8 @@ import torch
 
 from . import _native as N
 from .fp8 import BLOCK_SIZE, DECODE_TOP_K, DirectFP8MoE, block_fp8_linear, swiglu
+from .ownership import (ResidentTensor, TensorLayout, borrowed_stable_tensor, owned_tensor, require_resident,
+                        resident_concatenate, storage_descriptor)
 from .router import Float32Gate
 
 
@@ -68,74 +70,86 @@ class _PackedExpertView:
         return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x), self.limit))
 
 
+def _bank_lease(value, name: str) -> ResidentTensor:
+    if isinstance(value, torch.Tensor):
+        raise TypeError(f"{name}: resident tensors require an explicit TensorLease; bare arrays have no storage "
+                        "lifetime contract (wrap with ownership.owned_tensor or borrowed_stable_tensor)")
+    return require_resident(value)
+
+
 class PackedFP8ExpertBank(torch.nn.Module):
     """Four contiguous canonical-FP8 buffers for one routed MoE layer.
 
     gate_up_weight u8 [E, 2I, H] (gate rows, then up rows), gate_up_scale_inv
     f32 [E, 2*ceil(I/128), ceil(H/128)], down_weight u8 [E, H, I],
-    down_scale_inv f32 [E, ceil(H/128), ceil(I/128)].  The bank owns its
-    bytes (ownership.py:42-61 of the reference).
+    down_scale_inv f32 [E, ceil(H/128), ceil(I/128)] (packed.py:747-787).
+    Each buffer arrives as a storage lease (ownership.py): owned, or
+    borrowed-stable with its owner kept referenced by the bank; an
+    ephemeral lease or a bare tensor is refused, because native plans and
+    captured graphs keep the bank's device pointers.
     """
 
     def __init__(self, gate_up_weight, gate_up_scale_inv, down_weight, down_scale_inv, *, intermediate_size: int):
         super().__init__()
-        tensors = (gate_up_weight, gate_up_scale_inv, down_weight, down_scale_inv)
-        if any(not isinstance(t, torch.Tensor) for t in tensors):
-            raise ValueError("bank buffers must be tensors")
-        if any(not t.is_contiguous() for t in tensors):
-            raise ValueError("bank buffers must be row-major contiguous")
-        if gate_up_weight.dtype != torch.uint8 or down_weight.dtype != torch.uint8:
-            raise ValueError("packed expert weights must remain uint8 E4M3")
-        if gate_up_scale_inv.dtype != torch.float32 or down_scale_inv.dtype != torch.float32:
-            raise ValueError("packed expert scales must remain float32")
+        names = ("gate_up_weight", "gate_up_scale_inv", "down_weight", "down_scale_inv")
+        resident = {n: _bank_lease(v, n) for n, v in zip(names, (gate_up_weight, gate_up_scale_inv, down_weight,
+                                                                    down_scale_inv))}
+        values = {n: r.value for n, r in resident.items()}
+        for n in ("gate_up_weight", "down_weight"):
+            if values[n].dtype != torch.uint8 or values[n].dim() != 3:
+                raise ValueError(f"{n} must be a 3-D uint8 E4M3 tensor, got {values[n].dtype} "
+                                 f"{tuple(values[n].shape)}")
+        for n in ("gate_up_scale_inv", "down_scale_inv"):
+            if values[n].dtype != torch.float32 or values[n].dim() != 3:
+                raise ValueError(f"{n} must be a 3-D float32 block table, got {values[n].dtype}")
         inter = int(intermediate_size)
-        experts, rows, hidden = gate_up_weight.shape
-        sr, sh = math.ceil(inter / BLOCK_SIZE), math.ceil(hidden / BLOCK_SIZE)
-        expected = {
-            "gate_up_weight": (gate_up_weight.shape, (experts, 2 * inter, hidden)),
-            "gate_up_scale_inv": (gate_up_scale_inv.shape, (experts, 2 * sr, sh)),
-            "down_weight": (down_weight.shape, (experts, hidden, inter)),
-            "down_scale_inv": (down_scale_inv.shape, (experts, sh, sr)),
-        }
-        for name, (actual, wanted) in expected.items():
-            if tuple(actual) != wanted:
-                raise ValueError(f"{name} shape {tuple(actual)} != {wanted}")
-        if len({t.device for t in tensors}) != 1:
+        n_exp, _, hidden = values["gate_up_weight"].shape
+        ri, rh = math.ceil(inter / BLOCK_SIZE), math.ceil(hidden / BLOCK_SIZE)
+        layout = {"gate_up_weight": (n_exp, 2 * inter, hidden), "gate_up_scale_inv": (n_exp, 2 * ri, rh),
+                  "down_weight": (n_exp, hidden, inter), "down_scale_inv": (n_exp, rh, ri)}
+        wrong = [f"{n} {tuple(values[n].shape)} (want {shape})" for n, shape in layout.items()
+                 if tuple(values[n].shape) != shape]
+        if wrong:
+            raise ValueError("bank layout mismatch: " + "; ".join(wrong))
+        if len({v.device for v in values.values()}) != 1:
             raise ValueError("bank buffers must live on one device")
-        self.register_buffer("gate_up_weight", gate_up_weight)
-        self.register_buffer("gate_up_scale_inv", gate_up_scale_inv)
-        self.register_buffer("down_weight", down_weight)
-        self.register_buffer("down_scale_inv", down_scale_inv)
+        for n, v in values.items():
+            self.register_buffer(n, v)
+        self.storage_contracts = {n: storage_descriptor(r) for n, r in resident.items()}
+        self._storage_owners = tuple(r.owner for r in resident.values() if r.owner is not None)
         self.intermediate_size = inter
-        self.intermediate_scale_rows = sr
+        self.intermediate_scale_rows = ri
 
     @classmethod
     def pack(cls, experts) -> "PackedFP8ExpertBank":
+        """Stack separate experts (each with gate_proj / up_proj / down_proj
+        block-FP8 linears) into one owned bank, expert-major, gate rows
+        before up rows (packed.py:782-850 layout).  Every projection must
+        keep uint8 E4M3 weights and float32 block scales of one shape per
+        projection kind."""
         experts = list(experts)
         if not experts:
-            raise ValueError("cannot pack an empty expert list")
-        hidden = experts[0].gate_proj.weight.shape[1]
-        inter = experts[0].gate_proj.weight.shape[0]
-        for expert in experts:
-            expected = (
-                (tuple(expert.gate_proj.weight.shape), (inter, hidden)),
-                (tuple(expert.up_proj.weight.shape), (inter, hidden)),
-                (tuple(expert.down_proj.weight.shape), (hidden, inter)),
-            )
-            if any(actual != wanted for actual, wanted in expected):
-                raise ValueError("expert projection shapes are not uniform")
-            for projection in (expert.gate_proj, expert.up_proj, expert.down_proj):
-                if projection.weight.dtype != torch.uint8:
-                    raise ValueError("packed expert weights must remain uint8 E4M3")
-                if projection.weight_scale_inv.dtype != torch.float32:
-                    raise ValueError("packed expert scales must remain float32")
-        gate_up_weight = torch.stack([torch.cat([e.gate_proj.weight, e.up_proj.weight], 0) for e in experts])
-        gate_up_scale = torch.stack([torch.cat([e.gate_proj.weight_scale_inv, e.up_proj.weight_scale_inv], 0)
-                                     for e in experts])
-        down_weight = torch.stack([e.down_proj.weight for e in experts])
-        down_scale = torch.stack([e.down_proj.weight_scale_inv for e in experts])
-        return cls(gate_up_weight.contiguous(), gate_up_scale.contiguous(), down_weight.contiguous(),
-                   down_scale.contiguous(), intermediate_size=inter)
+            raise ValueError("pack() needs at least one expert")
+        inter, hidden = (int(d) for d in experts[0].gate_proj.weight.shape)
+        kinds = (("gate_proj", (inter, hidden)), ("up_proj", (inter, hidden)), ("down_proj", (hidden, inter)))
+        for index, expert in enumerate(experts):
+            for kind, shape in kinds:
+                proj = getattr(expert, kind)
+                if tuple(proj.weight.shape) != shape:
+                    raise ValueError(f"expert {index} {kind} weight {tuple(proj.weight.shape)} breaks the uniform "
+                                     f"shape {shape}")
+                if proj.weight.dtype != torch.uint8 or proj.weight_scale_inv.dtype != torch.float32:
+                    raise ValueError(f"expert {index} {kind}: weights must stay uint8 E4M3 with float32 scales")
+
+        def stack(kinds_in_row_order, attr):
+            parts = [borrowed_stable_tensor(getattr(getattr(e, k), attr), owner=getattr(e, k))
+                     for e in experts for k in kinds_in_row_order]
+            flat = resident_concatenate(parts, axis=0).value
+            return owned_tensor(flat.view(len(experts), -1, flat.shape[-1]), layout=TensorLayout.ROW_MAJOR_CONTIGUOUS)
+
+        return cls(stack(("gate_proj", "up_proj"), "weight"), stack(("gate_proj", "up_proj"), "weight_scale_inv"),
+                   stack(("down_proj",), "weight"), stack(("down_proj",), "weight_scale_inv"),
+                   intermediate_size=inter)
 
     @property
     def expert_count(self) -> int:
@@ -206,7 +220,15 @@ class BankHandle:
 
 
 class DecodePlan:
-    """Fixed-scratch batch-1 decode plan (one per layer and stream)."""
+    """Fixed-scratch batch-1 decode plan, one per layer and stream: the
+    counterpart of ``NativePackedMoEDecodePlan`` (native_packed_moe_plan.h:
+    22-146, bindings.cpp:562-632) over ``glm53_decode_plan``.
+
+    Weights are borrowed (their pointers are passed per call, or recorded by
+    bind_weights); scratch is one device arena allocated at creation.  The
+    counters are the native plan's own (glm53_decode_plan_counters)."""
+
+    _IDENTITY_CAPACITY = 16
 
     def __init__(self, hidden: int, intermediate: int, shared_intermediate: int, experts: int, top_k: int,
                  limit: float):
@@ -217,7 +239,8 @@ class DecodePlan:
         self.handle = handle
         self.top_k = top_k
         self._dims = (int(hidden), int(intermediate), int(shared_intermediate), int(experts))
-        self._executions = 0
+        self._bound = None
+        self._output = None  # plan-owned output of execute_bound (overwritten by the next call)
 
     def __del__(self):
         handle = getattr(self, "handle", None)
@@ -225,11 +248,19 @@ class DecodePlan:
             self._lib.glm53_decode_plan_destroy(handle)
             self.handle = None
 
-    def _execute(self, status: int) -> None:
-        N.check(status)
-        self._executions += 1
+    # ---- read-only state of the reference plan (bindings.cpp:584-632)
+    def _counters(self) -> N.PlanCounters:
+        c = N.PlanCounters()
+        N.check(self._lib.glm53_decode_plan_counters(self.handle, ctypes.byref(c)))
+        return c
 
-    # Read-only counters of the reference plan (bindings.cpp:584-632).
+    def _identities(self, which: int) -> list[int]:
+        buf = (ctypes.c_uint64 * self._IDENTITY_CAPACITY)()
+        count = ctypes.c_int32()
+        N.check(self._lib.glm53_decode_plan_identities(self.handle, which, buf, self._IDENTITY_CAPACITY,
+                                                       ctypes.byref(count)))
+        return [int(buf[i]) for i in range(count.value)]
+
     @property
     def hidden_size(self) -> int:
         return self._dims[0]
@@ -248,56 +279,93 @@ class DecodePlan:
 
     @property
     def execution_count(self) -> int:
-        return self._executions
+        return int(self._counters().execution_count)
 
     @property
     def dynamic_allocation_count(self) -> int:
-        return 0  # all device scratch is one arena allocated at creation
+        return int(self._counters().dynamic_allocation_count)
 
     @property
     def host_synchronization_count(self) -> int:
-        return 0  # every call only enqueues on the caller's stream
+        return int(self._counters().host_synchronization_count)
 
     @property
-    def weights_bound(self) -> bool:
-        return getattr(self, "_bound", None) is not None
+    def static_input_validation_count(self) -> int:
+        return int(self._counters().static_input_validation_count)
 
     @property
-    def bound_weight_identities_stable(self) -> bool:
-        bound = getattr(self, "_bound", None)
-        return bound is not None and [(t.data_ptr(), t._version) for t in self._bound_tensors(*bound[:3])] == \
-            self._bound_identity
+    def dynamic_input_validation_count(self) -> int:
+        return int(self._counters().dynamic_input_validation_count)
 
     @property
     def scratch_bytes(self) -> int:
-        ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
-        N.check(self._lib.glm53_decode_plan_scratch(self.handle, 4, ctypes.byref(ptr), ctypes.byref(nbytes)))
-        return int(nbytes.value)
+        return int(self._counters().scratch_bytes)
 
+    @property
+    def weights_bound(self) -> bool:
+        return bool(self._counters().weights_bound)
+
+    @property
+    def buffer_identities(self) -> list[int]:
+        """Device addresses of the plan's scratch buffers: fixed at creation."""
+        return self._identities(0)
+
+    @property
+    def bound_weight_identities(self) -> list[int]:
+        """Device addresses the plan recorded at bind_weights (bank, shared
+        expert, router when bound)."""
+        return self._identities(1)
+
+    @property
+    def bound_weight_identities_stable(self) -> bool:
+        """True while every bound tensor still has the storage and contents
+        version it had at bind_weights (the reference's identity re-check,
+        native_packed_moe_plan.cpp:400-411)."""
+        if self._bound is None:
+            return False
+        tensors = self._bound_tensors(*self._bound[0][:3])  # what the weight objects hold now
+        if [(t.data_ptr(), t._version) for t in tensors] != self._bound[2]:
+            return False
+        return [t.data_ptr() for t in tensors] == self.bound_weight_identities
+
+    def debug_scratch(self, which: int) -> torch.Tensor:
+        """A device view of plan scratch after the last call (diagnostics):
+        0 SwiGLU rows bf16 [top_k + 1, I] (routed slots, then the shared
+        expert: debug_routed_hidden / debug_shared_hidden), 1 ids int32
+        [top_k], 2 scores f32 [top_k], 5 shared output bf16 [H]
+        (debug_shared_down).  The view aliases the plan's arena."""
+        ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
+        N.check(self._lib.glm53_decode_plan_scratch(self.handle, int(which), ctypes.byref(ptr), ctypes.byref(nbytes)))
+        dtype = {0: torch.bfloat16, 1: torch.int32, 2: torch.float32, 5: torch.bfloat16}[int(which)]
+        return _device_view(ptr.value, int(nbytes.value), dtype)
+
+    # ---- execution
     def routed(self, bank, shared, x, ids, scores, out, device):
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
-        self._execute(self._lib.glm53_decode_moe_routed(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                                        N.ptr(x), N.ptr(ids), N.ptr(scores), N.ptr(out),
-                                                        N.stream_handle(device)))
+        N.check(self._lib.glm53_decode_moe_routed(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                                  N.ptr(x), N.ptr(ids), N.ptr(scores), N.ptr(out),
+                                                  N.stream_handle(device)))
 
     def full(self, bank, shared, router, x, out, ids_out, scores_out, device):
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
         r = router.as_c_struct()
-        self._execute(self._lib.glm53_decode_moe(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                                 ctypes.byref(r), N.ptr(x), N.ptr(out), N.ptr(ids_out),
-                                                 N.ptr(scores_out), N.stream_handle(device)))
+        N.check(self._lib.glm53_decode_moe(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                           ctypes.byref(r), N.ptr(x), N.ptr(out), N.ptr(ids_out),
+                                           N.ptr(scores_out), N.stream_handle(device)))
 
     def step(self, bank, shared, router, x, residual, out, stages, device):
         """Decoder-step form: out = T(residual + T(moe(x))) (residual may be
-        None); stages is a mask of the router / gate-up / down launches."""
+        None); stages is a mask of the router / gate-up / down launches
+        (without the router bit, router may be None and the plan's last
+        selection is used)."""
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
         r = router.as_c_struct() if router is not None else None
-        self._execute(self._lib.glm53_decode_moe_ex(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                                    ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual),
-                                                    N.ptr(out), int(stages), N.stream_handle(device)))
+        N.check(self._lib.glm53_decode_moe_ex(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
+                                              ctypes.byref(r) if r else None, N.ptr(x), N.ptr(residual),
+                                              N.ptr(out), int(stages), N.stream_handle(device)))
 
     @staticmethod
     def _bound_tensors(bank, shared, router):
@@ -305,48 +373,97 @@ class DecodePlan:
         if shared is not None:
             for proj in (shared.gate_proj, shared.up_proj, shared.down_proj):
                 tensors += [proj.weight, proj.weight_scale_inv]
-        return tensors + [router.weight, router.e_score_correction_bias]
+        if router is not None:
+            tensors += [router.weight, router.e_score_correction_bias]
+        return tensors
 
-    def bind_weights(self, bank, shared, router) -> None:
-        """Bind one layer's weights once (bindings.cpp:576-583,
-        native_packed_moe_plan.cpp:231-258); binding again raises
-        RuntimeError.  The storage identity of every bound tensor is
-        recorded for execute_bound."""
+    def bind_weights(self, bank, shared, router=None) -> None:
+        """Record one layer's weights once (bindings.cpp:576-579,
+        native_packed_moe_plan.cpp:231-258): the bank, the shared expert
+        (None when absent) and optionally the router.  Binding again raises
+        RuntimeError.  The plan keeps the weight objects referenced and
+        records each tensor's storage identity for execute_bound."""
         b = bank.as_c_struct()
         s = shared.as_c_struct() if shared is not None else None
-        r = router.as_c_struct()
+        r = router.as_c_struct() if router is not None else None
         N.check(self._lib.glm53_decode_plan_bind(self.handle, ctypes.byref(b), ctypes.byref(s) if s else None,
-                                                 ctypes.byref(r)))
+                                                 ctypes.byref(r) if r else None))
         flags = [bank.code_flags()]
         if shared is not None:
             flags += [shared.gate_proj.code_flags(), shared.up_proj.code_flags(), shared.down_proj.code_flags()]
-        self._bound = (bank, shared, router, flags)  # keeps the scanned flag tensors the plan points at alive
-        self._bound_identity = [(t.data_ptr(), t._version) for t in self._bound_tensors(bank, shared, router)]
+        tensors = self._bound_tensors(bank, shared, router)
+        # the weight objects, the bound tensors and the scanned flag tensors the plan points at stay referenced
+        self._bound = ((bank, shared, router, flags), tensors, [(t.data_ptr(), t._version) for t in tensors])
 
-    def execute_bound(self, x, out, device) -> None:
-        """Decode x [H] with the bound weights into out [H]
-        (native_packed_moe_plan.cpp:260-280).  Raises RuntimeError when
-        nothing is bound, or when a bound tensor was replaced or modified in
-        place since binding (its 0x7F/0xFF code flags were scanned then)."""
-        bound = getattr(self, "_bound", None)
-        if bound is None:
+    def _check_bound(self):
+        if self._bound is None:
             raise RuntimeError("decode plan weights are not bound")
-        now = [(t.data_ptr(), t._version) for t in self._bound_tensors(*bound[:3])]
-        if now != self._bound_identity:
+        tensors = self._bound_tensors(*self._bound[0][:3])  # what the weight objects hold now
+        if [(t.data_ptr(), t._version) for t in tensors] != self._bound[2]:
             raise RuntimeError("decode plan bound weight identity changed")
-        self._execute(self._lib.glm53_decode_moe_bound(self.handle, N.ptr(x), N.ptr(out), N.stream_handle(device)))
+
+    def _out_for(self, x, out):
+        if out is not None:
+            return out
+        if self._output is None or self._output.device != x.device:
+            self._output = torch.empty(self.hidden_size, dtype=torch.bfloat16, device=x.device)
+        return self._output
+
+    def execute_bound(self, x, expert_ids, scores, *, out=None) -> torch.Tensor:
+        """Decode x [H] (bf16) with the bound weights and caller-chosen
+        routing: expert_ids [top_k] int, scores [top_k] f32
+        (native_packed_moe_plan.h:48, .cpp:260-280).  Returns `out`, or the
+        plan-owned output, which the next call overwrites.  Raises
+        RuntimeError when nothing is bound or a bound tensor was replaced or
+        modified in place since binding."""
+        self._check_bound()
+        N.require_device(x, expert_ids, scores)
+        flat = x.reshape(-1)
+        ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
+        sc = scores.reshape(-1).to(torch.float32).contiguous()
+        if flat.numel() != self.hidden_size or ids.numel() != self.top_k or sc.numel() != self.top_k:
+            raise ValueError(f"execute_bound expects x [{self.hidden_size}], {self.top_k} ids and scores")
+        dst = self._out_for(x, out)
+        N.check(self._lib.glm53_decode_moe_bound_routed(self.handle, N.ptr(flat.contiguous()), N.ptr(ids), N.ptr(sc),
+                                                        N.ptr(dst), N.stream_handle(x.device)))
+        return dst
+
+    def execute_bound_router(self, x, *, out=None) -> torch.Tensor:
+        """Decode x [H] with the bound weights and the bound router (no
+        reference counterpart: there the router stays in MLX)."""
+        self._check_bound()
+        if self._bound[0][2] is None:
+            raise RuntimeError("decode plan was bound without a router")
+        N.require_device(x)
+        flat = x.reshape(-1)
+        if flat.numel() != self.hidden_size:
+            raise ValueError(f"execute_bound_router expects x [{self.hidden_size}]")
+        dst = self._out_for(x, out)
+        N.check(self._lib.glm53_decode_moe_bound(self.handle, N.ptr(flat.contiguous()), N.ptr(dst),
+                                                 N.stream_handle(x.device)))
+        return dst
 
     def tune(self, gate_up_rows_per_wave: int = 8, down_rows_per_wg: int = 16) -> None:
         N.check(self._lib.glm53_decode_plan_tune(self.handle, int(gate_up_rows_per_wave), int(down_rows_per_wg)))
-
-    def set_mode(self, mode: int) -> None:
-        """N.DECODE_THREE_LAUNCH (default) or N.DECODE_SINGLE_LAUNCH."""
-        N.check(self._lib.glm53_decode_plan_set_mode(self.handle, int(mode)))
 
     def error_flag(self) -> int:
         value = ctypes.c_int32()
         N.check(self._lib.glm53_decode_plan_error_flag(self.handle, ctypes.byref(value)))
         return int(value.value)
+
+
+class _ArrayInterface:
+    def __init__(self, address: int, count: int, typestr: str):
+        self.__cuda_array_interface__ = {"shape": (count,), "typestr": typestr, "data": (address, False),
+                                         "version": 2}
+
+
+def _device_view(address: int, nbytes: int, dtype: torch.dtype) -> torch.Tensor:
+    """A tensor over device memory the library owns (no copy; the plan that
+    owns the memory must outlive the view)."""
+    carrier = {torch.bfloat16: ("<i2", 2), torch.int32: ("<i4", 4), torch.float32: ("<f4", 4)}[dtype]
+    view = torch.as_tensor(_ArrayInterface(address, nbytes // carrier[1], carrier[0]), device="cuda")
+    return view.view(dtype)
 
 
 def _c_shared(shared_experts):

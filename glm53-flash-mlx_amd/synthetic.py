@@ -16,6 +16,7 @@ import torch
 
 from . import _native as N
 from .fp8 import BLOCK_SIZE, ClampedMLP
+from .ownership import TensorLayout, owned_tensor
 from .packed import PackedFP8ExpertBank
 from .router import Float32Gate
 
@@ -85,7 +86,9 @@ def synth_bank(experts: int, hidden: int, intermediate: int, seed: int, layer: i
                                         2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "up"), std, stream))
     N.check(lib.glm53_synth_fp8_batched(N.ptr(dw), N.ptr(dws), hidden, intermediate, experts, hidden * intermediate,
                                         sh * sr, key(seed, layer, "down"), std, stream))
-    return PackedFP8ExpertBank(gu, gus, dw, dws, intermediate_size=intermediate)
+    rm = TensorLayout.ROW_MAJOR_CONTIGUOUS
+    return PackedFP8ExpertBank(owned_tensor(gu, layout=rm), owned_tensor(gus, layout=rm), owned_tensor(dw, layout=rm),
+                               owned_tensor(dws, layout=rm), intermediate_size=intermediate)
 
 
 def synth_shared(hidden: int, intermediate: int, limit: float, seed: int, layer: int = 0, device="cuda",

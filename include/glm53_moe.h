@@ -137,11 +137,10 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
  * Router -- replaces patch.py:131-142 `Float32Gate.__call__` (with the
  * selection half of mlx-vlm dsv32.group_expert_select, n_group = 1).
  * x bf16 [tokens, H] -> ids int32 [tokens, top_k], scores f32 [tokens, top_k].
- * The workspace holds, for several tokens, FP32 activations or BF16-MFMA
- * partial sums (tokens x max(H, 16 x experts) floats), FP32 logits
- * (tokens x experts) and the
- * weights' three BF16 parts (6 x experts x H bytes); for one token, the
- * logits.
+ * The workspace holds, for several tokens, the FP32 partial sums of the
+ * BF16-MFMA logits (up to 16 K chunks x tokens x experts floats) and FP32
+ * logits (tokens x experts, for shapes the MFMA form does not take); for one
+ * token, the logits.
  * ---------------------------------------------------------------------- */
 size_t glm53_router_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts);
 int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens, int32_t* ids,
@@ -179,10 +178,14 @@ int glm53_decode_moe(glm53_decode_plan* plan, const glm53_bank* bank,
  * residual / x), else out = moe(x).  stages selects launches:
  * GLM53_STAGE_ROUTER (router + top-k into the plan), GLM53_STAGE_GATE_UP
  * (routed + shared gate/up/SwiGLU), GLM53_STAGE_DOWN (down, ordered
- * reduction, shared add, residual).  Partial masks let a caller time each
- * launch; they need the fused path (16-byte aligned pointers, supported
- * widths).  A captured HIP graph of this call replays correctly: it records
- * no memset and resets its own counters. */
+ * reduction, shared add, residual).  router is required with
+ * GLM53_STAGE_ROUTER (and for shapes without the fused step kernels, which
+ * run only the whole mask); without that bit the routed launches use the
+ * selection the plan holds from an earlier router stage, and router may be
+ * NULL.  Partial masks let a caller time each launch; they need the fused
+ * path (16-byte aligned pointers, supported widths).  A captured HIP graph
+ * of this call replays correctly: it records no memset and resets its own
+ * counters. */
 #define GLM53_STAGE_ROUTER 1
 #define GLM53_STAGE_GATE_UP 2
 #define GLM53_STAGE_DOWN 4
@@ -192,10 +195,27 @@ int glm53_decode_moe_ex(glm53_decode_plan* plan, const glm53_bank* bank,
                         const void* x, const void* residual, void* out, int32_t stages,
                         void* stream);
 
-/* bind_weights / execute_bound (native_packed_moe_plan.cpp:231-280): bind
- * once, then run with only the activation.  Binding twice is GLM53_BAD_STATE. */
+/* bind_weights (native_packed_moe_plan.h:40-47, .cpp:231-258;
+ * bindings.cpp:576-581): record the layer's weights once -- the bank, the
+ * shared expert (may be NULL) and, beyond the reference, the router (may be
+ * NULL) -- so later calls pass only activations.  The plan keeps the
+ * pointers, not the bytes: the caller keeps the weights alive and unchanged
+ * while bound (glm53_decode_plan_identities(plan, 1, ...) returns the
+ * recorded pointers for an identity re-check).  Binding twice is
+ * GLM53_BAD_STATE. */
 int glm53_decode_plan_bind(glm53_decode_plan* plan, const glm53_bank* bank,
                            const glm53_shared_expert* shared, const glm53_router* router);
+
+/* execute_bound(x, expert_ids, scores) (native_packed_moe_plan.h:48,
+ * .cpp:260-280; bindings.cpp:580): the bound weights with caller-chosen
+ * routing, as glm53_decode_moe_routed.  GLM53_BAD_STATE when nothing is
+ * bound. */
+int glm53_decode_moe_bound_routed(glm53_decode_plan* plan, const void* x, const int32_t* expert_ids,
+                                  const float* scores, void* out, void* stream);
+
+/* The bound weights with the bound router, as glm53_decode_moe (no
+ * reference counterpart: the reference's router stays in MLX).
+ * GLM53_BAD_STATE when nothing, or no router, is bound. */
 int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, void* stream);
 
 /* Launch shape of the fused decode kernels: rows of one slot streamed per
@@ -204,35 +224,44 @@ int glm53_decode_moe_bound(glm53_decode_plan* plan, const void* x, void* out, vo
 int glm53_decode_plan_tune(glm53_decode_plan* plan, int32_t gate_up_rows_per_wave,
                            int32_t down_rows_per_wg);
 
-/* Execution form of the full decode calls (glm53_decode_moe, _routed,
- * _bound, and _ex with GLM53_STAGE_ALL):
- *   GLM53_DECODE_THREE_LAUNCH (default) -- router, gate/up, down as three
- *     launches;
- *   GLM53_DECODE_SINGLE_LAUNCH -- one persistent launch per layer (router,
- *     top-k, routed + shared gate/up/SwiGLU, down, reduction, residual) for
- *     the instantiated shapes (H, I) in {(4096, 1536), (4096, 2048),
- *     (2048, 1024), (1024, 512)} with experts <= 320 (other shapes and
- *     partial stage masks run the three-launch form).  Its workgroups on
- *     different XCDs exchange data through uncached memory, which makes it
- *     slower than the three-launch form on MI355X today.
- * Both forms apply the same BF16 roundings; the FP32 summation order inside
- * a row differs (router logits, down rows), so they agree to within the BF16
- * rounding of those sums. */
-#define GLM53_DECODE_THREE_LAUNCH 0
-#define GLM53_DECODE_SINGLE_LAUNCH 1
-int glm53_decode_plan_set_mode(glm53_decode_plan* plan, int32_t mode);
-
 /* Device scratch of the last call (read-only diagnostics): which = 0 hidden
- * bf16 [top_k + 1, I] (routed rows, then shared), 1 expert ids int32
- * [top_k], 2 scores f32 [top_k], 3 the launch control words (64 B), 4 the
- * plan's whole device arena (allocated once at creation; the reference's
- * scratch_bytes, native_packed_moe_plan.h:73). */
+ * bf16 [top_k + 1, I] (routed SwiGLU rows in slot order, then the shared
+ * expert's; the reference's debug_routed_hidden / debug_shared_hidden,
+ * native_packed_moe_plan.h:81-85), 1 expert ids int32 [top_k], 2 scores f32
+ * [top_k], 3 the router words u64 [E] of the router launch (sigmoid bits <<
+ * 32 | selection key), 4 the plan's whole device arena (allocated once at
+ * creation; scratch_bytes, native_packed_moe_plan.h:73), 5 the shared
+ * expert's output bf16 [H] (debug_shared_down). */
 int glm53_decode_plan_scratch(glm53_decode_plan* plan, int32_t which, void** ptr, size_t* bytes);
 
 /* Synchronous: copies the plan's device error flag to *host_value and
- * clears it: bit 0 = an expert id was out of range, bit 1 = a wait of the
- * single-launch kernel gave up (its outputs are then not valid). */
+ * clears it.  Bit 0 = an expert id was out of range (those slots produce
+ * NaN rows and the layer output is NaN); no other bit is used. */
 int glm53_decode_plan_error_flag(glm53_decode_plan* plan, int32_t* host_value);
+
+/* Read-only counters of a plan (native_packed_moe_plan.h:55-73;
+ * native_prefill_moe_plan.h; bindings.cpp:389-407, 584-632).  Host-side
+ * bookkeeping only: reading them touches no device. */
+typedef struct glm53_plan_counters {
+  uint64_t execution_count;                /* calls that enqueued a forward */
+  uint64_t dynamic_allocation_count;       /* device allocations after creation: always 0 */
+  uint64_t host_synchronization_count;     /* synchronous readbacks (error flag, status) */
+  uint64_t static_input_validation_count;  /* weight-set validations (each unbound call, each bind) */
+  uint64_t dynamic_input_validation_count; /* activation / routing validations (every call) */
+  uint64_t scratch_bytes;                  /* the plan's device arena */
+  int32_t weights_bound;                   /* decode: glm53_decode_plan_bind has run */
+  int32_t router_bound;                    /* decode: ... with a router */
+} glm53_plan_counters;
+int glm53_decode_plan_counters(const glm53_decode_plan* plan, glm53_plan_counters* out);
+
+/* Identities (device addresses) the plan works with, for the reference's
+ * buffer_identities / bound_weight_identities checks
+ * (native_packed_moe_plan.cpp:382-411): which = 0 its scratch buffers
+ * (fixed at creation), 1 the bound weight pointers (bank 4, shared 6 when
+ * bound, router 2 when bound; GLM53_BAD_STATE when nothing is bound).
+ * Writes min(count, capacity) values to out (host) and the count to *count. */
+int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, uint64_t* out,
+                                 int32_t capacity, int32_t* count);
 
 /* ------------------------------------------------------------------------
  * Prefill building blocks -- replace grouped_fp8.py:157-276.
@@ -342,6 +371,16 @@ int glm53_prefill_moe_hc(glm53_prefill_plan* plan, const glm53_bank* bank,
 
 /* Synchronous: invalid route count of the last glm53_prefill_moe. */
 int glm53_prefill_plan_status(glm53_prefill_plan* plan, uint32_t* invalid_routes);
+
+/* Read-only counters (NativePrefillMoEPlan, bindings.cpp:389-407): as the
+ * decode plan's (weights_bound / router_bound stay 0). */
+int glm53_prefill_plan_counters(const glm53_prefill_plan* plan, glm53_plan_counters* out);
+
+/* buffer_identities (bindings.cpp:406-407): device addresses of the plan's
+ * scratch buffers, fixed at creation; min(count, capacity) values to out
+ * (host), the count to *count. */
+int glm53_prefill_plan_identities(const glm53_prefill_plan* plan, uint64_t* out, int32_t capacity,
+                                  int32_t* count);
 
 /* Device scratch of the last call: which = 0 ids int32 [tokens, top_k],
  * 1 scores f32 [tokens, top_k], 2 sorted route order int32 [routes],

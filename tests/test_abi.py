@@ -74,8 +74,6 @@ def test_abi_version_and_constants(N, libso):
         header_define(n) for n in ("GLM53_OK", "GLM53_INVALID_ARGUMENT", "GLM53_BAD_STATE", "GLM53_DEVICE_ERROR"))
     assert (N.REDUCE_GROUPED, N.REDUCE_DIRECT) == (header_define("GLM53_REDUCE_GROUPED"),
                                                    header_define("GLM53_REDUCE_DIRECT"))
-    assert (N.DECODE_THREE_LAUNCH, N.DECODE_SINGLE_LAUNCH) == (header_define("GLM53_DECODE_THREE_LAUNCH"),
-                                                             header_define("GLM53_DECODE_SINGLE_LAUNCH"))
     assert (N.STAGE_ROUTER, N.STAGE_GATE_UP, N.STAGE_DOWN, N.STAGE_ALL) == tuple(
         header_define(n) for n in ("GLM53_STAGE_ROUTER", "GLM53_STAGE_GATE_UP", "GLM53_STAGE_DOWN",
                                    "GLM53_STAGE_ALL"))
@@ -85,7 +83,7 @@ def test_struct_layouts_match_header(N, tmp_path):
     """sizeof / offsetof of every public struct, compiled from the header with
     the host C compiler, equal the ctypes mirrors."""
     structs = {"glm53_bank": N.Bank, "glm53_linear": N.Linear, "glm53_shared_expert": N.SharedExpert,
-               "glm53_router": N.Router}
+               "glm53_router": N.Router, "glm53_plan_counters": N.PlanCounters}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, py in structs.items():
         lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
@@ -124,6 +122,13 @@ def test_invalid_arguments_fail_before_any_device_work(N, libso):
         (lambda: libso.glm53_router_topk(None, P(16), 4, P(16), P(16), P(16), 1 << 20, None), "router is null"),
         (lambda: libso.glm53_grouped_linear(P(16), 8, None, 8, 100, P(16), P(16), P(16), 1, P(16), P(16), None, 1,
                                             128, P(16), P(16), 1 << 20, None), "block-aligned"),
+        (lambda: libso.glm53_decode_moe_bound_routed(None, P(16), P(16), P(16), P(16), None), "plan is null"),
+        (lambda: libso.glm53_decode_moe_bound(None, P(16), P(16), None), "plan is null"),
+        (lambda: libso.glm53_decode_moe_ex(None, P(16), None, None, P(16), None, P(16), 4, None), "plan is null"),
+        (lambda: libso.glm53_decode_plan_counters(None, P(16)), "null pointer"),
+        (lambda: libso.glm53_prefill_plan_counters(None, P(16)), "null pointer"),
+        (lambda: libso.glm53_decode_plan_identities(None, 0, None, 0, P(16)), "null pointer"),
+        (lambda: libso.glm53_prefill_plan_identities(None, None, 0, P(16)), "null pointer"),
     ]
     for call, fragment in cases:
         assert call() == N.INVALID_ARGUMENT, fragment

@@ -203,7 +203,6 @@ def test_step_router_selection_matches_oracle(M, O, dev, case):
         b[100:120] = 3.0
     g = M.Float32Gate(w, b, top_k=8, routed_scaling_factor=2.5, norm_topk_prob=True)
     plan = packed.DecodePlan(1024, 512, 512, 288, 8, cfg.swiglu_limit)
-    plan.set_mode(N.DECODE_THREE_LAUNCH)
     hs = host_shared(shared)
     for step in range(3):
         x = syn.normal_bf16((cfg.hidden_size,), syn.key(43, case, step), device=dev)
@@ -269,8 +268,12 @@ def test_bank_handle_scans_once_and_decodes_like_the_bank(M, O, dev, small_layer
                                              N.ptr(y_handle), None, None, N.stream_handle(dev)))
             torch.cuda.synchronize()
             assert torch.equal(y_plain.view(torch.int16), y_handle.view(torch.int16))
-    marked = packed.PackedFP8ExpertBank(bank.gate_up_weight.clone(), bank.gate_up_scale_inv, bank.down_weight,
-                                        bank.down_scale_inv, intermediate_size=bank.intermediate_size)
+    own = submodule("ownership")
+    marked = packed.PackedFP8ExpertBank(own.owned_tensor(bank.gate_up_weight.clone()),
+                                        own.borrowed_stable_tensor(bank.gate_up_scale_inv, owner=bank),
+                                        own.borrowed_stable_tensor(bank.down_weight, owner=bank),
+                                        own.borrowed_stable_tensor(bank.down_scale_inv, owner=bank),
+                                        intermediate_size=bank.intermediate_size)
     marked.gate_up_weight[3, 5, 7] = 0x7F
     with packed.BankHandle(marked, dev) as handle:
         assert _device_int32(handle.ptr.contents.code_flags) != 0
@@ -414,10 +417,13 @@ def test_decode_rejects_bad_shapes(M, dev, small_layer):
 
 
 def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
-    """bind_weights / execute_bound (native_packed_moe_plan.cpp:231-280):
-    the bound run equals the unbound one bit for bit; executing unbound,
-    binding twice, or executing after a bound tensor was replaced or
-    modified in place raise RuntimeError."""
+    """bind_weights / execute_bound(x, expert_ids, scores)
+    (native_packed_moe_plan.h:40-48, .cpp:231-280; bindings.cpp:576-581):
+    the bound run with caller routing equals glm53_decode_moe_routed bit
+    for bit, the bound-router run equals glm53_decode_moe; the plan's
+    native counters and identities follow; executing unbound, binding
+    twice, or executing after a bound tensor was replaced or modified in
+    place raise RuntimeError."""
     import torch
 
     syn = submodule("synthetic")
@@ -430,27 +436,53 @@ def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
     ids = torch.empty(8, dtype=torch.int32, device=dev)
     sc = torch.empty(8, dtype=torch.float32, device=dev)
     plan.full(bank, shared, gate, x, want, ids, sc, dev)
-    out = torch.empty_like(want)
+    other_ids = torch.tensor([3, 9, 27, 1, 30, 0, 12, 5], dtype=torch.int32, device=dev)
+    other_sc = torch.linspace(0.3, 0.05, 8, device=dev)
+    want_routed = torch.empty_like(want)
+    plan.routed(bank, shared, x, other_ids, other_sc, want_routed, dev)
     with pytest.raises(RuntimeError, match="not bound"):
-        plan.execute_bound(x, out, dev)
-    assert not plan.weights_bound and plan.execution_count == 1
-    plan.bind_weights(bank, shared, gate)
-    plan.execute_bound(x, out, dev)
-    assert torch.equal(out, want)
-    assert plan.weights_bound and plan.bound_weight_identities_stable and plan.execution_count == 2
+        plan.execute_bound(x, other_ids, other_sc)
+    assert not plan.weights_bound and plan.execution_count == 2
+    assert plan.static_input_validation_count == 2 and plan.dynamic_input_validation_count == 2
+    scratch = plan.buffer_identities
+    assert len(scratch) == 8 and all(scratch)
+
+    plan.bind_weights(bank, shared)  # the reference binds the 10 bank + shared arrays, no router
+    got = plan.execute_bound(x, other_ids, other_sc)
+    assert torch.equal(got, want_routed)
+    assert got.data_ptr() == plan.execute_bound(x, ids, sc).data_ptr()  # plan-owned output, reused
+    assert torch.equal(got, want)
+    with pytest.raises(RuntimeError, match="without a router"):
+        plan.execute_bound_router(x)
+    assert plan.weights_bound and plan.bound_weight_identities_stable and plan.execution_count == 4
+    assert plan.static_input_validation_count == 3  # bind validates the weights; bound calls do not
+    assert plan.dynamic_input_validation_count == 4
+    assert plan.bound_weight_identities == [t.data_ptr() for t in packed.DecodePlan._bound_tensors(bank, shared,
+                                                                                                 None)]
+    assert plan.buffer_identities == scratch
     assert (plan.hidden_size, plan.intermediate_size, plan.shared_intermediate_size, plan.expert_count) == \
         (1024, 512, 512, 32)
     assert plan.dynamic_allocation_count == 0 and plan.host_synchronization_count == 0
     assert plan.scratch_bytes >= 2 * 9 * 512 + 4 * 8 + 4 * 8
+    hidden = plan.debug_scratch(0)
+    assert hidden.shape == (9 * 512,) and torch.isfinite(hidden.float()).all()
     with pytest.raises(RuntimeError, match="already bound"):
-        plan.bind_weights(bank, shared, gate)
+        plan.bind_weights(bank, shared)
+    assert plan.error_flag() == 0 and plan.host_synchronization_count == 1
+
+    routed_plan = packed.DecodePlan(1024, 512, 512, 32, 8, 10.0)
+    routed_plan.bind_weights(bank, shared, gate)
+    out = routed_plan.execute_bound_router(x)
+    assert torch.equal(out, want)
+    assert len(routed_plan.bound_weight_identities) == 12
+
     shared.down_proj.weight_scale_inv.mul_(1.0)  # in place: a new version of a bound tensor
     assert not plan.bound_weight_identities_stable
     with pytest.raises(RuntimeError, match="identity changed"):
-        plan.execute_bound(x, out, dev)
-    assert plan.execution_count == 2
+        plan.execute_bound(x, ids, sc)
+    assert plan.execution_count == 4
     plan2 = packed.DecodePlan(1024, 512, 512, 32, 8, 10.0)
     plan2.bind_weights(bank, shared, gate)
     bank.down_weight = bank.down_weight.clone()  # replaced storage
     with pytest.raises(RuntimeError, match="identity changed"):
-        plan2.execute_bound(x, out, dev)
+        plan2.execute_bound_router(x)

@@ -75,7 +75,7 @@ def _small_bank(M, dev, rng, experts, hidden, inter):
     dw = torch.from_numpy(random_codes(rng, shapes["dw"])).to(dev)
     gus = torch.from_numpy((rng.uniform(size=shapes["gus"]) * 0.002).astype(np.float32)).to(dev)
     dws = torch.from_numpy((rng.uniform(size=shapes["dws"]) * 0.002).astype(np.float32)).to(dev)
-    return M.PackedFP8ExpertBank(gu, gus, dw, dws, intermediate_size=inter)
+    return M.PackedFP8ExpertBank(*(M.owned_tensor(t) for t in (gu, gus, dw, dws)), intermediate_size=inter)
 
 
 def test_grouped_linear_matches_oracle(M, O, dev):
@@ -417,5 +417,112 @@ def test_prefill_graph_replays_match_eager(M, dev):
         torch.cuda.synchronize(dev)
         assert torch.equal(out, eager), i
         noise = syn.normal_bf16((1, 300, 512), syn.key(111, "noise", i), device=dev)
-        moe(noise)  # eager work on the same plan between replays
+        with torch.cuda.stream(stream):
+            moe(noise)  # eager work on the captured plan (same stream) between replays
         torch.cuda.synchronize(dev)
+    plan = moe._prefill_plans[(dev.index, stream.cuda_stream)]
+    assert plan.dynamic_allocation_count == 0 and plan.host_synchronization_count == 0
+    assert plan.execution_count == 5  # warm-up, capture, three eager calls (replays are not calls)
+    assert len(plan.buffer_identities) == 16
+
+
+def test_prefill_plan_growth_keeps_captured_plans_alive(M, dev):
+    """A call with more tokens than the stream's plan holds replaces the plan;
+    a graph captured with the old one still replays correctly (its arena is
+    retired with the module, not freed)."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=113, device=dev)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    x = syn.normal_bf16((1, 64, 512), syn.key(113, "x"), device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        eager = moe(x).clone()
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = moe(x)
+    with torch.cuda.stream(stream):
+        moe(syn.normal_bf16((1, 600, 512), syn.key(113, "long"), device=dev))  # grows the plan past 256 tokens
+    torch.cuda.synchronize(dev)
+    assert len(moe._retired_prefill_plans) == 1
+    torch.cuda.empty_cache()
+    filler = torch.full((64 << 20,), 7, dtype=torch.uint8, device=dev)  # reuse of freed memory would show
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, eager)
+    del filler
+
+
+def test_config5_zipf_2048_tokens_matches_oracle(M, O, dev, config5):
+    """BASELINE config 5 as bench.py runs it: 2,048 tokens on the config-2
+    layer (seed of the bench) with the Zipf(1.1) router bias -> 16,384
+    routes, heavy experts with over 5% of the routes (tens of 64-route
+    descriptors of one expert) and many experts under 10 routes; the
+    many-token router above 1,024 tokens.  Every token's selection is
+    checked against the oracle's router (near-tie rule); the MoE output of
+    every 4th token against the oracle's Direct MoE and, for the grouped
+    reduction, its grouped restatement (grouped_fp8.py:279-328), on the
+    device's selection and the touched experts."""
+    cfg, bank, shared, gate, x, tokens = config5
+    ids_d, sc_d = gate(x.reshape(tokens, -1))
+    ids, sc = ids_d.cpu().numpy(), sc_d.cpu().numpy()
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_routed_experts)
+    assert counts.max() / ids.size > 0.05, counts.max()
+    assert (counts < 10).sum() >= 100, (counts < 10).sum()
+    xb = to_bits(x).reshape(tokens, -1)
+    from test_gpu_decode import _router_check
+
+    _router_check(O, gate, xb, ids, sc)
+    sel = np.arange(0, tokens, 4)
+    sub, local = _touched(bank, ids[sel])
+    hs = host_shared(shared)
+    want_d = O.direct_moe(xb[sel], sub, local, sc[sel], cfg.swiglu_limit, hs)
+    want_g = O.grouped_moe(xb[sel], sub, local, sc[sel], cfg.swiglu_limit, hs)
+    for reduction, want in (("grouped", want_g), ("direct", want_d)):
+        y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared, reduction=reduction)(x)
+        got = to_bits(y).reshape(tokens, -1)[sel]
+        assert_parity(got, want_d, O)
+        stats = assert_parity(got, want, O, exact_fraction=0.75)
+        print(f"config 5 {reduction}: {stats}")
+
+
+@pytest.fixture(scope="module")
+def config5(dev):
+    from conftest import pkg as package
+
+    syn = submodule("synthetic")
+    pkg = package()
+    cfg = syn.layer_config()
+    bank, shared, gate0 = syn.synth_layer(cfg, 20260901, 0, dev)  # bench.py's seed, layer 0
+    gate = pkg.Float32Gate(gate0.weight, syn.zipf_bias(cfg.n_routed_experts).to(dev), top_k=8)
+    tokens = 2048
+    x = syn.normal_bf16((1, tokens, cfg.hidden_size), syn.key(20260901, "config5_2048_tokens_zipf"), device=dev)
+    return cfg, bank, shared, gate, x, tokens
+
+
+@pytest.mark.parametrize("tokens", [9, 256, 2048])
+def test_direct_order_prefill_equals_direct_bit_for_bit(M, dev, config2_layer, tokens):
+    """The Direct-order parity anchor (native_indexer_plan.metal:1997-2207;
+    README.md:819-823 of the reference): DirectFP8MoE's host bucket loop
+    (ascending experts, every bucket -- one-row buckets included -- on the
+    FP8 MFMA tree, BF16 accumulation) and the fused grouped plan with
+    reduction="direct" produce the same bytes, at 9 tokens (below the
+    grouped threshold: called directly), 256 and 2,048 tokens (the
+    many-token router)."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg, bank, shared, gate = config2_layer
+    x = syn.normal_bf16((1, tokens, cfg.hidden_size), syn.key(4242, "anchor", tokens), device=dev)
+    direct = M.PackedFP8MoE(bank, cfg, gate, shared)  # T > 1: the Direct semantics over the bank's experts
+    exact = M.SortedGroupedFP8MoE(bank, cfg, gate, shared, min_routes=0, reduction="direct")
+    want = direct(x)
+    got = exact(x)
+    torch.cuda.synchronize()
+    ids, _ = gate(x.reshape(tokens, -1))
+    singletons = int((torch.bincount(ids.reshape(-1).long(), minlength=cfg.n_routed_experts) == 1).sum())
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (tokens, singletons)
