@@ -101,6 +101,7 @@ _SIGNATURES = {
     "glm53_decode_plan_error_flag": (ctypes.c_int, [P, P]),
     "glm53_decode_plan_counters": (ctypes.c_int, [P, P]),
     "glm53_decode_plan_identities": (ctypes.c_int, [P, I32, P, I32, P]),
+    "glm53_decode_moe_static": (ctypes.c_int, [I64, I64, I64, I64, F32, P, P, P, P, P, P, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),
     "glm53_route_plan": (ctypes.c_int, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, I64, P, P, SZ, P]),
     "glm53_grouped_linear_workspace_bytes": (SZ, [I64, I64]),

@@ -1638,3 +1638,113 @@ int glm53_synth_bf16(void* out, int64_t n, uint64_t seed, float std, void* strea
 }
 
 }  // extern "C"
+// ------------------------------------------------- allocation-free decode --
+//
+// glm53_decode_moe_static is glm53_decode_moe_ex (whole stage mask) without a
+// plan, for callers that cannot allocate.  Its scratch is one file-scope
+// device array; each GPU holds its own copy at its own address, which host
+// code takes from hipGetSymbolAddress once per device -- the array's name in
+// host code is only a stand-in, never a device address.
+
+static __device__ __align__(256) uint8_t scratch[GLM53_DECODE_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kStaticMaxDevices = 64;
+std::mutex g_static_mutex;
+uint8_t* g_static_base[kStaticMaxDevices] = {};  // device address of `scratch` per GPU, set up once
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = 0u;
+}
+
+// Byte offsets inside the static scratch (each region 256-byte aligned).
+struct StaticLayout {
+  size_t count, err, ids, scores, words, shared_out, hidden, end;
+};
+StaticLayout static_layout(int64_t H, int64_t I, int64_t E, int64_t k) {
+  StaticLayout l{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += round_up(bytes);
+    return o;
+  };
+  l.count = take(4);  // launch-1 arrival counter: zero between calls (the last arriver resets it)
+  l.err = take(4);
+  l.ids = take(4 * k);
+  l.scores = take(4 * k);
+  l.words = take(8 * E);
+  l.shared_out = take(2 * H);
+  l.hidden = take(2 * (k + 1) * I);
+  l.end = off;
+  return l;
+}
+
+// The current GPU's copy of the scratch: its address is looked up, and the
+// whole array cleared with a fill kernel on `st`, on the first call made on
+// that GPU.
+int static_scratch_base(hipStream_t st, uint8_t** out) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  CHECK_ARG(dev >= 0 && dev < kStaticMaxDevices, "device %d is beyond the static scratch table (%d devices)", dev,
+            kStaticMaxDevices);
+  std::lock_guard<std::mutex> lock(g_static_mutex);
+  if (g_static_base[dev] == nullptr) {
+    void* ptr = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, static_cast<uint32_t*>(ptr),
+                       static_cast<int64_t>(GLM53_DECODE_STATIC_SCRATCH_BYTES / 4));
+    HIP_TRY(hipGetLastError(), "static scratch clear launch");
+    g_static_base[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_static_base[dev];
+  return GLM53_OK;
+}
+
+}  // namespace
+
+extern "C" int glm53_decode_moe_static(int64_t hidden, int64_t intermediate, int64_t experts, int64_t top_k,
+                                       float swiglu_limit, const glm53_bank* bank, const glm53_shared_expert* shared,
+                                       const glm53_router* router, const void* x, const void* residual, void* out,
+                                       void* stream) {
+  const int64_t H = hidden, I = intermediate, E = experts, k = top_k;
+  CHECK_ARG(H > 0 && I > 0 && E > 0 && k > 0 && k <= kMaxTopK && k <= E, "invalid dimensions");
+  CHECK_ARG(step_shape_supported(H, I),
+            "glm53_decode_moe_static runs the fused step shapes only; (hidden %lld, intermediate %lld) is not one",
+            (long long)H, (long long)I);
+  CHECK_ARG(E <= 320, "glm53_decode_moe_static supports at most 320 experts (got %lld)", (long long)E);
+  const StaticLayout lay = static_layout(H, I, E, k);
+  CHECK_ARG(lay.end <= GLM53_DECODE_STATIC_SCRATCH_BYTES,
+            "this shape needs %zu bytes of static scratch, more than its maximum of %d", lay.end,
+            GLM53_DECODE_STATIC_SCRATCH_BYTES);
+  int rc = check_bank(bank, H, I, E);
+  if (rc) return rc;
+  if (shared != nullptr) {
+    if ((rc = check_linear(shared->gate, I, H, "shared gate"))) return rc;
+    if ((rc = check_linear(shared->up, I, H, "shared up"))) return rc;
+    if ((rc = check_linear(shared->down, H, I, "shared down"))) return rc;
+  }
+  if ((rc = check_router(router, H, E, k))) return rc;
+  CHECK_ARG(x && out, "null pointer argument");
+  CHECK_ARG(decode_fast_ok(H, I, I, bank, shared, x) && aligned(router->weight, 16) && aligned(out, 4),
+            "glm53_decode_moe_static needs 16-byte aligned x and weights and a 4-byte aligned out");
+  hipStream_t st = S(stream);
+  uint8_t* base = nullptr;
+  if ((rc = static_scratch_base(st, &base))) return rc;
+  int slots = 0;  // launch width: depends on the shape, so found per call (a host-side query)
+  const StepContext c{H, I, I, E, k, swiglu_limit,
+                      reinterpret_cast<uint16_t*>(base + lay.hidden),
+                      reinterpret_cast<unsigned long long*>(base + lay.words),
+                      reinterpret_cast<uint32_t*>(base + lay.count),
+                      reinterpret_cast<int32_t*>(base + lay.ids),
+                      reinterpret_cast<float*>(base + lay.scores),
+                      reinterpret_cast<int*>(base + lay.err),
+                      reinterpret_cast<uint16_t*>(base + lay.shared_out),
+                      &slots};
+  rc = run_step(c, bank, shared, router, x, nullptr, nullptr, residual, out, GLM53_STAGE_ALL, 8, st);
+  if (rc < 0) return fail(GLM53_INVALID_ARGUMENT, "glm53_decode_moe_static: inputs outside the fused step kernels");
+  return rc;
+}

@@ -263,6 +263,31 @@ int glm53_decode_plan_counters(const glm53_decode_plan* plan, glm53_plan_counter
 int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, uint64_t* out,
                                  int32_t capacity, int32_t* count);
 
+/* Allocation-free decode step.  No counterpart in the reference: this entry
+ * point is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * is glm53_decode_moe_ex with the whole stage mask and a router, without a
+ * plan: out = T(residual + T(moe(x))) (residual may be NULL; out may alias x
+ * and residual), the same kernels and bits as the plan form.  It calls no
+ * hipMalloc / hipFree: its scratch is a static device array of
+ * GLM53_DECODE_STATIC_SCRATCH_BYTES, one copy per GPU held until the process
+ * ends; the first call on a GPU looks up that copy's address and clears it
+ * with a fill kernel on `stream` (make that first call outside graph capture
+ * to keep the clear out of the graph).  Limits: the fused step shapes
+ * (H, I) in {(4096, 1536), (4096, 2048), (7168, 2048), (6144, 2048),
+ * (2048, 1024), (2048, 1536), (1024, 512), (1024, 1024)}, at most 320
+ * experts, top_k <= 8, a shared expert (if any) of width I, 16-byte aligned
+ * x and weights; other inputs return GLM53_INVALID_ARGUMENT with a message.
+ * Every call on one GPU shares that GPU's scratch, so calls that overlap on
+ * one GPU (concurrent streams or threads) race; the scratch keeps the last
+ * call's contents, and out-of-range expert ids (NaN output) are not
+ * reported through a readable flag. */
+#define GLM53_DECODE_STATIC_SCRATCH_BYTES 131072
+int glm53_decode_moe_static(int64_t hidden, int64_t intermediate, int64_t experts, int64_t top_k,
+                            float swiglu_limit, const glm53_bank* bank,
+                            const glm53_shared_expert* shared, const glm53_router* router,
+                            const void* x, const void* residual, void* out, void* stream);
+
 /* ------------------------------------------------------------------------
  * Prefill building blocks -- replace grouped_fp8.py:157-276.
  * ---------------------------------------------------------------------- */
