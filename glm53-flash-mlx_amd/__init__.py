@@ -50,7 +50,7 @@ from .ownership import (
     require_resident,
     resident_concatenate,
 )
-from .packed import BankHandle, DecodePlan, PackedFP8ExpertBank, PackedFP8MoE
+from .packed import BankHandle, DecodePlan, PackedFP8ExpertBank, PackedFP8MoE, RoutedDiagnostic
 from .router import Float32Gate
 
 __all__ = [
@@ -62,7 +62,7 @@ __all__ = [
     "PackedFP8ExpertBank", "PackedFP8MoE", "DecodePlan", "Float32Gate", "build_route_plan",
     "build_grouped_tile_plan", "grouped_fp8_linear", "activate_gate_up", "restore_and_reduce",
     "SortedGroupedFP8MoE", "PrefillPlan", "install_packed_moe", "install_packed_grouped_moe",
-    "install_packed_decode_moe", "BankHandle", "ResidentTensor", "TensorLayout", "TensorLease", "TensorOwnership",
+    "install_packed_decode_moe", "BankHandle", "RoutedDiagnostic", "ResidentTensor", "TensorLayout", "TensorLease", "TensorOwnership",
     "TensorOwnershipError", "borrowed_ephemeral_tensor", "borrowed_stable_tensor", "materialize_owned",
     "owned_tensor", "require_resident", "resident_concatenate",
 ]

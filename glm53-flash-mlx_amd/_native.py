@@ -102,6 +102,11 @@ _SIGNATURES = {
     "glm53_decode_plan_counters": (ctypes.c_int, [P, P]),
     "glm53_decode_plan_identities": (ctypes.c_int, [P, I32, P, I32, P]),
     "glm53_decode_moe_static": (ctypes.c_int, [I64, I64, I64, I64, F32, P, P, P, P, P, P, P]),
+    "glm53_routed_diagnostic_create": (ctypes.c_int, [I64, I64, I64, I64, F32, P]),
+    "glm53_routed_diagnostic_destroy": (None, [P]),
+    "glm53_routed_diagnostic_execute": (ctypes.c_int, [P, P, P, P, P, P]),
+    "glm53_routed_diagnostic_stage": (ctypes.c_int, [P, I32, P, P]),
+    "glm53_routed_diagnostic_counters": (ctypes.c_int, [P, P, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),
     "glm53_route_plan": (ctypes.c_int, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, I64, P, P, SZ, P]),
     "glm53_grouped_linear_workspace_bytes": (SZ, [I64, I64]),

@@ -971,6 +971,99 @@ int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, u
 }
 
 
+// ------------------------------------------------- routed diagnostic ------
+
+struct glm53_routed_diagnostic {
+  int64_t H, I, E, k;
+  float limit;
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+  uint16_t* stage[5] = {};  // gate, up, sigmoid, silu, hidden: bf16 [k, I] each
+  int* err = nullptr;
+  uint64_t executions = 0;
+};
+
+int glm53_routed_diagnostic_create(int64_t hidden, int64_t intermediate, int64_t experts, int64_t top_k,
+                                   float swiglu_limit, glm53_routed_diagnostic** out) {
+  CHECK_ARG(out != nullptr, "out is null");
+  *out = nullptr;
+  CHECK_ARG(hidden > 0 && hidden <= 16384 && intermediate > 0 && intermediate <= 16384,
+            "invalid dimensions (the diagnostic runs the any-shape GEMV: widths up to 16384)");
+  CHECK_ARG(experts > 0 && experts <= kMaxExperts && top_k > 0 && top_k <= kMaxTopK && top_k <= experts,
+            "invalid expert count or top_k");
+  auto* d = new glm53_routed_diagnostic();
+  d->H = hidden;
+  d->I = intermediate;
+  d->E = experts;
+  d->k = top_k;
+  d->limit = swiglu_limit;
+  const size_t plane = round_up(2 * static_cast<size_t>(top_k * intermediate));
+  d->arena_bytes = 5 * plane + 256;
+  hipError_t e = hipMalloc(&d->arena, d->arena_bytes);
+  if (e == hipSuccess) e = hipMemset(d->arena, 0, d->arena_bytes);
+  if (e != hipSuccess) {
+    if (d->arena) (void)hipFree(d->arena);
+    delete d;
+    return hip_fail(e, "routed diagnostic allocation");
+  }
+  uint8_t* b = static_cast<uint8_t*>(d->arena);
+  for (int i = 0; i < 5; ++i) d->stage[i] = reinterpret_cast<uint16_t*>(b + i * plane);
+  d->err = reinterpret_cast<int*>(b + 5 * plane);
+  *out = d;
+  return GLM53_OK;
+}
+
+void glm53_routed_diagnostic_destroy(glm53_routed_diagnostic* diag) {
+  if (diag == nullptr) return;
+  if (diag->arena) (void)hipFree(diag->arena);
+  delete diag;
+}
+
+int glm53_routed_diagnostic_execute(glm53_routed_diagnostic* d, const void* x, const int32_t* expert_ids,
+                                    const uint8_t* gate_up_weight, const float* gate_up_scale_inv, void* stream) {
+  CHECK_ARG(d != nullptr, "diagnostic is null");
+  CHECK_ARG(x && expert_ids && gate_up_weight && gate_up_scale_inv, "null pointer argument");
+  hipStream_t st = S(stream);
+  const int64_t H = d->H, I = d->I, k = d->k;
+  const int64_t SR = cdiv(I, 128), SC = cdiv(H, 128);
+  int rc;
+  if ((rc = generic_linear(x, 0, 1, k, gate_up_weight, 2 * I * H, 0, gate_up_scale_inv, 2 * SR * SC, 0, SC,
+                           expert_ids, d->E, I, H, d->stage[0], I, d->err, st)))
+    return rc;
+  if ((rc = generic_linear(x, 0, 1, k, gate_up_weight, 2 * I * H, I, gate_up_scale_inv, 2 * SR * SC, SR, SC,
+                           expert_ids, d->E, I, H, d->stage[1], I, d->err, st)))
+    return rc;
+  SwigluArgs a{};
+  a.gate = d->stage[0];
+  a.up = d->stage[1];
+  a.gate_row_stride = I;
+  a.up_row_stride = I;
+  a.rows = k;
+  a.cols = I;
+  a.limit = d->limit;
+  a.out = d->stage[4];
+  a.out_row_stride = I;
+  HIP_TRY(launch_swiglu_stages(a, d->stage[2], d->stage[3], st), "swiglu stages launch");
+  ++d->executions;
+  return GLM53_OK;
+}
+
+int glm53_routed_diagnostic_stage(glm53_routed_diagnostic* d, int32_t which, void** ptr, size_t* bytes) {
+  CHECK_ARG(d && ptr && bytes, "null pointer argument");
+  CHECK_ARG(which >= 0 && which < 5, "unknown stage %d", which);
+  *ptr = d->stage[which];
+  *bytes = 2 * static_cast<size_t>(d->k * d->I);
+  return GLM53_OK;
+}
+
+int glm53_routed_diagnostic_counters(const glm53_routed_diagnostic* d, uint64_t* execution_count,
+                                     uint64_t* scratch_bytes) {
+  CHECK_ARG(d && execution_count && scratch_bytes, "null pointer argument");
+  *execution_count = d->executions;
+  *scratch_bytes = d->arena_bytes;
+  return GLM53_OK;
+}
+
 // ---------------------------------------------------- prefill pieces ------
 
 size_t glm53_route_plan_workspace_bytes(int64_t routes, int64_t experts) {

@@ -501,6 +501,28 @@ __global__ void swiglu_kernel(SwigluArgs a) {
   a.out[r * a.out_row_stride + c] = swiglu_mlx(g, u, a.limit);
 }
 
+// swiglu_mlx with every rounding point kept (the routed-stage diagnostic):
+// gate/up rows of `cols` at row strides gate_row_stride / up_row_stride ->
+// sigma = T(sigmoid(g')), silu = T(g' * sigma), hidden = T(silu * u') with
+// g' = T(min(g, L)), u' = T(clip(u, -L, L)) (packed.py:146-163), [rows, cols].
+__global__ void swiglu_stages_kernel(SwigluArgs a, uint16_t* sigma_out, uint16_t* silu_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= a.rows * a.cols) return;
+  const int64_t r = i / a.cols, c = i % a.cols;
+  const float g = bf16_to_f32(a.gate[r * a.gate_row_stride + c]);
+  const float u = bf16_to_f32(a.up[r * a.up_row_stride + c]);
+  float gv = (g < a.limit) ? g : a.limit;
+  if (isnan(g)) gv = g;
+  float uv = fminf(fmaxf(u, -a.limit), a.limit);
+  if (isnan(u)) uv = u;
+  const uint16_t ga = f32_to_bf16(gv);
+  const float sigma = sigmoid_mlx_bf16(ga);
+  const float silu = bf16_round(bf16_to_f32(ga) * sigma);
+  sigma_out[r * a.out_row_stride + c] = f32_to_bf16(sigma);
+  silu_out[r * a.out_row_stride + c] = f32_to_bf16(silu);
+  a.out[r * a.out_row_stride + c] = f32_to_bf16(silu * bf16_round(uv));
+}
+
 // packed.py:168-179: out[h] = T(sum_s float(down[s,h]) * score[s]), FP32
 // products summed in slot order; optional BF16 add of `addend`.
 __global__ void weighted_reduction_kernel(WeightedReductionArgs a) {
@@ -638,6 +660,14 @@ hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st) {
   dim3 grid(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(a.G));
   size_t lds = sizeof(float) * static_cast<size_t>(a.tile_rows) * static_cast<size_t>(a.K);
   hipLaunchKernelGGL(linear_generic_kernel, grid, dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_stages(const SwigluArgs& a, uint16_t* sigma, uint16_t* silu, hipStream_t st) {
+  const int64_t n = a.rows * a.cols;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_stages_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, a, sigma,
+                     silu);
   return hipGetLastError();
 }
 

@@ -207,6 +207,7 @@ RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t expert
 hipError_t launch_router_logits(const RouterGemmArgs& a, const float* weight, hipStream_t st);
 hipError_t launch_linear_generic(const GenericLinearArgs& a, hipStream_t st);
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st);
+hipError_t launch_swiglu_stages(const SwigluArgs& a, uint16_t* sigma, uint16_t* silu, hipStream_t st);
 hipError_t launch_weighted_reduction(const WeightedReductionArgs& a, hipStream_t st);
 hipError_t launch_sigmoid_bf16(const uint16_t* g, uint16_t* out, int64_t n, hipStream_t st);
 hipError_t launch_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n, hipStream_t st);

@@ -452,6 +452,76 @@ class DecodePlan:
         return int(value.value)
 
 
+class RoutedDiagnostic:
+    """One decode's routed gate/up/SwiGLU boundary with every stage kept
+    (native_packed_moe_plan.h:148-183 ``NativePackedMoERoutedDiagnostic``,
+    bindings.cpp:634-649): after ``execute(x, expert_ids, gate_up_weight,
+    gate_up_scale_inv)`` the properties ``gate``, ``up``, ``sigmoid``,
+    ``silu`` and ``hidden`` are bf16 [top_k, I] device views of object-owned
+    buffers (fixed addresses; the next execute overwrites them).  Separate
+    from DecodePlan, so instrumenting never changes the decode's launches."""
+
+    _STAGES = ("gate", "up", "sigmoid", "silu", "hidden")
+
+    def __init__(self, expert_count: int = 288, *, hidden_size: int = 4096, intermediate_size: int = 2048,
+                 top_k: int = DECODE_TOP_K, swiglu_limit: float = 10.0):
+        self._lib = N.lib()
+        handle = ctypes.c_void_p()
+        N.check(self._lib.glm53_routed_diagnostic_create(hidden_size, intermediate_size, expert_count, top_k,
+                                                         float(swiglu_limit), ctypes.byref(handle)))
+        self.handle = handle
+        self.hidden_size, self.intermediate_size, self.top_k = int(hidden_size), int(intermediate_size), int(top_k)
+
+    def __del__(self):
+        handle = getattr(self, "handle", None)
+        if handle is not None and handle.value:
+            self._lib.glm53_routed_diagnostic_destroy(handle)
+            self.handle = None
+
+    def execute(self, x, expert_ids, gate_up_weight, gate_up_scale_inv) -> torch.Tensor:
+        N.require_device(x, expert_ids, gate_up_weight, gate_up_scale_inv)
+        flat = x.reshape(-1).contiguous()
+        ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
+        if flat.numel() != self.hidden_size or ids.numel() != self.top_k:
+            raise ValueError(f"expected x [{self.hidden_size}] and {self.top_k} expert ids")
+        if gate_up_weight.dtype != torch.uint8 or gate_up_weight.shape[1:] != (2 * self.intermediate_size,
+                                                                                self.hidden_size):
+            raise ValueError("gate_up_weight must be uint8 [E, 2I, H]")
+        N.check(self._lib.glm53_routed_diagnostic_execute(self.handle, N.ptr(flat), N.ptr(ids),
+                                                          N.ptr(gate_up_weight.contiguous()),
+                                                          N.ptr(gate_up_scale_inv.contiguous()),
+                                                          N.stream_handle(x.device)))
+        return self.hidden
+
+    def _stage(self, which: int) -> torch.Tensor:
+        ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
+        N.check(self._lib.glm53_routed_diagnostic_stage(self.handle, which, ctypes.byref(ptr), ctypes.byref(nbytes)))
+        return _device_view(ptr.value, int(nbytes.value), torch.bfloat16).view(self.top_k, self.intermediate_size)
+
+    gate = property(lambda self: self._stage(0))
+    up = property(lambda self: self._stage(1))
+    sigmoid = property(lambda self: self._stage(2))
+    silu = property(lambda self: self._stage(3))
+    hidden = property(lambda self: self._stage(4))
+
+    def _counters(self):
+        ex, sb = ctypes.c_uint64(), ctypes.c_uint64()
+        N.check(self._lib.glm53_routed_diagnostic_counters(self.handle, ctypes.byref(ex), ctypes.byref(sb)))
+        return int(ex.value), int(sb.value)
+
+    @property
+    def execution_count(self) -> int:
+        return self._counters()[0]
+
+    @property
+    def scratch_bytes(self) -> int:
+        return self._counters()[1]
+
+    @property
+    def buffer_identities(self) -> list[int]:
+        return [self._stage(i).data_ptr() for i in range(len(self._STAGES))]
+
+
 class _ArrayInterface:
     def __init__(self, address: int, count: int, typestr: str):
         self.__cuda_array_interface__ = {"shape": (count,), "typestr": typestr, "data": (address, False),

@@ -263,6 +263,29 @@ int glm53_decode_plan_counters(const glm53_decode_plan* plan, glm53_plan_counter
 int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, uint64_t* out,
                                  int32_t capacity, int32_t* count);
 
+/* Routed-stage diagnostic -- replaces native_packed_moe_plan.h:148-183
+ * `NativePackedMoERoutedDiagnostic` (bindings.cpp:634-649): one decode's
+ * routed gate/up/SwiGLU boundary with every stage kept, for localising
+ * numerics.  execute(x bf16 [H], expert_ids int32 [top_k], the bank's
+ * gate_up_weight u8 [E, 2I, H] and gate_up_scale_inv) fills five bf16
+ * [top_k, I] stages owned by the object (fixed addresses from creation):
+ * 0 gate = T(x . W_gate[e]^T), 1 up = T(x . W_up[e]^T), 2 sigmoid =
+ * T(sigmoid(g')), 3 silu = T(g' * sigmoid), 4 hidden = T(silu * u') with
+ * g' = T(min(gate, L)), u' = T(clip(up, -L, L)) (packed.py:146-163).  It is
+ * separate from the decode plan and runs the any-shape GEMV, so its gate /
+ * up may differ from the fused step's by the FP32 summation order; the
+ * stages after gate / up are exact functions of them. */
+typedef struct glm53_routed_diagnostic glm53_routed_diagnostic;
+int glm53_routed_diagnostic_create(int64_t hidden, int64_t intermediate, int64_t experts, int64_t top_k,
+                                   float swiglu_limit, glm53_routed_diagnostic** out);
+void glm53_routed_diagnostic_destroy(glm53_routed_diagnostic* diag);
+int glm53_routed_diagnostic_execute(glm53_routed_diagnostic* diag, const void* x, const int32_t* expert_ids,
+                                    const uint8_t* gate_up_weight, const float* gate_up_scale_inv,
+                                    void* stream);
+int glm53_routed_diagnostic_stage(glm53_routed_diagnostic* diag, int32_t which, void** ptr, size_t* bytes);
+int glm53_routed_diagnostic_counters(const glm53_routed_diagnostic* diag, uint64_t* execution_count,
+                                     uint64_t* scratch_bytes);
+
 /* Allocation-free decode step.  No counterpart in the reference: this entry
  * point is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It

@@ -486,3 +486,51 @@ def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
     bank.down_weight = bank.down_weight.clone()  # replaced storage
     with pytest.raises(RuntimeError, match="identity changed"):
         plan2.execute_bound_router(x)
+
+
+def test_routed_diagnostic_stages_match_oracle(M, O, dev, small_layer):
+    """NativePackedMoERoutedDiagnostic (native_packed_moe_plan.h:148-183):
+    gate / up against the oracle's block-FP8 linear per selected expert (the
+    BASELINE gates); sigmoid, silu and hidden are exact functions of the
+    device's gate / up in the MLX BF16 sequence (packed.py:146-163), checked
+    bit for bit against the oracle's sigmoid and BF16 roundings; the hidden
+    rows agree with the decode plan's within the gates."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg, bank, shared, gate = small_layer
+    I, H = cfg.moe_intermediate_size, cfg.hidden_size
+    diag = M.RoutedDiagnostic(cfg.n_routed_experts, hidden_size=H, intermediate_size=I, swiglu_limit=cfg.swiglu_limit)
+    x = syn.normal_bf16((H,), syn.key(7, "diag"), device=dev)
+    ids = torch.tensor([5, 0, 31, 7, 12, 3, 30, 19], dtype=torch.int32, device=dev)
+    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv)
+    torch.cuda.synchronize()
+    assert diag.execution_count == 1 and diag.scratch_bytes >= 5 * 2 * 8 * I
+    xb = to_bits(x).reshape(1, -1)
+    hb = host_bank(bank)
+    g, u = to_bits(diag.gate), to_bits(diag.up)
+    for s, e in enumerate(ids.tolist()):
+        mats = O.expert_matrices(hb, e)
+        assert_parity(g[s], O.fp8_linear(xb, *mats.gate)[0], O, exact_fraction=0.95)
+        assert_parity(u[s], O.fp8_linear(xb, *mats.up)[0], O, exact_fraction=0.95)
+    L = cfg.swiglu_limit
+    gf, uf = O.bf16_to_f32(g), O.bf16_to_f32(u)
+    gp = O.f32_to_bf16(np.where(np.isnan(gf), gf, np.minimum(gf, np.float32(L))).astype(np.float32))
+    up = O.f32_to_bf16(np.clip(uf, -L, L).astype(np.float32))
+    sig = O.sigmoid_bf16(gp)
+    silu = O.f32_to_bf16((O.bf16_to_f32(gp) * O.bf16_to_f32(sig)).astype(np.float32))
+    hid = O.f32_to_bf16((O.bf16_to_f32(silu) * O.bf16_to_f32(up)).astype(np.float32))
+    np.testing.assert_array_equal(to_bits(diag.sigmoid), sig)
+    np.testing.assert_array_equal(to_bits(diag.silu), silu)
+    np.testing.assert_array_equal(to_bits(diag.hidden), hid)
+    np.testing.assert_array_equal(hid, O.swiglu(g, u, L))
+    # beside the decode plan's own hidden rows (fused kernels, other FP32 order)
+    plan = submodule("packed").DecodePlan(H, I, I, cfg.n_routed_experts, 8, L)
+    out = torch.empty_like(x)
+    plan.routed(bank, shared, x, ids, torch.full((8,), 0.125, device=dev), out, dev)
+    torch.cuda.synchronize()
+    plan_hidden = to_bits(plan.debug_scratch(0)).reshape(9, I)[:8]
+    assert_parity(plan_hidden.reshape(-1), hid.reshape(-1), O, exact_fraction=0.9)
+    ident = diag.buffer_identities
+    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv)
+    assert diag.buffer_identities == ident and diag.execution_count == 2
