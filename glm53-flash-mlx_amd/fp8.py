@@ -16,6 +16,7 @@ import math
 import torch
 
 from . import _native as N
+from . import ops as _ops  # noqa: F401  (registers the glm53 custom ops)
 
 BLOCK_SIZE = 128
 DECODE_TOP_K = 8
@@ -46,6 +47,13 @@ def block_fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Ten
     expected = _scale_shape(out_features, in_features)
     if tuple(scale_inv.shape) != expected:
         raise ValueError(f"scale shape {tuple(scale_inv.shape)} != block128 shape {expected}")
+    return torch.ops.glm53.block_fp8_linear(x, weight, scale_inv, code_flags)
+
+
+def native_block_fp8_linear(x, weight, scale_inv, code_flags):
+    """The native call behind the glm53::block_fp8_linear op (arguments
+    validated by ``block_fp8_linear``)."""
+    out_features, in_features = weight.shape
     flat = x.reshape(-1, in_features).contiguous()
     weight = weight.contiguous()
     scale_inv = scale_inv.contiguous()

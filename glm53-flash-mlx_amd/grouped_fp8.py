@@ -283,25 +283,35 @@ class SortedGroupedFP8MoE(PackedFP8MoE):
             self._prefill_plans[key] = plan
         return plan
 
-    def _run(self, x, indices, scores, router):
-        N.require_device(x)
+    def native_prefill(self, x, expert_ids=None, scores=None):
+        """The native call behind glm53::moe_prefill: the fused prefill plan
+        with the module's Float32Gate (expert_ids None) or the caller's
+        routing."""
         flat = x.reshape(-1, x.shape[-1]).contiguous()
         tokens = flat.shape[0]
         out = torch.empty_like(flat)
         reduction = N.REDUCE_DIRECT if self.reduction == "direct" else N.REDUCE_GROUPED
         plan = self._prefill_plan(x.device, tokens)
         ids = sc = None
-        if indices is not None:
-            ids = indices.reshape(tokens, -1).to(torch.int32).contiguous()
+        router = self.gate if expert_ids is None else None
+        if expert_ids is not None:
+            ids = expert_ids.reshape(tokens, -1).to(torch.int32).contiguous()
             sc = scores.reshape(tokens, -1).to(torch.float32).contiguous()
-            if ids.shape[1] != self.config.num_experts_per_tok:
-                raise ValueError("indices do not match num_experts_per_tok")
         plan.run(self.bank, _c_shared(self.shared_experts), router, flat, tokens, ids, sc, reduction, out, x.device)
-        return out.reshape(x.shape), plan
+        return out.reshape(x.shape)
+
+    def _last_plan(self, device) -> PrefillPlan:
+        return self._prefill_plans[(device.index, torch.cuda.current_stream(device).cuda_stream)]
 
     def grouped_from_routes(self, x, indices, scores, *, check: bool = True):
-        result, plan = self._run(x, indices, scores, None)
-        if check and plan.invalid_routes() != 0:
+        """The grouped prefill on caller-chosen routes (grouped_fp8.py:
+        300-321).  check=True reads the plan's invalid-route count back (one
+        host synchronisation) and raises ValueError for ids out of range."""
+        N.require_device(x, indices, scores)
+        if indices.shape[-1] != self.config.num_experts_per_tok:
+            raise ValueError("indices do not match num_experts_per_tok")
+        result = torch.ops.glm53.moe_prefill(x, self._op_key, indices, scores)
+        if check and self._last_plan(x.device).invalid_routes() != 0:
             raise ValueError(f"expert ids must lie in [0, {self.bank.expert_count})")
         return result
 
@@ -310,6 +320,7 @@ class SortedGroupedFP8MoE(PackedFP8MoE):
         if routes < self.min_routes:
             return super().forward(x)
         if isinstance(self.gate, Float32Gate):
-            return self._run(x, None, None, self.gate)[0]
+            N.require_device(x)
+            return torch.ops.glm53.moe_prefill(x, self._op_key, None, None)
         indices, scores = self.gate(x)
         return self.grouped_from_routes(x, indices, scores)

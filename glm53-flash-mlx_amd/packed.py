@@ -18,6 +18,7 @@ import math
 import torch
 
 from . import _native as N
+from . import ops
 from .fp8 import BLOCK_SIZE, DECODE_TOP_K, DirectFP8MoE, block_fp8_linear, swiglu
 from .ownership import (ResidentTensor, TensorLayout, borrowed_stable_tensor, owned_tensor, require_resident,
                         resident_concatenate, storage_descriptor)
@@ -546,7 +547,11 @@ def _c_shared(shared_experts):
 
 
 class PackedFP8MoE(DirectFP8MoE):
-    """Exact fused batch-1 decode and Direct semantics over a packed bank."""
+    """Exact fused batch-1 decode and Direct semantics over a packed bank.
+
+    One-token calls go through the ``glm53::moe_decode`` custom op (one
+    opaque node under torch.compile); prefill keeps the Direct semantics
+    (a host readback of the ids per call, as the reference's Direct)."""
 
     def __init__(self, bank, config, gate, shared_experts):
         torch.nn.Module.__init__(self)
@@ -556,6 +561,7 @@ class PackedFP8MoE(DirectFP8MoE):
         self.shared_experts = shared_experts
         self._expert_views = tuple(bank.expert(i, limit=config.swiglu_limit) for i in range(bank.expert_count))
         self._plans: dict = {}
+        self._op_key = ops.register_owner(self)
 
     def _expert(self, expert_id: int):
         return self._expert_views[expert_id]
@@ -572,18 +578,31 @@ class PackedFP8MoE(DirectFP8MoE):
             self._plans[key] = plan
         return plan
 
+    def native_decode(self, x, expert_ids=None, scores=None):
+        """The native call behind glm53::moe_decode: x holds one token;
+        with expert_ids / scores the caller's routing (the reference's
+        execute(x, ids, scores), native_packed_moe_plan.cpp:151), else the
+        module's Float32Gate in the router launch."""
+        flat = x.reshape(-1).contiguous()
+        out = torch.empty_like(flat)
+        plan = self._plan(x.device)
+        if expert_ids is None:
+            plan.full(self.bank, _c_shared(self.shared_experts), self.gate, flat, out, None, None, x.device)
+        else:
+            ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
+            sc = scores.reshape(-1).to(torch.float32).contiguous()
+            plan.routed(self.bank, _c_shared(self.shared_experts), flat, ids, sc, out, x.device)
+        return out.reshape(x.shape)
+
     def decode_routed(self, x, expert_ids, scores):
         """Routed + shared decode for externally chosen experts (the
         reference's execute(x, ids, scores), native_packed_moe_plan.cpp:151)."""
-        N.require_device(x)
-        flat = x.reshape(-1).contiguous()
-        ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
-        sc = scores.reshape(-1).to(torch.float32).contiguous()
-        if ids.numel() != DECODE_TOP_K or sc.numel() != DECODE_TOP_K:
+        N.require_device(x, expert_ids, scores)
+        if expert_ids.numel() != DECODE_TOP_K or scores.numel() != DECODE_TOP_K:
             raise ValueError(f"decode expects {DECODE_TOP_K} expert ids and scores")
-        out = torch.empty_like(flat)
-        self._plan(x.device).routed(self.bank, _c_shared(self.shared_experts), flat, ids, sc, out, x.device)
-        return out.reshape(x.shape)
+        if x.numel() != self.bank.hidden_size:
+            raise ValueError(f"decode expects one token of width {self.bank.hidden_size}")
+        return torch.ops.glm53.moe_decode(x, self._op_key, expert_ids, scores)
 
     def forward(self, x):
         flat_x = x.reshape(-1, x.shape[-1])
@@ -591,11 +610,7 @@ class PackedFP8MoE(DirectFP8MoE):
             return super().forward(x)
         if isinstance(self.gate, Float32Gate) and self.gate.top_k == DECODE_TOP_K:
             N.require_device(x)
-            flat = flat_x.reshape(-1).contiguous()
-            out = torch.empty_like(flat)
-            self._plan(x.device).full(self.bank, _c_shared(self.shared_experts), self.gate, flat, out, None, None,
-                                      x.device)
-            return out.reshape(x.shape)
+            return torch.ops.glm53.moe_decode(x, self._op_key, None, None)
         indices, scores = self.gate(x)
         if indices.shape[-1] != DECODE_TOP_K:
             return super().forward(x)

@@ -7,8 +7,9 @@ multiplied by ``routed_scaling_factor``.  The selection rule is the
 DeepSeek-V3 auxiliary-loss-free rule that mlx-vlm's
 ``dsv32.group_expert_select`` implements, with n_group = 1; the slot order
 (MLX leaves argpartition order unspecified) is this build's documented tie
-policy.  Decode (one token) runs a fused GEMV + top-k kernel; prefill runs an
-FP32 rocBLAS GEMM for the logits and a wavefront-per-token top-k.
+policy.  One token runs a one-workgroup-per-logit kernel, several tokens an
+LDS-tiled BF16-MFMA GEMM over the exact three-way BF16 split of the FP32
+weights; then a wavefront-per-token top-k.
 """
 
 from __future__ import annotations
@@ -16,6 +17,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as N
+from . import ops as _ops  # noqa: F401  (registers the glm53 custom ops)
 
 
 class Float32Gate(torch.nn.Module):
@@ -52,15 +54,23 @@ class Float32Gate(torch.nn.Module):
         hidden = self.weight.shape[1]
         if x.shape[-1] != hidden:
             raise ValueError(f"input width {x.shape[-1]} != router width {hidden}")
-        flat = x.reshape(-1, hidden).contiguous()
-        tokens = flat.shape[0]
-        ids = torch.empty((tokens, self.top_k), dtype=torch.int32, device=x.device)
-        scores = torch.empty((tokens, self.top_k), dtype=torch.float32, device=x.device)
-        lib = N.lib()
-        ws_bytes = lib.glm53_router_workspace_bytes(tokens, hidden, self.weight.shape[0])
-        ws = N.workspace(ws_bytes, x.device)
-        router = self.as_c_struct()
-        N.check(lib.glm53_router_topk(N.ctypes.byref(router), N.ptr(flat), tokens, N.ptr(ids), N.ptr(scores),
-                                      N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
-        lead = x.shape[:-1]
-        return ids.reshape(*lead, self.top_k), scores.reshape(*lead, self.top_k)
+        return torch.ops.glm53.router_topk(x, self.weight, self.e_score_correction_bias, self.top_k,
+                                           self.routed_scaling_factor, self.norm_topk_prob)
+
+
+def native_router_topk(x, weight, bias, top_k: int, routed_scaling_factor: float, norm_topk_prob: bool):
+    """The native call behind the glm53::router_topk op."""
+    hidden = weight.shape[1]
+    flat = x.reshape(-1, hidden).contiguous()
+    tokens = flat.shape[0]
+    ids = torch.empty((tokens, top_k), dtype=torch.int32, device=x.device)
+    scores = torch.empty((tokens, top_k), dtype=torch.float32, device=x.device)
+    lib = N.lib()
+    ws_bytes = lib.glm53_router_workspace_bytes(tokens, hidden, weight.shape[0])
+    ws = N.workspace(ws_bytes, x.device)
+    router = N.Router(weight.data_ptr(), bias.data_ptr(), weight.shape[0], hidden, top_k, float(routed_scaling_factor),
+                      int(norm_topk_prob))
+    N.check(lib.glm53_router_topk(N.ctypes.byref(router), N.ptr(flat), tokens, N.ptr(ids), N.ptr(scores),
+                                  N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
+    lead = x.shape[:-1]
+    return ids.reshape(*lead, top_k), scores.reshape(*lead, top_k)

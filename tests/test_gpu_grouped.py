@@ -526,3 +526,34 @@ def test_direct_order_prefill_equals_direct_bit_for_bit(M, dev, config2_layer, t
     ids, _ = gate(x.reshape(tokens, -1))
     singletons = int((torch.bincount(ids.reshape(-1).long(), minlength=cfg.n_routed_experts) == 1).sum())
     assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (tokens, singletons)
+
+
+def test_custom_ops_compile_without_graph_breaks(M, dev):
+    """The MoE modules call the glm53 custom ops: torch.compile with
+    fullgraph=True (no graph break allowed) traces decode and prefill, and
+    the compiled calls equal the eager ones bit for bit; torch.library.opcheck
+    validates the FP8 linear op's registration (schema, fake tensor, AOT
+    dispatch) against its real kernel."""
+    import torch
+
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
+    bank, shared, gate = syn.synth_layer(cfg, seed=131, device=dev)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    xd = syn.normal_bf16((1, 1, 512), syn.key(131, "d"), device=dev)
+    xp = syn.normal_bf16((1, 96, 512), syn.key(131, "p"), device=dev)
+
+    def step(a, b):
+        return moe(a) * 2, moe(b) + 1
+
+    compiled = torch.compile(step, fullgraph=True, backend="aot_eager")
+    want = step(xd, xp)
+    got = compiled(xd, xp)
+    torch.cuda.synchronize()
+    for g, w in zip(got, want):
+        assert torch.equal(g.view(torch.int16), w.view(torch.int16))
+    x = syn.normal_bf16((4, 256), syn.key(131, "lin"), device=dev)
+    torch.library.opcheck(torch.ops.glm53.block_fp8_linear,
+                          (x, shared.gate_proj.weight[:, :256].contiguous(),
+                           shared.gate_proj.weight_scale_inv[:, :2].contiguous(), None),
+                          test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
