@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--traffic-run", action="store_true", help="short eager program for rocprofv3 --pmc passes")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="print the counter summary of two --pmc runs of --traffic-run")
+    p.add_argument("--summarize-prefill", nargs=4, metavar=("TRACE_CSV", "FETCH_CSV", "WRITE_CSV", "BENCH_JSON"),
+                   help="print the per-kernel summary of --prefill-only runs: a --kernel-trace run, two --pmc runs "
+                        "and the JSON line of the traced run")
     return p.parse_args()
 
 
@@ -88,6 +91,9 @@ def main():
     args = parse()
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic)
+        return
+    if args.summarize_prefill:
+        summarize_prefill(*args.summarize_prefill)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported on this single-GPU build "
@@ -125,7 +131,10 @@ def main():
     log(f"generated {L} layers, {resident / 1e9:.1f} GB resident, in {gen_s:.1f} s")
 
     if args.prefill_only:
-        print(json.dumps({"prefill": bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn)}))
+        line = json.dumps({"prefill": bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn)})
+        print(line, flush=True)
+        if args.json_out:
+            Path(args.json_out).write_text(line + "\n")
         return
 
     # ------------------------------------------------------- decode graph ---
@@ -570,6 +579,89 @@ def summarize_traffic(fetch_csv, write_csv):
           f"-> WRITE_SIZE x {write_scale:.4f}")
     print()
     print("traffic_json: " + json.dumps({"fetch_scale": fetch_scale, "write_scale": write_scale, "kernels": out}))
+
+
+def _prefill_calls(rows, order_key):
+    """Dispatch rows of a --prefill-only run cut into MoE calls: a call runs
+    from a many-token router launch to the reduction that ends it, and counts
+    when it holds a grouped GEMM (the gate call bench_prefill makes before
+    each config has none).  The first half of the calls is config 4, the
+    second config 5."""
+    rows = sorted(rows, key=order_key)
+    calls, cur = [], None
+    for r in rows:
+        if "router_tile_kernel" in r["Kernel_Name"]:
+            cur = []
+            calls.append(cur)
+        if cur is not None:
+            cur.append(r)
+            if "reduce_kernel" in r["Kernel_Name"] and "glm53::" in r["Kernel_Name"]:
+                cur = None  # the call's last launch: the restore or Direct-order reduction
+    calls = [c for c in calls if any("grouped_gemm_kernel" in r["Kernel_Name"] for r in c)]
+    half = len(calls) // 2
+    return {"4": calls[:half], "5": calls[half:]}
+
+
+def _prefill_label(name, seen):
+    """Short kernel label; repeated kernels of one call get their position."""
+    short = name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "").replace("glm53::", "")
+    seen[short] = seen.get(short, 0) + 1
+    return short if seen[short] == 1 else f"{short} #{seen[short]}"
+
+
+def summarize_prefill(trace_csv, fetch_csv, write_csv, bench_json):
+    """Per-kernel mean duration (kernel trace) and calibrated HBM bytes
+    (FETCH_SIZE x the read-probe factor of the decode traffic summary,
+    WRITE_SIZE 1:1) of one grouped prefill call at configs 4 and 5, with
+    each GEMM's fetched bytes against its unique weight bytes."""
+    import csv
+
+    bench = json.loads(Path(bench_json).read_text())["prefill"]
+    fetch_scale = 1.0
+    for line in (ROOT / "profiles" / "decode_traffic_pmc.md").read_text().splitlines():
+        if line.startswith("traffic_json: "):
+            fetch_scale = json.loads(line[len("traffic_json: "):])["fetch_scale"]
+    trace = _prefill_calls(list(csv.DictReader(open(trace_csv))), lambda r: int(r["Start_Timestamp"]))
+
+    def counters(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        return _prefill_calls(rows, lambda r: int(r["Dispatch_Id"]))
+
+    fetch, write = counters(fetch_csv, "FETCH_SIZE"), counters(write_csv, "WRITE_SIZE")
+
+    def per_kernel(calls, value):
+        acc = {}
+        for call in calls:
+            seen = {}
+            for r in call:
+                acc.setdefault(_prefill_label(r["Kernel_Name"], seen), []).append(value(r))
+        return {k: statistics.mean(v) for k, v in acc.items()}
+
+    H, I = 4096, 1536
+    unique = {"grouped_gemm_kernel<1,": 2 * I * H, "grouped_gemm_kernel<0,": I * H}
+    print("| config | kernel | us | fetched MB | written MB | unique weight MB | fetched / unique |")
+    print("|---|---|---|---|---|---|---|")
+    out = {}
+    for cfg, name in (("4", "config4_256_tokens"), ("5", "config5_2048_tokens_zipf")):
+        us = per_kernel(trace[cfg], lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+        fb = per_kernel(fetch[cfg], lambda r: float(r["Counter_Value"]) * 1024.0 * fetch_scale)
+        wb = per_kernel(write[cfg], lambda r: float(r["Counter_Value"]) * 1024.0)
+        touched = bench[name]["touched_experts"]
+        for k in us:
+            u = next((b for key, b in unique.items() if k.startswith(key)), None)
+            uw = (touched + 1) * u if u else None  # touched routed experts + the shared expert
+            ratio = f"{fb[k] / uw:.2f}" if uw and k in fb else ""
+            print(f"| {cfg} | {k} | {us[k]:.1f} | {fb.get(k, float('nan')) / 1e6:.1f} | "
+                  f"{wb.get(k, float('nan')) / 1e6:.1f} | {uw / 1e6 if uw else '':{'.1f' if uw else ''}} | {ratio} |")
+            out.setdefault(cfg, {})[k] = {"us": round(us[k], 2), "fetch_bytes": round(fb.get(k, 0)),
+                                          "write_bytes": round(wb.get(k, 0))}
+        print(f"| {cfg} | whole call (HIP events, traced run) | {bench[name]['us']:.1f} | | | | |")
+    print()
+    print(f"calls: {len(trace['4'])} + {len(trace['5'])} traced, {len(fetch['4'])} + {len(fetch['5'])} counted; "
+          f"FETCH_SIZE x {fetch_scale:.4f}, WRITE_SIZE x 1; touched experts: config 4 "
+          f"{bench['config4_256_tokens']['touched_experts']}, config 5 {bench['config5_2048_tokens_zipf']['touched_experts']}")
+    print()
+    print("prefill_json: " + json.dumps(out))
 
 
 def load_traffic(kernel_key):
