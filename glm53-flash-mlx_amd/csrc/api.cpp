@@ -1450,10 +1450,11 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   }
   // 1. activations -> exact hi/lo E4M3 split
   HIP_TRY(split(x, T, H, p->xq, st), "split x");
-  // 2. expert-sorted route plan: 64-route descriptors when experts average
-  // at least 32 routes (fewer re-reads of each weight tile), 32-route ones
-  // (a deeper load ring per workgroup) otherwise
-  const int tile = R >= 32 * E ? kGemmTileRows : kGemmMinTileRows;
+  // 2. expert-sorted route plan: 128-route descriptors (the wide GEMM shape)
+  // when experts average at least 48 routes, 64-route ones from 32 (fewer
+  // re-reads of each weight tile), 32-route ones (a deeper load ring per
+  // workgroup) below
+  const int tile = R >= 48 * E ? kGemmWideRows : R >= 32 * E ? kGemmTileRows : kGemmMinTileRows;
   const int64_t cap = cdiv(R, tile) + E;
   if ((rc = route_plan_impl(ids, sc, R, k, E, tile, p->sorted_route, p->inverse, p->sorted_expert,
                             p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,
@@ -1475,6 +1476,7 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   g.tile_start = p->tile_start;
   g.tile_len = p->tile_len;
   g.tile_rows = tile;
+  g.used_descriptors = p->status + 1;
   g.experts = E;
   g.weight = bank->gate_up_weight;
   g.weight_up = bank->gate_up_weight + I * H;
@@ -1517,6 +1519,7 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   d.tile_start = p->tile_start;
   d.tile_len = p->tile_len;
   d.tile_rows = tile;
+  d.used_descriptors = p->status + 1;
   d.experts = E;
   d.weight = bank->down_weight;
   d.w_expert_stride = H * I;

@@ -18,14 +18,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even FP32 -> BF16 (the Metal/MLX bfloat conversion).
+// Round-to-nearest-even FP32 -> BF16 (the Metal/MLX bfloat conversion); a
+// NaN keeps its upper bits and is made quiet.  gfx950's v_cvt_pk_bf16_f32
+// (what the __bf16 conversion compiles to) gives exactly these bits: checked
+// on the GPU against the integer form -- (u + 0x7fff + ((u >> 16) & 1)) >> 16,
+// NaN -> (u >> 16) | 0x40 -- for all 2^32 FP32 patterns.  One instruction
+// instead of a rounding sequence with a NaN select at every BF16 step.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -126,21 +126,49 @@ __device__ __forceinline__ float sigmoid_mlx_bf16(uint16_t gbits) {
   return g < 0.0f ? tail : bf16_round(1.0f - tail);
 }
 
+// The same function from the hardware exponential (v_exp_f32 through
+// __expf) and reciprocal (v_rcp_f32): over all 65536 BF16 inputs its BF16
+// steps round to the same bits as sigmoid_mlx_bf16's except where |g| > 87
+// (exp(|g|) near FP32 overflow, 1/d near the subnormal range) and at the
+// fast::exp point above; those inputs take sigmoid_mlx_bf16 itself.  The
+// equality over all patterns is a GPU test (through glm53_sigmoid_bf16).
+__device__ __forceinline__ float sigmoid_mlx_bf16_fast(uint16_t gbits) {
+  const float g = bf16_to_f32(gbits);
+  const float a = fabsf(g);
+  const float e = bf16_round(__expf(a));
+  const float d = bf16_round(1.0f + e);
+  const float tail = bf16_round(__builtin_amdgcn_rcpf(d));
+  const float upper = bf16_round(1.0f - tail);
+  if (!(a <= 87.0f) || gbits == 0xC0DBu) return sigmoid_mlx_bf16(gbits);
+  return g < 0.0f ? tail : upper;
+}
+
 // Clamped SwiGLU with the reference's exact rounding points:
 // g' = T(min(T(g), L)); u' = T(clip(T(u), -L, L)); h = T(T(g' * s(g')) * u').
 // Inputs are the FP32 accumulator values before the projection's BF16 store.
-__device__ __forceinline__ uint16_t swiglu_mlx(float gate_acc, float up_acc, float limit) {
+// swiglu_mlx_prepare gives g' (BF16 bits) and u'; swiglu_mlx_finish the
+// output from them and s(g').
+__device__ __forceinline__ void swiglu_mlx_prepare(float gate_acc, float up_acc, float limit, uint16_t& ga, float& ua) {
   float g = bf16_round(gate_acc);
   float u = bf16_round(up_acc);
   float gv = (g < limit) ? g : limit;
   if (isnan(g)) gv = g;
   float uv = fminf(fmaxf(u, -limit), limit);
   if (isnan(u)) uv = u;
-  uint16_t ga = f32_to_bf16(gv);
-  float gaf = bf16_to_f32(ga);
-  float ua = bf16_round(uv);
-  float silu = bf16_round(gaf * sigmoid_mlx_bf16(ga));
+  ga = f32_to_bf16(gv);
+  ua = bf16_round(uv);
+}
+
+__device__ __forceinline__ uint16_t swiglu_mlx_finish(uint16_t ga, float ua, float sigma) {
+  float silu = bf16_round(bf16_to_f32(ga) * sigma);
   return f32_to_bf16(silu * ua);
+}
+
+__device__ __forceinline__ uint16_t swiglu_mlx(float gate_acc, float up_acc, float limit) {
+  uint16_t ga;
+  float ua;
+  swiglu_mlx_prepare(gate_acc, up_acc, limit, ga, ua);
+  return swiglu_mlx_finish(ga, ua, sigmoid_mlx_bf16_fast(ga));
 }
 
 }  // namespace glm53

@@ -536,12 +536,13 @@ __global__ void weighted_reduction_kernel(WeightedReductionArgs a) {
   a.out[h] = f32_to_bf16(r);
 }
 
-// The MLX BF16 sigmoid of the SwiGLU epilogue on its own (diagnostic entry
-// point; lets a test pin the device arithmetic against the reference's
-// exhaustive sweep).
+// The MLX BF16 sigmoid of the SwiGLU epilogues on its own, in the form they
+// evaluate (diagnostic entry point; lets a test pin the device arithmetic
+// against the reference's exhaustive sweep and the oracle over every BF16
+// pattern).
 __global__ void sigmoid_bf16_kernel(const uint16_t* g, uint16_t* out, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = f32_to_bf16(sigmoid_mlx_bf16(g[i]));
+  if (i < n) out[i] = f32_to_bf16(sigmoid_mlx_bf16_fast(g[i]));
 }
 
 __global__ void add_bf16_kernel(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n) {

@@ -10,6 +10,7 @@ constexpr int kPlanMaxExperts = 1024;
 constexpr int kGroupedTileRows = 32;   // routes per descriptor of the reference (grouped_fp8.py:20)
 constexpr int kGemmTileRows = 64;      // routes per descriptor of the MFMA grouped GEMM (many routes per expert)
 constexpr int kGemmMinTileRows = 32;   // its narrow form (one group per wavefront, deeper ring)
+constexpr int kGemmWideRows = 128;     // its wide form (128-route descriptors x 256 weight rows per item)
 constexpr int kMaxReduceTopK = 16;
 enum { GEMM_PLAIN = 0, GEMM_SWIGLU = 1 };
 
@@ -70,8 +71,12 @@ struct GroupedGemmArgs {
   int64_t out_row_stride;
   const int32_t* fixup;       // device flag: weights hold 0x7F/0xFF codes (or null)
   const int32_t* fixup_up;    // SwiGLU mode: the up weights' flag when kept apart (or null)
-  int tile_rows;                 // routes per descriptor: kGemmMinTileRows, or kGemmTileRows (also 0)
+  int tile_rows;                 // routes per descriptor: kGemmMinTileRows, kGemmTileRows (also 0) or kGemmWideRows
   int64_t n_tiles, descriptors;  // set by the launcher
+  // device count of the routed descriptors in use (the route plan's
+  // status[1]), or null: all `descriptors`.  Work items are dealt over
+  // the descriptors in use only, so unused capacity costs no XCD share.
+  const unsigned* used_descriptors;
   // A dense problem run by the same launch after the routed descriptors (the
   // shared expert): x_descriptors implicit descriptors of tile_rows rows over
   // rows 0 .. x_routes - 1 (identity activation rows), with its own

@@ -437,6 +437,32 @@ struct ItemSource {
   int64_t out_row_stride;
 };
 
+// SWIGLU epilogue of a wavefront: group j of the wavefront is descriptor
+// group g0 + gstep j; lane l holds, for its routes 8 g + 2 (l / 16) + h,
+// gate tiles 0 .. T - 1 in acc[j][t] and the matching up tiles in
+// acc[j][t + T]; output column c0 + 16 t + l % 16.
+template <int NGW, int T>
+__device__ __forceinline__ void swiglu_epilogue(const GroupedGemmArgs& a, const ItemSource& src, int32_t start,
+                                                int32_t len, int g0, int gstep, int64_t c0,
+                                                const float (&acc)[NGW > 0 ? NGW : 1][2 * T][2], int lane) {
+  const int n16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int g = g0 + gstep * j;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = g * 8 + 2 * kq + h;
+      if (r >= len) continue;
+      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int64_t c = c0 + 16 * t + n16;
+        if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][h], acc[j][t + T][h], a.limit);
+      }
+    }
+  }
+}
+
 template <int MODE, bool FIX, int GPW, int NGW>
 __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile, int32_t start, int32_t len,
                                                   int64_t KB, const uint8_t* const (&gb)[2][2],
@@ -491,6 +517,21 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
       i32x8 bt[8];  // all eight weight tiles read ahead: one LDS wait per stage
 #pragma unroll
       for (int t = 0; t < 8; ++t) bt[t] = lds_operand(st + t * kOperand, slots);
+      // Every (group, tile) product gets its own result registers, and tile
+      // t's results are folded into the accumulators only after tile t + 1's
+      // MFMAs are issued: the MFMAs of a stage issue back to back while the
+      // folding VALU work runs beside them.  (One shared result register set
+      // made each MFMA wait for the previous one's result to be read.)
+      f32x4 c[NGW > 0 ? NGW : 1][8];
+      auto fold = [&](int t) {
+        const float sw = t < 4 ? sw_lo : sw_hi;
+#pragma unroll
+        for (int j = 0; j < NGW; ++j) {
+          // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
+          acc[j][t][0] = fmaf(fmaf(c[j][t][1], 0.0625f, c[j][t][0]), sa[j][0] * sw, acc[j][t][0]);
+          acc[j][t][1] = fmaf(fmaf(c[j][t][3], 0.0625f, c[j][t][2]), sa[j][1] * sw, acc[j][t][1]);
+        }
+      };
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         i32x8 bq = bt[t];
@@ -498,23 +539,22 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
         if (FIX) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            uint32_t f, c;
-            split_480(static_cast<uint32_t>(bq[i]), f, c);
+            uint32_t f, cr;
+            split_480(static_cast<uint32_t>(bq[i]), f, cr);
             bq[i] = static_cast<int>(f);
-            bc[i] = static_cast<int>(c);
+            bc[i] = static_cast<int>(cr);
           }
         }
-        const float sw = t < 4 ? sw_lo : sw_hi;
 #pragma unroll
         for (int j = 0; j < NGW; ++j) {
-          f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bq, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
-                                                                      0, 127, 0, 127);
-          if (FIX) c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bc, c, 0, 0, 0, 127, 0, 127);
-          // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
-          acc[j][t][0] = fmaf(fmaf(c[1], 0.0625f, c[0]), sa[j][0] * sw, acc[j][t][0]);
-          acc[j][t][1] = fmaf(fmaf(c[3], 0.0625f, c[2]), sa[j][1] * sw, acc[j][t][1]);
+          c[j][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bq, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
+                                                                     127, 0, 127);
+          if (FIX) c[j][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bc, c[j][t], 0, 0, 0, 127, 0, 127);
         }
+        if (t > 0) fold(t - 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      fold(7);
     }
     slot = slot == kStages - 1 ? 0 : slot + 1;
   }
@@ -535,13 +575,37 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
           const int64_t c = ntile * kTileRows + t * 16 + n16;
           if (c < a.N) orow[c] = f32_to_bf16(acc[j][t][h]);
         }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int64_t c = ntile * (kTileRows / 2) + t * 16 + n16;
-          if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][h], acc[j][t + 4][h], a.limit);
-        }
       }
+    }
+  }
+  if (MODE == GEMM_SWIGLU) swiglu_epilogue<NGW, 4>(a, src, start, len, GPW * wave, 1, ntile * (kTileRows / 2), acc, lane);
+}
+
+// Activation block scales of a work item's ROUTES routes into LDS
+// (route-major [r][kb], or K-block-major [kb][r]): THREADS / ROUTES threads
+// per route, each with its route's token row, eight loads in flight per
+// thread (indices clamped so that every load is unconditional), then the
+// stores.  Routes past the descriptor's end repeat its last route.
+template <int ROUTES, int THREADS, bool KB_MAJOR>
+__device__ __forceinline__ void load_activation_scales(const ItemSource& src, int32_t start, int32_t len,
+                                                       int64_t KB, float* lds_sa) {
+  constexpr int TPR = THREADS / ROUTES;
+  static_assert(TPR * ROUTES == THREADS, "threads split evenly over the routes");
+  const int r = static_cast<int>(threadIdx.x) / TPR, sub = static_cast<int>(threadIdx.x) % TPR;
+  const int64_t route = start + (r < len ? r : len - 1);
+  const int64_t token = src.a_row_index != nullptr ? src.a_row_index[route] : route;
+  const float* row = src.a_scale + token * KB;
+  for (int64_t kb0 = sub; kb0 < KB; kb0 += 8 * TPR) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t kb = kb0 + u * TPR;
+      v[u] = row[kb < KB ? kb : KB - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t kb = kb0 + u * TPR;
+      if (kb < KB) lds_sa[KB_MAJOR ? kb * ROUTES + r : r * KB + kb] = v[u];
     }
   }
 }
@@ -554,20 +618,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int32_t expert, start, len;
-  if (src.tile_expert != nullptr) {
-    expert = src.tile_expert[d];
-    start = src.tile_start[d];
-    len = src.tile_len[d];
-    if (start >= src.routes || len <= 0) return;
-    if (expert < 0 || expert >= src.experts) return;
-    if (len > kRoutes) len = kRoutes;
-    if (start + len > src.routes) len = static_cast<int32_t>(src.routes - start);
-  } else {
-    expert = 0;
-    start = static_cast<int32_t>(d * kRoutes);
-    len = static_cast<int32_t>(src.routes - start < kRoutes ? src.routes - start : kRoutes);
-    if (len <= 0) return;
-  }
+  if (!item_routes<kRoutes>(src, d, expert, start, len)) return;
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
   const int groups = (len + 7) >> 3;
@@ -581,10 +632,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
     const int64_t route = start + (r < len ? r : len - 1);
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
-  for (int64_t i = threadIdx.x; i < kRoutes * KB; i += 256) {
-    const int r = static_cast<int>(i / KB);
-    lds_sa[i] = src.a_scale[token_of(r) * KB + (i - r * KB)];
-  }
+  load_activation_scales<kRoutes, 256, false>(src, start, len, KB, lds_sa);
   const int64_t srow = MODE == GEMM_PLAIN ? ntile : (ntile >> 1);
   const int64_t soff = static_cast<int64_t>(expert) * a.s_expert_stride + srow * a.s_cols;
   for (int64_t i = threadIdx.x; i < (MODE == GEMM_SWIGLU ? 2 : 1) * KB; i += 256)
@@ -640,22 +688,16 @@ size_t gemm_lds_bytes(int64_t K) {
          sizeof(float) * (32 * GPW + 2) * static_cast<size_t>(K / kBlock);
 }
 
-// Work items (column tile, descriptor) are dealt to the XCDs in contiguous
-// runs: workgroup i runs on XCD i % 8, and item w = (i % 8) * ceil(W / 8) +
-// i / 8 keeps neighbouring items (same tile, consecutive descriptors of one
-// expert) on one XCD and its L2.
-template <int MODE, int GPW>
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
-  const int64_t D = a.descriptors + a.x_descriptors;
-  const int64_t items = a.n_tiles * D;
-  const int64_t per_xcd = (items + 7) / 8;
-  const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (w >= items) return;
-  const int64_t ntile = w / D;
-  int64_t d = w % D;
-  const bool dense = d >= a.descriptors;  // an item of the dense problem
-  if (dense) d -= a.descriptors;
+// The work item w of a launch: its column tile, its descriptor (of the
+// routed problem or, past the routed descriptors, of the dense one), the
+// operands it reads and whether its weights hold 0x7F/0xFF codes.
+__device__ __forceinline__ ItemSource item_source(const GroupedGemmArgs& a, int64_t used, int64_t w, int64_t& ntile,
+                                                  int64_t& d, bool& fix) {
+  const int64_t D = used + a.x_descriptors;
+  ntile = w / D;
+  d = w % D;
+  const bool dense = d >= used;  // an item of the dense problem
+  if (dense) d -= used;
   ItemSource src;
   src.a_hi = dense ? a.x_a_hi : a.a_hi;
   src.a_lo = dense ? a.x_a_lo : a.a_lo;
@@ -673,9 +715,294 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   src.out = dense ? a.x_out : a.out;
   src.out_row_stride = dense ? a.x_out_row_stride : a.out_row_stride;
   auto set = [](const int32_t* flag) { return flag != nullptr && *flag != 0; };
-  const bool fix = dense ? set(a.x_fixup) || set(a.x_fixup_up) : set(a.fixup) || set(a.fixup_up);
+  fix = dense ? set(a.x_fixup) || set(a.x_fixup_up) : set(a.fixup) || set(a.fixup_up);
+  return src;
+}
+
+// The descriptor's expert, first route and route count (at most R routes);
+// false for an unused descriptor.
+template <int R>
+__device__ __forceinline__ bool item_routes(const ItemSource& src, int64_t d, int32_t& expert, int32_t& start,
+                                            int32_t& len) {
+  if (src.tile_expert != nullptr) {
+    expert = src.tile_expert[d];
+    start = src.tile_start[d];
+    len = src.tile_len[d];
+    if (start >= src.routes || len <= 0) return false;
+    if (expert < 0 || expert >= src.experts) return false;
+    if (len > R) len = R;
+    if (start + len > src.routes) len = static_cast<int32_t>(src.routes - start);
+  } else {
+    expert = 0;
+    start = static_cast<int32_t>(d * R);
+    len = static_cast<int32_t>(src.routes - start < R ? src.routes - start : R);
+    if (len <= 0) return false;
+  }
+  return true;
+}
+
+// The routed descriptors in use: the route plan's device count when given
+// (clamped to the capacity), else all of them.
+__device__ __forceinline__ int64_t used_descriptors(const GroupedGemmArgs& a) {
+  if (a.used_descriptors == nullptr) return a.descriptors;
+  const int64_t u = static_cast<int64_t>(*a.used_descriptors);
+  return u < a.descriptors ? u : a.descriptors;
+}
+
+// Work items (column tile, descriptor in use) are dealt to the XCDs in
+// contiguous runs: workgroup i runs on XCD i % 8, and item w = (i % 8) *
+// ceil(W / 8) + i / 8 keeps neighbouring items (same tile, consecutive
+// descriptors of one expert) on one XCD and its L2.  W counts the items of
+// descriptors in use, so every XCD gets the same share of real work; the
+// grid is sized for the capacity and its surplus workgroups exit at once.
+template <int MODE, int GPW>
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+  const int64_t used = used_descriptors(a);
+  const int64_t items = a.n_tiles * (used + a.x_descriptors);
+  const int64_t per_xcd = (items + 7) / 8;
+  if (static_cast<int64_t>(blockIdx.x / 8) >= per_xcd) return;
+  const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (w >= items) return;
+  int64_t ntile, d;
+  bool fix;
+  const ItemSource src = item_source(a, used, w, ntile, d, fix);
   if (fix) grouped_gemm_body<MODE, true, GPW>(a, src, ntile, d, lds_dyn);
   else grouped_gemm_body<MODE, false, GPW>(a, src, ntile, d, lds_dyn);
+}
+
+// ------------------------------------------ grouped GEMM, wide shape --
+//
+// For plans whose experts carry many routes: work item = one 128-route
+// descriptor (16 groups of 8 routes) x 256 weight rows (PLAIN: 256 output
+// columns; SWIGLU: 128 gate rows and the matching 128 up rows), one
+// 512-thread workgroup per CU (8 wavefronts, two per SIMD; the 2-stage ring
+// of 64 KB stages takes 128 KB of LDS).  Against the 64-route x 128-row
+// item a weight tile streams once per 128 routes instead of 64 and an
+// activation row once per 256 weight rows instead of 128, and a wavefront
+// does 32 MFMAs per stage from 12 operand reads instead of 16 from 10.
+// Wavefront w = 4 wr + wc: groups wr, wr + 2, .. wr + 14 against four 16-row weight
+// tiles (PLAIN: tiles 4 wc .. 4 wc + 3; SWIGLU: gate tiles 2 wc, 2 wc + 1 and
+// up tiles 8 + 2 wc, 9 + 2 wc).  Each wavefront issues the direct loads of
+// weight tiles 2 w, 2 w + 1 and of activation groups 2 w, 2 w + 1 (none for
+// a group past the descriptor's routes).  Every (group, tile) MFMA writes
+// its own result registers and is folded into the FP32 accumulators one
+// tile later, with the arithmetic of the narrower shapes: every shape gives
+// the same bits.
+namespace {
+constexpr int kWideGroups = kGemmWideRows / 8;                    // 16
+constexpr int kWideTiles = 16;                                    // 16-row weight tiles: 256 rows
+constexpr int kWideStageB = kWideTiles * kOperand;                // 32 KB
+constexpr int kWideStage = kWideStageB + kWideGroups * kOperand;  // 64 KB
+}  // namespace
+
+size_t gemm_wide_lds_bytes(int64_t K) {
+  // 2-stage ring, activation scales [KB][128 routes], weight scales [2][KB]
+  return 2 * static_cast<size_t>(kWideStage) + sizeof(float) * (kGemmWideRows + 2) * static_cast<size_t>(K / kBlock);
+}
+
+template <int MODE, bool FIX, int NGW>
+__device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
+                                               int32_t start, int32_t len, int64_t KB,
+                                               const uint8_t* const (&gb)[2][2], const uint8_t* const (&ga)[2][2],
+                                               int na, uint8_t* lds, uint32_t lds_addr, const float* lds_sa,
+                                               const float* lds_sw, int wave, int lane) {
+  const int wr = wave >> 2, wc = wave & 3;
+  const int kq = lane >> 4;
+  const OperandSlots slots = operand_slots(lane);
+  auto issue = [&](int64_t kb, int slot) {
+    const int64_t ko = kb * kBlock;
+    const uint32_t sb = lds_addr + slot * kWideStage + 2 * wave * kOperand;
+    lds_direct16(gb[0][0] + ko, sb);
+    lds_direct16(gb[0][1] + ko, sb + 1024);
+    lds_direct16(gb[1][0] + ko, sb + kOperand);
+    lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
+    const uint32_t sa = lds_addr + slot * kWideStage + kWideStageB + 2 * wave * kOperand;
+    if (na > 0) {
+      lds_direct16(ga[0][0] + ko, sa);
+      lds_direct16(ga[0][1] + ko, sa + 1024);
+    }
+    if (na > 1) {
+      lds_direct16(ga[1][0] + ko, sa + kOperand);
+      lds_direct16(ga[1][1] + ko, sa + kOperand + 1024);
+    }
+  };
+  // the LDS tile of the wavefront's weight tile tt (0..3)
+  auto tile_of = [&](int tt) { return MODE == GEMM_PLAIN ? 4 * wc + tt : (tt < 2 ? 2 * wc + tt : 8 + 2 * wc + tt - 2); };
+
+  float acc[NGW > 0 ? NGW : 1][4][2];
+#pragma unroll
+  for (int j = 0; j < NGW; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[j][t][0] = acc[j][t][1] = 0.0f;
+
+  issue(0, 0);
+  int slot = 0;
+  for (int64_t kb = 0; kb < KB; ++kb) {
+    stage_barrier<0>();  // stage kb landed; every wavefront is done reading the other slot
+    if (kb + 1 < KB) issue(kb + 1, slot ^ 1);
+    if (NGW > 0) {
+      const uint8_t* st = lds + slot * kWideStage;
+      // the wavefront's four weight tiles stay in registers for the stage;
+      // activation groups stream through them one at a time
+      i32x8 bq[4], bc[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        bq[tt] = lds_operand(st + tile_of(tt) * kOperand, slots);
+        bc[tt] = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+        if (FIX) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            uint32_t f, cr;
+            split_480(static_cast<uint32_t>(bq[tt][i]), f, cr);
+            bq[tt][i] = static_cast<int>(f);
+            bc[tt][i] = static_cast<int>(cr);
+          }
+        }
+      }
+      const float sw0 = lds_sw[kb], sw1 = lds_sw[KB + kb];
+      // PLAIN: the wavefront's four tiles lie in one 128-row scale block;
+      // SWIGLU: tiles 0-1 are gate rows, 2-3 up rows
+      auto sw_of = [&](int tt) { return MODE == GEMM_PLAIN ? (wc >> 1 ? sw1 : sw0) : (tt < 2 ? sw0 : sw1); };
+      // group of step j: 2 j + wr (both wavefront rows of a SIMD busy on part-filled descriptors)
+      const float* sa_row = lds_sa + kb * kGemmWideRows + 8 * wr + 2 * kq;
+      f32x4 c[4];
+      float2 sa_prev = make_float2(0.0f, 0.0f);
+      // c[tt] of group j - 1 is folded just before group j's MFMA on tile tt
+      // overwrites it (4 MFMAs after it was issued)
+      auto fold = [&](int j, int tt, float2 sa) {
+        const float sw = sw_of(tt);
+        // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
+        acc[j][tt][0] = fmaf(fmaf(c[tt][1], 0.0625f, c[tt][0]), sa.x * sw, acc[j][tt][0]);
+        acc[j][tt][1] = fmaf(fmaf(c[tt][3], 0.0625f, c[tt][2]), sa.y * sw, acc[j][tt][1]);
+      };
+#pragma unroll
+      for (int j = 0; j < NGW; ++j) {
+        const i32x8 av = lds_operand(st + kWideStageB + (2 * j + wr) * kOperand, slots);
+        const float2 sa = *reinterpret_cast<const float2*>(sa_row + 16 * j);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          if (j > 0) fold(j - 1, tt, sa_prev);
+          c[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bq[tt], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
+                                                                   127, 0, 127);
+          if (FIX) c[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bc[tt], c[tt], 0, 0, 0, 127, 0, 127);
+        }
+        sa_prev = sa;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) fold(NGW - 1, tt, sa_prev);
+    }
+    slot ^= 1;
+  }
+
+  // epilogue: lane holds columns 16 tile + l % 16 of routes 8 g + 2 kq + h
+  const int n16 = lane & 15;
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int g = 2 * j + wr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = g * 8 + 2 * kq + h;
+      if (r >= len) continue;
+      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
+      if (MODE == GEMM_PLAIN) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int64_t col = ntile * 256 + 16 * (4 * wc + tt) + n16;
+          if (col < a.N) orow[col] = f32_to_bf16(acc[j][tt][h]);
+        }
+      }
+    }
+  }
+  if (MODE == GEMM_SWIGLU) swiglu_epilogue<NGW, 2>(a, src, start, len, wr, 2, ntile * 128 + 32 * wc, acc, lane);
+}
+
+template <int MODE, bool FIX>
+__device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
+                                               int64_t d, uint8_t* lds) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  int32_t expert, start, len;
+  if (!item_routes<kGemmWideRows>(src, d, expert, start, len)) return;
+  const int64_t K = a.K;
+  const int64_t KB = K / kBlock;
+  const int groups = (len + 7) >> 3;
+  float* lds_sa = reinterpret_cast<float*>(lds + 2 * kWideStage);  // [KB][128]
+  float* lds_sw = lds_sa + kGemmWideRows * KB;                       // [2][KB]
+  auto token_of = [&](int r) -> int64_t {
+    const int64_t route = start + (r < len ? r : len - 1);
+    return src.a_row_index != nullptr ? src.a_row_index[route] : route;
+  };
+  load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_sa);
+  const int64_t srows = (a.N + 127) / 128;
+  const int64_t s0 = MODE == GEMM_PLAIN ? 2 * ntile : ntile;
+  const int64_t s1 = MODE == GEMM_PLAIN ? (2 * ntile + 1 < srows ? 2 * ntile + 1 : srows - 1) : ntile;
+  const float* sc0 = src.scale + static_cast<int64_t>(expert) * a.s_expert_stride + s0 * a.s_cols;
+  const float* sc1 = (MODE == GEMM_PLAIN ? src.scale : src.scale_up) + static_cast<int64_t>(expert) * a.s_expert_stride +
+                     s1 * a.s_cols;
+  for (int64_t i = threadIdx.x; i < 2 * KB; i += 512) lds_sw[i] = i < KB ? sc0[i] : sc1[i - KB];
+  __syncthreads();
+
+  // per-lane global sources of the direct loads: load h of a tile fills its
+  // rows 8 h .. 8 h + 7, lane l reading row 8 h + l / 8
+  auto b_row = [&](int t, int h) -> const uint8_t* {
+    const int rr = 8 * h + (lane >> 3);
+    int64_t row;
+    const uint8_t* w;
+    if (MODE == GEMM_PLAIN) {
+      row = ntile * 256 + t * 16 + rr;
+      w = src.weight;
+    } else {
+      row = ntile * 128 + (t & 7) * 16 + rr;
+      w = t < 8 ? src.weight : src.weight_up;
+    }
+    if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
+    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + load_piece_offset(lane, h);
+  };
+  const uint8_t* gb[2][2];
+  const uint8_t* ga[2][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      gb[q][h] = b_row(2 * wave + q, h);
+      // activation operand row rho: route 2 (rho / 4) + (rho / 2) % 2 of the
+      // group, hi plane for even rho, lo plane for odd
+      const int rho = 8 * h + (lane >> 3);
+      const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
+      const uint8_t* plane = (rho & 1) ? src.a_lo : src.a_hi;
+      ga[q][h] = plane + token_of((2 * wave + q) * 8 + rt) * K + load_piece_offset(lane, h);
+    }
+  int na = groups - 2 * wave;  // wave-uniform: activation groups this wavefront loads
+  na = na < 0 ? 0 : (na > 2 ? 2 : na);
+  int ngw = (groups - (wave >> 2) + 1) >> 1;  // groups this wavefront multiplies: wr, wr + 2, ...
+  ngw = ngw < 0 ? 0 : (ngw > 8 ? 8 : ngw);
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+#define GLM53_WIDE(n) \
+  wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, gb, ga, na, lds, lds_addr, lds_sa, lds_sw, wave, lane)
+  // groups past the descriptor's routes hold stale activations: their
+  // products are computed when ngw rounds up, and never stored
+  if (ngw == 0) GLM53_WIDE(0);
+  else if (FIX || ngw > 4) GLM53_WIDE(8);
+  else if (ngw > 2) GLM53_WIDE(FIX ? 8 : 4);
+  else GLM53_WIDE(FIX ? 8 : 2);
+#undef GLM53_WIDE
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512) void grouped_gemm_wide_kernel(GroupedGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+  const int64_t used = used_descriptors(a);
+  const int64_t items = a.n_tiles * (used + a.x_descriptors);
+  const int64_t per_xcd = (items + 7) / 8;
+  if (static_cast<int64_t>(blockIdx.x / 8) >= per_xcd) return;
+  const int64_t w = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (w >= items) return;
+  int64_t ntile, d;
+  bool fix;
+  const ItemSource src = item_source(a, used, w, ntile, d, fix);
+  if (fix) wide_gemm_body<MODE, true>(a, src, ntile, d, lds_dyn);
+  else wide_gemm_body<MODE, false>(a, src, ntile, d, lds_dyn);
 }
 
 // Sets *flag (pre-cleared by clear_flag_kernel) when any byte of codes is
@@ -865,6 +1192,18 @@ hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st) {
 
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st) {
   if (descriptors == 0 && a.x_descriptors == 0) return hipSuccess;
+  if (a.tile_rows == kGemmWideRows) {
+    GroupedGemmArgs g = a;
+    g.n_tiles = mode == GEMM_PLAIN ? (a.N + 255) / 256 : (a.N + 127) / 128;
+    g.descriptors = descriptors;
+    const int64_t items = g.n_tiles * (descriptors + g.x_descriptors);
+    const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
+    const size_t lds = gemm_wide_lds_bytes(a.K);
+    if (a.K % kBlock != 0 || a.K <= 0 || lds > 160 * 1024) return hipErrorInvalidValue;
+    if (mode == GEMM_PLAIN) hipLaunchKernelGGL(grouped_gemm_wide_kernel<GEMM_PLAIN>, dim3(grid), dim3(512), lds, st, g);
+    else hipLaunchKernelGGL(grouped_gemm_wide_kernel<GEMM_SWIGLU>, dim3(grid), dim3(512), lds, st, g);
+    return hipGetLastError();
+  }
   GroupedGemmArgs g = a;
   g.n_tiles = mode == GEMM_PLAIN ? (a.N + 127) / 128 : (a.N + 63) / 64;
   g.descriptors = descriptors;

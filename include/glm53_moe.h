@@ -379,8 +379,10 @@ int glm53_direct_order_reduce(const void* sorted_out, const int32_t* inverse,
                               void* stream);
 
 /* MLX BF16 sigmoid used inside the SwiGLU epilogue (packed.py:155-160),
- * elementwise over n BF16 values.  Diagnostic: pins the device arithmetic
- * against the reference's exhaustive sweep. */
+ * elementwise over n BF16 values, in the form every SwiGLU of the library
+ * evaluates (hardware exponential and reciprocal, with the correctly
+ * rounding steps where those would change a BF16 result).  Diagnostic: pins
+ * the device arithmetic against the reference's exhaustive sweep. */
 int glm53_sigmoid_bf16(const void* gate, int64_t n, void* out, void* stream);
 
 /* ------------------------------------------------------------------------

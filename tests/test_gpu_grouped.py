@@ -287,9 +287,9 @@ class SkewedGate:
 @pytest.mark.parametrize("reduction", ["grouped", "direct"])
 def test_skewed_routing_many_descriptors_matches_oracle(M, O, dev, reduction):
     """1,024 tokens over 16 experts (512 routes per expert on average): the
-    prefill takes 64-route descriptors for the routed GEMMs and 64-token
-    tiles for the shared expert; experts 0-2 hold 1,024 routes each (16
-    descriptors of one expert side by side)."""
+    prefill takes the wide GEMM shape (128-route descriptors, 128-token
+    dense tiles for the shared expert); experts 0-2 hold 1,024 routes each
+    (8 descriptors of one expert side by side)."""
     syn = submodule("synthetic")
     cfg = syn.layer_config(hidden=256, intermediate=128, experts=16, top_k=8, limit=7.0)
     bank, shared, _ = syn.synth_layer(cfg, seed=77, device=dev)
@@ -307,6 +307,56 @@ def test_skewed_routing_many_descriptors_matches_oracle(M, O, dev, reduction):
         assert_parity(to_bits(y).reshape(T, -1), want_g, O, exact_fraction=0.75)
     else:
         assert stats["bit_exact_fraction"] >= 0.75, stats
+
+
+class WeightedGate:
+    """Each token takes top_k distinct experts drawn with weights 1 / (e + 1):
+    expert route counts fall from about a third of the tokens to a few, so
+    descriptors of every fill (full, part-filled wavefront rows, one group)
+    occur side by side."""
+
+    def __init__(self, experts, top_k, seed):
+        self.experts, self.top_k, self.seed = experts, top_k, seed
+
+    def __call__(self, x):
+        import torch
+
+        rows = x.reshape(-1, x.shape[-1]).shape[0]
+        rng = np.random.default_rng(self.seed)
+        w = 1.0 / np.arange(1, self.experts + 1)
+        ids = np.stack([rng.choice(self.experts, size=self.top_k, replace=False, p=w / w.sum())
+                        for _ in range(rows)]).astype(np.int32)
+        sc = rng.uniform(0.05, 0.3, size=ids.shape).astype(np.float32)
+        return (torch.from_numpy(ids).to(x.device).reshape(*x.shape[:-1], self.top_k),
+                torch.from_numpy(sc).to(x.device).reshape(*x.shape[:-1], self.top_k))
+
+
+@pytest.mark.parametrize("codes_480", [False, True])
+def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, codes_480):
+    """The wide GEMM shape (128-route descriptors x 256 weight rows, taken
+    when experts average at least 48 routes): 300 tokens x top-4 over 8
+    experts with skewed counts (descriptors full, part-filled and single
+    groups), hidden 640 (the down GEMM's last 256-row tile half past the
+    matrix, its second scale row clamped), intermediate 384, the shared
+    expert as dense descriptors in the same launches; with 0x7F / 0xFF codes
+    in the routed gate/up and down weights, the fixup path of both modes.
+    Against the oracle's Direct MoE."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=640, intermediate=384, experts=8, top_k=4, limit=7.0)
+    bank, shared, _ = syn.synth_layer(cfg, seed=131, device=dev)
+    if codes_480:
+        bank.gate_up_weight[1, ::7, ::13] = 0x7F
+        bank.gate_up_weight[0, 5::11, 3::17] = 0xFF
+        bank.down_weight[2, ::9, 1::7] = 0x7F
+    gate = WeightedGate(8, 4, seed=13)
+    T = 300
+    x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(131, "wide"), device=dev)
+    ids, sc = (t.reshape(T, 4).cpu().numpy() for t in gate(x))
+    counts = np.bincount(ids.reshape(-1), minlength=8)
+    assert counts.max() > 128 and counts.min() < 96, counts
+    y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)(x)
+    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
 
 
 @pytest.mark.parametrize("shared_experts", [1, 2])
@@ -378,8 +428,8 @@ def test_prefill_hc_expand_epilogue_matches_plain_then_oracle(M, O, dev, reducti
 
 def test_prefill_4096_tokens_matches_oracle(M, O, dev):
     """A long prompt on a small layer: 32,768 routes (128 route-count blocks,
-    the library FP32 router above 1,024 tokens, 64-route descriptors)
-    against the oracle's Direct MoE."""
+    the many-token router, the wide GEMM shape) against the oracle's
+    Direct MoE."""
     syn = submodule("synthetic")
     cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
     bank, shared, gate = syn.synth_layer(cfg, seed=101, device=dev)
@@ -391,8 +441,10 @@ def test_prefill_4096_tokens_matches_oracle(M, O, dev):
     assert_parity(to_bits(y).reshape(T, -1), want, O)
 
 
-def test_prefill_graph_replays_match_eager(M, dev):
-    """A 300-token prefill (BF16-MFMA router, route plan, grouped GEMMs,
+@pytest.mark.parametrize("tokens", [300, 2048])
+def test_prefill_graph_replays_match_eager(M, dev, tokens):
+    """A prefill (many-token BF16-MFMA router, route plan, grouped GEMMs --
+    the 64-route shape at 300 tokens, the wide shape at 2,048 -- and the
     reduction) captured in a HIP graph: every replay, with eager work and
     synchronisations between replays, equals the eager output bit for bit."""
     import torch
@@ -401,7 +453,7 @@ def test_prefill_graph_replays_match_eager(M, dev):
     cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0)
     bank, shared, gate = syn.synth_layer(cfg, seed=111, device=dev)
     moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
-    x = syn.normal_bf16((1, 300, 512), syn.key(111, "x"), device=dev)
+    x = syn.normal_bf16((1, tokens, 512), syn.key(111, "x", tokens), device=dev)
     eager = moe(x).clone()
     torch.cuda.synchronize(dev)
     stream = torch.cuda.Stream(device=dev)
@@ -416,7 +468,7 @@ def test_prefill_graph_replays_match_eager(M, dev):
         graph.replay()
         torch.cuda.synchronize(dev)
         assert torch.equal(out, eager), i
-        noise = syn.normal_bf16((1, 300, 512), syn.key(111, "noise", i), device=dev)
+        noise = syn.normal_bf16((1, tokens, 512), syn.key(111, "noise", i), device=dev)
         with torch.cuda.stream(stream):
             moe(noise)  # eager work on the captured plan (same stream) between replays
         torch.cuda.synchronize(dev)
@@ -460,8 +512,9 @@ def test_prefill_plan_growth_keeps_captured_plans_alive(M, dev):
 def test_config5_zipf_2048_tokens_matches_oracle(M, O, dev, config5):
     """BASELINE config 5 as bench.py runs it: 2,048 tokens on the config-2
     layer (seed of the bench) with the Zipf(1.1) router bias -> 16,384
-    routes, heavy experts with over 5% of the routes (tens of 64-route
-    descriptors of one expert) and many experts under 10 routes; the
+    routes, heavy experts with over 5% of the routes (several 128-route
+    descriptors of one expert, the wide GEMM shape) and many experts under
+    10 routes; the
     many-token router above 1,024 tokens.  Every token's selection is
     checked against the oracle's router (near-tie rule); the MoE output of
     every 4th token against the oracle's Direct MoE and, for the grouped

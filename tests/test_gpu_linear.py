@@ -155,6 +155,28 @@ def test_sigmoid_matches_reference_exhaustive_sweep_hash(M, dev):
     assert hashlib.sha256(got.tobytes()).hexdigest() == golden["reference_sigmoid_sha256"]
 
 
+def test_sigmoid_every_bf16_pattern_matches_oracle(O, dev):
+    """The device sigmoid (the hardware-exponential form every SwiGLU uses,
+    with its correctly rounding fallback for |g| > 87 and the fast::exp
+    point) on all 65,536 BF16 patterns equals the oracle's MLX sigmoid bit
+    for bit on every non-NaN input (NaN in, NaN out)."""
+    import torch
+
+    N = submodule("_native")
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    vals = (bits.astype(np.uint32) << 16).view(np.float32)
+    g = from_bits(bits, dev)
+    out = torch.empty_like(g)
+    N.check(N.lib().glm53_sigmoid_bf16(N.ptr(g), g.numel(), N.ptr(out), N.stream_handle(dev)))
+    got = to_bits(out)
+    ok = ~np.isnan(vals)
+    want = O.sigmoid_bf16(bits[ok])
+    bad = np.flatnonzero(got[ok] != want)
+    assert bad.size == 0, [(hex(int(bits[ok][i])), hex(int(got[ok][i])), hex(int(want[i]))) for i in bad[:8]]
+    nan_out = (got[~ok] & 0x7F80) == 0x7F80
+    assert nan_out.all() and (got[~ok] & 0x007F).all()
+
+
 def test_swiglu_bit_exact_against_oracle(M, O, dev):
     rng = np.random.default_rng(11)
     bits = np.arange(1 << 16, dtype=np.uint16)
