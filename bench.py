@@ -597,7 +597,7 @@ def _prefill_calls(rows, order_key):
             cur.append(r)
             if "reduce_kernel" in r["Kernel_Name"] and "glm53::" in r["Kernel_Name"]:
                 cur = None  # the call's last launch: the restore or Direct-order reduction
-    calls = [c for c in calls if any("grouped_gemm_kernel" in r["Kernel_Name"] for r in c)]
+    calls = [c for c in calls if any("grouped_gemm" in r["Kernel_Name"] for r in c)]
     half = len(calls) // 2
     return {"4": calls[:half], "5": calls[half:]}
 
@@ -638,7 +638,8 @@ def summarize_prefill(trace_csv, fetch_csv, write_csv, bench_json):
         return {k: statistics.mean(v) for k, v in acc.items()}
 
     H, I = 4096, 1536
-    unique = {"grouped_gemm_kernel<1,": 2 * I * H, "grouped_gemm_kernel<0,": I * H}
+    unique = {"grouped_gemm_kernel<1,": 2 * I * H, "grouped_gemm_kernel<0,": I * H,
+              "grouped_gemm_wide_kernel<1>": 2 * I * H, "grouped_gemm_wide_kernel<0>": I * H}
     print("| config | kernel | us | fetched MB | written MB | unique weight MB | fetched / unique |")
     print("|---|---|---|---|---|---|---|")
     out = {}
