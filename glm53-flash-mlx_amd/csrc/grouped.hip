@@ -691,11 +691,11 @@ size_t gemm_lds_bytes(int64_t K) {
 // The work item w of a launch: its column tile, its descriptor (of the
 // routed problem or, past the routed descriptors, of the dense one), the
 // operands it reads and whether its weights hold 0x7F/0xFF codes.
-__device__ __forceinline__ ItemSource item_source(const GroupedGemmArgs& a, int64_t used, int64_t w, int64_t& ntile,
-                                                  int64_t& d, bool& fix) {
+__device__ __forceinline__ ItemSource item_source(const GroupedGemmArgs& a, int64_t used, int64_t w, bool desc_major,
+                                                  int64_t& ntile, int64_t& d, bool& fix) {
   const int64_t D = used + a.x_descriptors;
-  ntile = w / D;
-  d = w % D;
+  ntile = desc_major ? w % a.n_tiles : w / D;
+  d = desc_major ? w / a.n_tiles : w % D;
   const bool dense = d >= used;  // an item of the dense problem
   if (dense) d -= used;
   ItemSource src;
@@ -751,10 +751,15 @@ __device__ __forceinline__ int64_t used_descriptors(const GroupedGemmArgs& a) {
 
 // Work items (column tile, descriptor in use) are dealt to the XCDs in
 // contiguous runs: workgroup i runs on XCD i % 8, and item w = (i % 8) *
-// ceil(W / 8) + i / 8 keeps neighbouring items (same tile, consecutive
-// descriptors of one expert) on one XCD and its L2.  W counts the items of
-// descriptors in use, so every XCD gets the same share of real work; the
-// grid is sized for the capacity and its surplus workgroups exit at once.
+// ceil(W / 8) + i / 8 keeps neighbouring items on one XCD and its L2.  W
+// counts the items of descriptors in use, so every XCD gets the same share
+// of real work; the grid is sized for the capacity and its surplus
+// workgroups exit at once.  This shape orders items descriptor-major (all
+// column tiles of a descriptor, i.e. one expert's whole matrix, in a row:
+// its weight rows stream in address order and its activation rows stay in
+// L2; config 4 -9%); the wide shape tile-major (descriptors of one heavy
+// expert side by side share each weight tile; descriptor-major was 4%
+// slower there).
 template <int MODE, int GPW>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
@@ -766,7 +771,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
   if (w >= items) return;
   int64_t ntile, d;
   bool fix;
-  const ItemSource src = item_source(a, used, w, ntile, d, fix);
+  const ItemSource src = item_source(a, used, w, true, ntile, d, fix);
   if (fix) grouped_gemm_body<MODE, true, GPW>(a, src, ntile, d, lds_dyn);
   else grouped_gemm_body<MODE, false, GPW>(a, src, ntile, d, lds_dyn);
 }
@@ -1000,7 +1005,7 @@ __global__ __launch_bounds__(512) void grouped_gemm_wide_kernel(GroupedGemmArgs 
   if (w >= items) return;
   int64_t ntile, d;
   bool fix;
-  const ItemSource src = item_source(a, used, w, ntile, d, fix);
+  const ItemSource src = item_source(a, used, w, false, ntile, d, fix);
   if (fix) wide_gemm_body<MODE, true>(a, src, ntile, d, lds_dyn);
   else wide_gemm_body<MODE, false>(a, src, ntile, d, lds_dyn);
 }
