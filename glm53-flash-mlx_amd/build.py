@@ -34,11 +34,15 @@ COMMON = [
     "-Wall",
     "-Wno-unused-function",
 ]
+# Per-source additions.  grouped.hip: MFMA results in ordinary VGPRs (the
+# compiler otherwise parks the chained hi/lo results of the narrow GEMM in
+# accumulation registers and copies every element out before folding it).
+EXTRA = {"grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> Path:
     obj = BUILD / (src + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

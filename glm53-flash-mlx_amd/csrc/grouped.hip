@@ -15,12 +15,13 @@
 //    on E4M3's subnormal grid, an absolute error of at most 2^-14 * s
 //    (< 2.8e-7 * amax of the row block); the MFMA then multiplies these
 //    operands by the raw weight codes with no further rounding of products.
-//  * Grouped GEMM (grouped_fp8.py:30-140): gfx950 v_mfma_f32_16x16x128 with
-//    raw E4M3 weight codes as the B operand (no decode) and the hi/lo
+//  * Grouped GEMM (grouped_fp8.py:30-140): gfx950 v_mfma_scale_f32_16x16x128
+//    with raw E4M3 weight codes as the B operand (no decode) and the hi/lo
 //    activation rows as the A operand, both streamed from HBM into an LDS
-//    ring by direct global->LDS loads.  One MFMA covers exactly one 128-deep
-//    scale block; its result is scaled by the weight block scale and the
-//    activation scale and accumulated in FP32 registers.
+//    ring by direct global->LDS loads.  Two chained MFMAs (hi rows, then lo
+//    rows) cover one 128-deep scale block, the activation scale riding as
+//    the MFMA's E8M0 row scale; their result, times the weight block scale,
+//    accumulates in FP32 registers.
 //  * Reductions: grouped FP32 slot-order restore (grouped_fp8.py:273-276) or
 //    the exact Direct ascending-expert BF16 order
 //    (native_indexer_plan.metal:2174-2207), each with the shared-expert add.
@@ -313,11 +314,12 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
 // --------------------------------------------------------- grouped GEMM --
 //
 // Workgroup = 4 wavefronts on one work item: one descriptor (32 GPW routes
-// of one expert, 4 GPW groups of 8) times one 128-row weight tile.  Per
+// of one expert, 2 GPW pairs of 16) times one 128-row weight tile.  Per
 // 128-deep K block (a "stage"):
 //   * B: the tile's 128 weight rows of raw E4M3 codes (16 KB),
-//   * A: per 8-route group, 16 activation rows ordered [hi(r0), lo(r0),
-//     hi(r1), lo(r1), ...], gathered through the sorted token index (2 KB),
+//   * A: per 16-route pair, one 16-row operand tile of the routes' hi rows
+//     and one of their lo rows, gathered through the sorted token index
+//     (2 x 2 KB),
 // both brought straight from global memory into an LDS ring by direct loads
 // (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so no
 // registers hold data in flight and the ring's other stages stream while
@@ -327,13 +329,18 @@ __global__ __launch_bounds__(256) void split_activations_kernel(SplitArgs a) {
 // l / 16) reads its 32 operand bytes (row r, bytes 32 q .. 32 q + 31) as two
 // conflict-free 16-byte LDS reads (operand_slots).  Whole lines per load
 // stream weight tiles about 14% faster than 64 bytes of 16 rows per load.
-// Wavefront w multiplies route groups GPW w .. GPW w + GPW - 1 against the 8
-// weight tiles, one v_mfma_scale_f32_16x16x128_f8f6f4 per (group, tile);
-// lane l's accumulator rows are hi/lo of routes 2 (l / 16) and 2 (l / 16) +
-// 1, and they combine as hi + lo / 16, times the route's activation block
-// scale and the tile's weight block scale (both staged in LDS at the start).
-// Two shapes: GPW = 2 (64-route descriptors, 2-stage ring) for many routes
-// per expert, GPW = 1 (32 routes, 3-stage ring) otherwise.
+// Per (pair, weight tile) two chained v_mfma_scale_f32_16x16x128_f8f6f4
+// (pair_pass): hi rows x tile, then lo rows x tile added into the same
+// result, with the route's activation block scale (a power of two) as the A
+// rows' E8M0 scale and the lo pass's 1/16 as the B scale; the result, times
+// the tile's weight block scale, accumulates in FP32 (one FMA per element).
+// Lane l holds routes 4 (l / 16) .. 4 (l / 16) + 3 of the pair in column
+// l % 16 of the tile.  Two shapes: GPW = 2 (64-route descriptors, 2-stage
+// ring; wavefront w multiplies pair w against the 8 tiles) for many routes
+// per expert, GPW = 1 (32 routes, 3-stage ring; wavefront w multiplies pair
+// w / 2 against half of the tiles) otherwise.  Every shape computes each
+// output element by the same sequence of operations, so all give the same
+// bits.
 //
 // mode GEMM_PLAIN : the tile is output columns [128 tile, +128).
 // mode GEMM_SWIGLU: the tile is gate rows j in [64 tile, +64) (tiles 0-3)
@@ -415,6 +422,48 @@ __device__ __forceinline__ i32x8 lds_operand(const uint8_t* tile, OperandSlots o
   return (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+// E8M0 code of an activation block scale: the split's scales are powers of
+// two 2^e, -126 <= e <= 127, whose FP32 exponent field e + 127 is the code.
+__device__ __forceinline__ uint32_t scale_e8m0(float s) { return (__float_as_uint(s) >> 23) & 0xFFu; }
+
+// A weight tile's B operand as the MFMA takes it: FIX feeds codes 0x7F /
+// 0xFF as 0x7E / 0xFE and returns the +-32 corrections in bc.
+template <bool FIX>
+__device__ __forceinline__ void weight_operand(i32x8& b, i32x8& bc) {
+  bc = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
+  if (FIX) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t f, cr;
+      split_480(static_cast<uint32_t>(b[i]), f, cr);
+      b[i] = static_cast<int>(f);
+      bc[i] = static_cast<int>(cr);
+    }
+  }
+}
+
+// One pass of a 16-route pair over a weight tile: rows a (the pair's hi or
+// lo rows) times b (FIX: plus the corrections bc) added into c.  The A rows'
+// E8M0 scale is byte OPSEL of se (the lane's route), the B scale SB (127:
+// 1 for the hi rows, 123: 1/16 for the lo rows).
+template <bool FIX, int OPSEL, int SB>
+__device__ __forceinline__ f32x4 pair_pass(const i32x8& a, const i32x8& b, const i32x8& bc, f32x4 c, int se) {
+  c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, OPSEL, se, 0, SB);
+  if (FIX) c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bc, c, 0, 0, OPSEL, se, 0, SB);
+  return c;
+}
+// pair_pass with the scale byte chosen by a value that unrolling makes constant
+template <bool FIX, int SB>
+__device__ __forceinline__ f32x4 pair_pass_byte(int byte, const i32x8& a, const i32x8& b, const i32x8& bc, f32x4 c,
+                                                int se) {
+  switch (byte) {
+    case 0: return pair_pass<FIX, 0, SB>(a, b, bc, c, se);
+    case 1: return pair_pass<FIX, 1, SB>(a, b, bc, c, se);
+    case 2: return pair_pass<FIX, 2, SB>(a, b, bc, c, se);
+    default: return pair_pass<FIX, 3, SB>(a, b, bc, c, se);
+  }
+}
+
 }  // namespace
 
 // What a work item reads and writes: the routed problem's operands or the
@@ -437,39 +486,52 @@ struct ItemSource {
   int64_t out_row_stride;
 };
 
-// SWIGLU epilogue of a wavefront: group j of the wavefront is descriptor
-// group g0 + gstep j; lane l holds, for its routes 8 g + 2 (l / 16) + h,
+// SWIGLU epilogue of a wavefront: pair j of the wavefront is descriptor
+// pair p0 + pstep j; lane l holds, for its routes 16 p + 4 (l / 16) + i,
 // gate tiles 0 .. T - 1 in acc[j][t] and the matching up tiles in
 // acc[j][t + T]; output column c0 + 16 t + l % 16.
-template <int NGW, int T>
+template <int NP, int T>
 __device__ __forceinline__ void swiglu_epilogue(const GroupedGemmArgs& a, const ItemSource& src, int32_t start,
-                                                int32_t len, int g0, int gstep, int64_t c0,
-                                                const float (&acc)[NGW > 0 ? NGW : 1][2 * T][2], int lane) {
+                                                int32_t len, int p0, int pstep, int64_t c0,
+                                                const float (&acc)[NP > 0 ? NP : 1][2 * T][4], int lane) {
   const int n16 = lane & 15, kq = lane >> 4;
 #pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int g = g0 + gstep * j;
+  for (int j = 0; j < NP; ++j) {
+    const int p = p0 + pstep * j;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = g * 8 + 2 * kq + h;
+    for (int i = 0; i < 4; ++i) {
+      const int r = p * 16 + 4 * kq + i;
       if (r >= len) continue;
       uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const int64_t c = c0 + 16 * t + n16;
-        if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][h], acc[j][t + T][h], a.limit);
+        if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][i], acc[j][t + T][i], a.limit);
       }
     }
   }
 }
 
-template <int MODE, bool FIX, int GPW, int NGW>
-__device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile, int32_t start, int32_t len,
-                                                  int64_t KB, const uint8_t* const (&gb)[2][2],
-                                                  const uint8_t* const (&ga)[GPW][2], uint8_t* lds, uint32_t lds_addr,
-                                                  const float* lds_sa, const float* lds_sw, int wave, int lane) {
+// Wavefront w's share of a work item: it loads weight tiles 2 w, 2 w + 1 and
+// activation tiles GPW w .. GPW w + GPW - 1 of every stage (NL of them: none
+// when their pair has no routes), and multiplies one pair (NP = 1; NP = 0
+// when the pair has no routes) against T weight tiles: GPW = 2 pair w
+// against all 8 tiles, GPW = 1 pair w / 2 against the tiles of half h =
+// w % 2 (PLAIN: tiles 4 h .. 4 h + 3; SWIGLU: gate tiles 2 h, 2 h + 1 and
+// the matching up tiles).
+template <int MODE, bool FIX, int GPW, int NP>
+__device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
+                                                  int32_t start, int32_t len, int64_t KB,
+                                                  const uint8_t* const (&gb)[2][2], const uint8_t* const (&ga)[GPW][2],
+                                                  uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
+                                                  const float* lds_sw, int wave, int lane) {
   constexpr int kStage = stage_bytes<GPW>();
-  constexpr int P = 4 + 2 * NGW;  // direct loads per stage of this wavefront
+  constexpr int kRoutes = 32 * GPW;
+  constexpr int NL = GPW == 2 ? 2 * NP : NP;  // activation tiles this wavefront loads per stage
+  constexpr int P = 4 + 2 * NL;               // its direct loads per stage
+  constexpr int T = GPW == 2 ? 8 : 4;         // weight tiles it multiplies
+  const int pair = GPW == 2 ? wave : wave >> 1;
+  const int half = wave & 1;
   const int kq = lane >> 4;
   const OperandSlots slots = operand_slots(lane);
   auto issue = [&](int64_t kb, int slot) {
@@ -481,17 +543,23 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
     lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
     const uint32_t sa = lds_addr + slot * kStage + kStageB + GPW * wave * kOperand;
 #pragma unroll
-    for (int j = 0; j < NGW; ++j) {
+    for (int j = 0; j < NL; ++j) {
       lds_direct16(ga[j][0] + ko, sa + j * kOperand);
       lds_direct16(ga[j][1] + ko, sa + j * kOperand + 1024);
     }
   };
+  // the LDS weight tile of local tile tt, and whether it holds up rows
+  auto tile_of = [&](int tt) {
+    if (GPW == 2) return tt;
+    return MODE == GEMM_PLAIN ? 4 * half + tt : (tt < 2 ? 2 * half + tt : 4 + 2 * half + tt - 2);
+  };
+  auto up_tile = [&](int tt) { return MODE == GEMM_SWIGLU && tt >= T / 2; };
 
-  float acc[NGW > 0 ? NGW : 1][8][2];
+  float acc[NP > 0 ? NP : 1][T][4];
 #pragma unroll
-  for (int j = 0; j < NGW; ++j)
+  for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[j][t][0] = acc[j][t][1] = 0.0f;
+    for (int i = 0; i < 4; ++i) acc[0][t][i] = 0.0f;
 
   constexpr int kStages = ring_stages<GPW>();
 #pragma unroll
@@ -502,99 +570,81 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
     if (kb + kStages - 2 < KB) stage_barrier<P * (kStages - 2)>();
     else stage_barrier<0>();
     if (kb + kStages - 1 < KB) issue(kb + kStages - 1, slot == 0 ? kStages - 1 : slot - 1);
-    if (NGW > 0) {
+    if (NP > 0) {
       const uint8_t* st = lds + slot * kStage;
-      i32x8 av[NGW > 0 ? NGW : 1];
-      float sa[NGW > 0 ? NGW : 1][2];
-#pragma unroll
-      for (int j = 0; j < NGW; ++j) {
-        av[j] = lds_operand(st + kStageB + (GPW * wave + j) * kOperand, slots);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) sa[j][h] = lds_sa[((GPW * wave + j) * 8 + 2 * kq + h) * KB + kb];
-      }
+      const i32x8 ahi = lds_operand(st + kStageB + (2 * pair) * kOperand, slots);
+      const i32x8 alo = lds_operand(st + kStageB + (2 * pair + 1) * kOperand, slots);
+      const int se = lds_se[kb * kRoutes + 16 * pair + (lane & 15)];
       const float sw_lo = lds_sw[kb];
       const float sw_hi = MODE == GEMM_SWIGLU ? lds_sw[KB + kb] : sw_lo;
-      i32x8 bt[8];  // all eight weight tiles read ahead: one LDS wait per stage
+      i32x8 bq[T], bc[T];  // every weight tile read ahead: one LDS wait per stage
 #pragma unroll
-      for (int t = 0; t < 8; ++t) bt[t] = lds_operand(st + t * kOperand, slots);
-      // Every (group, tile) product gets its own result registers, and tile
-      // t's results are folded into the accumulators only after tile t + 1's
-      // MFMAs are issued: the MFMAs of a stage issue back to back while the
-      // folding VALU work runs beside them.  (One shared result register set
-      // made each MFMA wait for the previous one's result to be read.)
-      f32x4 c[NGW > 0 ? NGW : 1][8];
-      auto fold = [&](int t) {
-        const float sw = t < 4 ? sw_lo : sw_hi;
+      for (int tt = 0; tt < T; ++tt) {
+        bq[tt] = lds_operand(st + tile_of(tt) * kOperand, slots);
+        weight_operand<FIX>(bq[tt], bc[tt]);
+      }
+      // Each tile's hi pass issues T MFMAs before its lo pass reads the
+      // result, and tile tt is folded into the accumulators after tile
+      // tt + 1's lo pass is issued: the MFMAs of a stage issue back to back
+      // while the folding runs beside them.
+      f32x4 c[T];
 #pragma unroll
-        for (int j = 0; j < NGW; ++j) {
-          // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
-          acc[j][t][0] = fmaf(fmaf(c[j][t][1], 0.0625f, c[j][t][0]), sa[j][0] * sw, acc[j][t][0]);
-          acc[j][t][1] = fmaf(fmaf(c[j][t][3], 0.0625f, c[j][t][2]), sa[j][1] * sw, acc[j][t][1]);
-        }
+      for (int tt = 0; tt < T; ++tt)
+        c[tt] = pair_pass<FIX, 0, 127>(ahi, bq[tt], bc[tt], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
+      auto fold = [&](int tt) {
+        const float sw = up_tile(tt) ? sw_hi : sw_lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[0][tt][i] = fmaf(c[tt][i], sw, acc[0][tt][i]);
       };
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        i32x8 bq = bt[t];
-        i32x8 bc = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
-        if (FIX) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            uint32_t f, cr;
-            split_480(static_cast<uint32_t>(bq[i]), f, cr);
-            bq[i] = static_cast<int>(f);
-            bc[i] = static_cast<int>(cr);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < NGW; ++j) {
-          c[j][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bq, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
-                                                                     127, 0, 127);
-          if (FIX) c[j][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[j], bc, c[j][t], 0, 0, 0, 127, 0, 127);
-        }
-        if (t > 0) fold(t - 1);
+      for (int tt = 0; tt < T; ++tt) {
+        c[tt] = pair_pass<FIX, 0, 123>(alo, bq[tt], bc[tt], c[tt], se);
+        if (tt > 0) fold(tt - 1);
         __builtin_amdgcn_sched_barrier(0);
       }
-      fold(7);
+      fold(T - 1);
     }
     slot = slot == kStages - 1 ? 0 : slot + 1;
   }
 
-  // epilogue: lane holds columns 16 t + l % 16 of routes 8 g + 2 kq + h
-  const int n16 = lane & 15;
+  // epilogue: lane holds routes 16 pair + 4 kq + i, column 16 tile + l % 16
+  if (NP > 0 && MODE == GEMM_PLAIN) {
+    const int n16 = lane & 15;
 #pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int g = GPW * wave + j;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = g * 8 + 2 * kq + h;
+    for (int i = 0; i < 4; ++i) {
+      const int r = pair * 16 + 4 * kq + i;
       if (r >= len) continue;
       uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
-      if (MODE == GEMM_PLAIN) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int64_t c = ntile * kTileRows + t * 16 + n16;
-          if (c < a.N) orow[c] = f32_to_bf16(acc[j][t][h]);
-        }
+      for (int tt = 0; tt < T; ++tt) {
+        const int64_t c = ntile * kTileRows + tile_of(tt) * 16 + n16;
+        if (c < a.N) orow[c] = f32_to_bf16(acc[0][tt][i]);
       }
     }
   }
-  if (MODE == GEMM_SWIGLU) swiglu_epilogue<NGW, 4>(a, src, start, len, GPW * wave, 1, ntile * (kTileRows / 2), acc, lane);
+  if (MODE == GEMM_SWIGLU)
+    swiglu_epilogue<NP, T / 2>(a, src, start, len, pair, 1, ntile * (kTileRows / 2) + (GPW == 2 ? 0 : 32 * half), acc,
+                               lane);
 }
 
-// Activation block scales of a work item's ROUTES routes into LDS
-// (route-major [r][kb], or K-block-major [kb][r]): THREADS / ROUTES threads
-// per route, each with its route's token row, eight loads in flight per
-// thread (indices clamped so that every load is unconditional), then the
-// stores.  Routes past the descriptor's end repeat its last route.
-template <int ROUTES, int THREADS, bool KB_MAJOR>
+// Activation block scales of a work item's ROUTES routes into LDS as E8M0
+// codes, K-block-major: [kb][r], or for the wide shape (WIDE)
+// [kb][wr][r % 16][j] with r = 16 (wr + 2 j) + r % 16, so that a wavefront
+// of row wr reads the codes of its four pairs as one word.  THREADS / ROUTES
+// threads per route, each with its route's token row, eight loads in
+// flight per thread (indices clamped so that every load is unconditional),
+// then the stores.  Routes past the descriptor's end repeat its last route.
+template <int ROUTES, int THREADS, bool WIDE>
 __device__ __forceinline__ void load_activation_scales(const ItemSource& src, int32_t start, int32_t len,
-                                                       int64_t KB, float* lds_sa) {
+                                                       int64_t KB, uint8_t* lds_se) {
   constexpr int TPR = THREADS / ROUTES;
   static_assert(TPR * ROUTES == THREADS, "threads split evenly over the routes");
   const int r = static_cast<int>(threadIdx.x) / TPR, sub = static_cast<int>(threadIdx.x) % TPR;
   const int64_t route = start + (r < len ? r : len - 1);
   const int64_t token = src.a_row_index != nullptr ? src.a_row_index[route] : route;
   const float* row = src.a_scale + token * KB;
+  const int64_t pos = WIDE ? ((((r >> 4) & 1) * 16 + (r & 15)) * 4 + (r >> 5)) : r;
+  constexpr int64_t kStride = WIDE ? 128 : ROUTES;  // bytes per K block
   for (int64_t kb0 = sub; kb0 < KB; kb0 += 8 * TPR) {
     float v[8];
 #pragma unroll
@@ -605,7 +655,7 @@ __device__ __forceinline__ void load_activation_scales(const ItemSource& src, in
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int64_t kb = kb0 + u * TPR;
-      if (kb < KB) lds_sa[KB_MAJOR ? kb * ROUTES + r : r * KB + kb] = v[u];
+      if (kb < KB) lds_se[kb * kStride + pos] = static_cast<uint8_t>(scale_e8m0(v[u]));
     }
   }
 }
@@ -621,9 +671,9 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
   if (!item_routes<kRoutes>(src, d, expert, start, len)) return;
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
-  const int groups = (len + 7) >> 3;
-  float* lds_sa = reinterpret_cast<float*>(lds + ring_stages<GPW>() * kStage);  // [kRoutes][KB]
-  float* lds_sw = lds_sa + kRoutes * KB;                              // [2][KB]
+  const int pairs = (len + 15) >> 4;
+  uint8_t* lds_se = lds + ring_stages<GPW>() * kStage;                    // [KB][kRoutes]
+  float* lds_sw = reinterpret_cast<float*>(lds_se + kRoutes * KB);        // [2][KB]
 
   // ---- block scales of the work item: activations of every route, weights
   // of the tile (one 128-row scale block: PLAIN tiles are 128-aligned, SWIGLU
@@ -632,7 +682,7 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
     const int64_t route = start + (r < len ? r : len - 1);
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
-  load_activation_scales<kRoutes, 256, false>(src, start, len, KB, lds_sa);
+  load_activation_scales<kRoutes, 256, false>(src, start, len, KB, lds_se);
   const int64_t srow = MODE == GEMM_PLAIN ? ntile : (ntile >> 1);
   const int64_t soff = static_cast<int64_t>(expert) * a.s_expert_stride + srow * a.s_cols;
   for (int64_t i = threadIdx.x; i < (MODE == GEMM_SWIGLU ? 2 : 1) * KB; i += 256)
@@ -660,32 +710,31 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int h = 0; h < 2; ++h) gb[t][h] = b_row(2 * wave + t, h);
-  // activation operand row rho: route 2 (rho / 4) + (rho / 2) % 2 of the
-  // group, hi plane for even rho, lo plane for odd
+  // activation operand tile g: the hi rows (g even) or lo rows (g odd) of
+  // pair g / 2; its row rho is route 16 (g / 2) + rho
   const uint8_t* ga[GPW][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int rho = 8 * h + (lane >> 3);
-    const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
-    const uint8_t* plane = (rho & 1) ? src.a_lo : src.a_hi;
+  for (int j = 0; j < GPW; ++j) {
+    const int g = GPW * wave + j;
+    const uint8_t* plane = (g & 1) ? src.a_lo : src.a_hi;
 #pragma unroll
-    for (int j = 0; j < GPW; ++j) ga[j][h] = plane + token_of((GPW * wave + j) * 8 + rt) * K + load_piece_offset(lane, h);
+    for (int h = 0; h < 2; ++h)
+      ga[j][h] = plane + token_of(16 * (g >> 1) + 8 * h + (lane >> 3)) * K + load_piece_offset(lane, h);
   }
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  int ngw = groups - GPW * wave;  // wave-uniform
-  ngw = ngw < 0 ? 0 : (ngw > GPW ? GPW : ngw);
+  const bool active = (GPW == 2 ? wave : wave >> 1) < pairs;  // wave-uniform: this wavefront's pair holds routes
 #define GLM53_LOOP(n) \
-  grouped_gemm_loop<MODE, FIX, GPW, n>(a, src, ntile, start, len, KB, gb, ga, lds, lds_addr, lds_sa, lds_sw, wave, lane)
-  if (GPW >= 2 && ngw == 2) GLM53_LOOP(GPW >= 2 ? 2 : 0);
-  else if (ngw == 1) GLM53_LOOP(1);
+  grouped_gemm_loop<MODE, FIX, GPW, n>(a, src, ntile, start, len, KB, gb, ga, lds, lds_addr, lds_se, lds_sw, wave, lane)
+  if (active) GLM53_LOOP(1);
   else GLM53_LOOP(0);
 #undef GLM53_LOOP
 }
 
 template <int GPW>
 size_t gemm_lds_bytes(int64_t K) {
+  // ring, activation scale codes [KB][32 GPW], weight scales [2][KB]
   return static_cast<size_t>(ring_stages<GPW>()) * stage_bytes<GPW>() +
-         sizeof(float) * (32 * GPW + 2) * static_cast<size_t>(K / kBlock);
+         (32 * GPW + 2 * sizeof(float)) * static_cast<size_t>(K / kBlock);
 }
 
 // The work item w of a launch: its column tile, its descriptor (of the
@@ -779,38 +828,38 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
 // ------------------------------------------ grouped GEMM, wide shape --
 //
 // For plans whose experts carry many routes: work item = one 128-route
-// descriptor (16 groups of 8 routes) x 256 weight rows (PLAIN: 256 output
+// descriptor (8 pairs of 16 routes) x 256 weight rows (PLAIN: 256 output
 // columns; SWIGLU: 128 gate rows and the matching 128 up rows), one
 // 512-thread workgroup per CU (8 wavefronts, two per SIMD; the 2-stage ring
 // of 64 KB stages takes 128 KB of LDS).  Against the 64-route x 128-row
 // item a weight tile streams once per 128 routes instead of 64 and an
-// activation row once per 256 weight rows instead of 128, and a wavefront
-// does 32 MFMAs per stage from 12 operand reads instead of 16 from 10.
-// Wavefront w = 4 wr + wc: groups wr, wr + 2, .. wr + 14 against four 16-row weight
-// tiles (PLAIN: tiles 4 wc .. 4 wc + 3; SWIGLU: gate tiles 2 wc, 2 wc + 1 and
-// up tiles 8 + 2 wc, 9 + 2 wc).  Each wavefront issues the direct loads of
-// weight tiles 2 w, 2 w + 1 and of activation groups 2 w, 2 w + 1 (none for
-// a group past the descriptor's routes).  Every (group, tile) MFMA writes
-// its own result registers and is folded into the FP32 accumulators one
-// tile later, with the arithmetic of the narrower shapes: every shape gives
-// the same bits.
+// activation row once per 256 weight rows instead of 128.  Wavefront w =
+// 4 wr + wc multiplies pairs wr, wr + 2, wr + 4, wr + 6 against four 16-row
+// weight tiles (PLAIN: tiles 4 wc .. 4 wc + 3; SWIGLU: gate tiles 2 wc,
+// 2 wc + 1 and up tiles 8 + 2 wc, 9 + 2 wc): the four B operands stay in
+// registers for the stage and each pair's hi and lo rows stream through
+// them, 32 MFMAs per stage from 12 operand reads.  Each wavefront issues
+// the direct loads of weight tiles 2 w, 2 w + 1 and of pair w's hi and lo
+// tiles (none when the pair holds no routes).  The arithmetic per output
+// element is that of the narrower shapes, so every shape gives the same
+// bits.
 namespace {
-constexpr int kWideGroups = kGemmWideRows / 8;                    // 16
-constexpr int kWideTiles = 16;                                    // 16-row weight tiles: 256 rows
-constexpr int kWideStageB = kWideTiles * kOperand;                // 32 KB
-constexpr int kWideStage = kWideStageB + kWideGroups * kOperand;  // 64 KB
+constexpr int kWidePairs = kGemmWideRows / 16;                          // 8
+constexpr int kWideTiles = 16;                                          // 16-row weight tiles: 256 rows
+constexpr int kWideStageB = kWideTiles * kOperand;                      // 32 KB
+constexpr int kWideStage = kWideStageB + 2 * kWidePairs * kOperand;     // 64 KB
 }  // namespace
 
 size_t gemm_wide_lds_bytes(int64_t K) {
-  // 2-stage ring, activation scales [KB][128 routes], weight scales [2][KB]
-  return 2 * static_cast<size_t>(kWideStage) + sizeof(float) * (kGemmWideRows + 2) * static_cast<size_t>(K / kBlock);
+  // 2-stage ring, activation scale codes [KB][128 routes], weight scales [2][KB]
+  return 2 * static_cast<size_t>(kWideStage) + (kGemmWideRows + 2 * sizeof(float)) * static_cast<size_t>(K / kBlock);
 }
 
-template <int MODE, bool FIX, int NGW>
+template <int MODE, bool FIX, int NP>
 __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
                                                int32_t start, int32_t len, int64_t KB,
                                                const uint8_t* const (&gb)[2][2], const uint8_t* const (&ga)[2][2],
-                                               int na, uint8_t* lds, uint32_t lds_addr, const float* lds_sa,
+                                               bool loads_pair, uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
                                                const float* lds_sw, int wave, int lane) {
   const int wr = wave >> 2, wc = wave & 3;
   const int kq = lane >> 4;
@@ -822,12 +871,10 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
     lds_direct16(gb[0][1] + ko, sb + 1024);
     lds_direct16(gb[1][0] + ko, sb + kOperand);
     lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
-    const uint32_t sa = lds_addr + slot * kWideStage + kWideStageB + 2 * wave * kOperand;
-    if (na > 0) {
+    if (loads_pair) {
+      const uint32_t sa = lds_addr + slot * kWideStage + kWideStageB + 2 * wave * kOperand;
       lds_direct16(ga[0][0] + ko, sa);
       lds_direct16(ga[0][1] + ko, sa + 1024);
-    }
-    if (na > 1) {
       lds_direct16(ga[1][0] + ko, sa + kOperand);
       lds_direct16(ga[1][1] + ko, sa + kOperand + 1024);
     }
@@ -835,91 +882,84 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
   // the LDS tile of the wavefront's weight tile tt (0..3)
   auto tile_of = [&](int tt) { return MODE == GEMM_PLAIN ? 4 * wc + tt : (tt < 2 ? 2 * wc + tt : 8 + 2 * wc + tt - 2); };
 
-  float acc[NGW > 0 ? NGW : 1][4][2];
+  float acc[NP > 0 ? NP : 1][4][4];
 #pragma unroll
-  for (int j = 0; j < NGW; ++j)
+  for (int j = 0; j < NP; ++j)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[j][t][0] = acc[j][t][1] = 0.0f;
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
   issue(0, 0);
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
     stage_barrier<0>();  // stage kb landed; every wavefront is done reading the other slot
     if (kb + 1 < KB) issue(kb + 1, slot ^ 1);
-    if (NGW > 0) {
+    if (NP > 0) {
       const uint8_t* st = lds + slot * kWideStage;
       // the wavefront's four weight tiles stay in registers for the stage;
-      // activation groups stream through them one at a time
+      // its pairs' hi and lo rows stream through them
       i32x8 bq[4], bc[4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         bq[tt] = lds_operand(st + tile_of(tt) * kOperand, slots);
-        bc[tt] = (i32x8){0, 0, 0, 0, 0, 0, 0, 0};
-        if (FIX) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            uint32_t f, cr;
-            split_480(static_cast<uint32_t>(bq[tt][i]), f, cr);
-            bq[tt][i] = static_cast<int>(f);
-            bc[tt][i] = static_cast<int>(cr);
-          }
-        }
+        weight_operand<FIX>(bq[tt], bc[tt]);
       }
       const float sw0 = lds_sw[kb], sw1 = lds_sw[KB + kb];
       // PLAIN: the wavefront's four tiles lie in one 128-row scale block;
       // SWIGLU: tiles 0-1 are gate rows, 2-3 up rows
       auto sw_of = [&](int tt) { return MODE == GEMM_PLAIN ? (wc >> 1 ? sw1 : sw0) : (tt < 2 ? sw0 : sw1); };
-      // group of step j: 2 j + wr (both wavefront rows of a SIMD busy on part-filled descriptors)
-      const float* sa_row = lds_sa + kb * kGemmWideRows + 8 * wr + 2 * kq;
+      // byte j: the E8M0 scale of this lane's route in pair wr + 2 j
+      const int se = *reinterpret_cast<const int*>(lds_se + kb * kGemmWideRows + (wr * 16 + (lane & 15)) * 4);
       f32x4 c[4];
-      float2 sa_prev = make_float2(0.0f, 0.0f);
-      // c[tt] of group j - 1 is folded just before group j's MFMA on tile tt
-      // overwrites it (4 MFMAs after it was issued)
-      auto fold = [&](int j, int tt, float2 sa) {
+      // c[tt] of pair j - 1 is folded just before pair j's hi pass on tile
+      // tt overwrites it (4 MFMAs after it was issued); each lo pass reads
+      // the hi pass issued 4 MFMAs before it
+      auto fold = [&](int j, int tt) {
         const float sw = sw_of(tt);
-        // rows of c: hi(r0), lo(r0), hi(r1), lo(r1) for routes r0 = 2kq, r1 = 2kq + 1
-        acc[j][tt][0] = fmaf(fmaf(c[tt][1], 0.0625f, c[tt][0]), sa.x * sw, acc[j][tt][0]);
-        acc[j][tt][1] = fmaf(fmaf(c[tt][3], 0.0625f, c[tt][2]), sa.y * sw, acc[j][tt][1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][tt][i] = fmaf(c[tt][i], sw, acc[j][tt][i]);
       };
 #pragma unroll
-      for (int j = 0; j < NGW; ++j) {
-        const i32x8 av = lds_operand(st + kWideStageB + (2 * j + wr) * kOperand, slots);
-        const float2 sa = *reinterpret_cast<const float2*>(sa_row + 16 * j);
+      for (int j = 0; j < NP; ++j) {
+        const int pp = wr + 2 * j;
+        const i32x8 ahi = lds_operand(st + kWideStageB + (2 * pp) * kOperand, slots);
+        const i32x8 alo = lds_operand(st + kWideStageB + (2 * pp + 1) * kOperand, slots);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-          if (j > 0) fold(j - 1, tt, sa_prev);
-          c[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bq[tt], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
-                                                                   127, 0, 127);
-          if (FIX) c[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bc[tt], c[tt], 0, 0, 0, 127, 0, 127);
+          if (j > 0) fold(j - 1, tt);
+          c[tt] = pair_pass_byte<FIX, 127>(j, ahi, bq[tt], bc[tt], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
         }
-        sa_prev = sa;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) c[tt] = pair_pass_byte<FIX, 123>(j, alo, bq[tt], bc[tt], c[tt], se);
       }
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) fold(NGW - 1, tt, sa_prev);
+      for (int tt = 0; tt < 4; ++tt) fold(NP - 1, tt);
     }
     slot ^= 1;
   }
 
-  // epilogue: lane holds columns 16 tile + l % 16 of routes 8 g + 2 kq + h
-  const int n16 = lane & 15;
+  // epilogue: lane holds columns 16 tile + l % 16 of routes 16 p + 4 kq + i
+  if (MODE == GEMM_PLAIN) {
+    const int n16 = lane & 15;
 #pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int g = 2 * j + wr;
+    for (int j = 0; j < NP; ++j) {
+      const int pp = wr + 2 * j;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = g * 8 + 2 * kq + h;
-      if (r >= len) continue;
-      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
-      if (MODE == GEMM_PLAIN) {
+      for (int i = 0; i < 4; ++i) {
+        const int r = pp * 16 + 4 * kq + i;
+        if (r >= len) continue;
+        uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
           const int64_t col = ntile * 256 + 16 * (4 * wc + tt) + n16;
-          if (col < a.N) orow[col] = f32_to_bf16(acc[j][tt][h]);
+          if (col < a.N) orow[col] = f32_to_bf16(acc[j][tt][i]);
         }
       }
     }
+  } else {
+    swiglu_epilogue<NP, 2>(a, src, start, len, wr, 2, ntile * 128 + 32 * wc, acc, lane);
   }
-  if (MODE == GEMM_SWIGLU) swiglu_epilogue<NGW, 2>(a, src, start, len, wr, 2, ntile * 128 + 32 * wc, acc, lane);
 }
 
 template <int MODE, bool FIX>
@@ -931,14 +971,14 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   if (!item_routes<kGemmWideRows>(src, d, expert, start, len)) return;
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
-  const int groups = (len + 7) >> 3;
-  float* lds_sa = reinterpret_cast<float*>(lds + 2 * kWideStage);  // [KB][128]
-  float* lds_sw = lds_sa + kGemmWideRows * KB;                       // [2][KB]
+  const int pairs = (len + 15) >> 4;
+  uint8_t* lds_se = lds + 2 * kWideStage;                                   // [KB][128]
+  float* lds_sw = reinterpret_cast<float*>(lds_se + kGemmWideRows * KB);    // [2][KB]
   auto token_of = [&](int r) -> int64_t {
     const int64_t route = start + (r < len ? r : len - 1);
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
-  load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_sa);
+  load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_se);
   const int64_t srows = (a.N + 127) / 128;
   const int64_t s0 = MODE == GEMM_PLAIN ? 2 * ntile : ntile;
   const int64_t s1 = MODE == GEMM_PLAIN ? (2 * ntile + 1 < srows ? 2 * ntile + 1 : srows - 1) : ntile;
@@ -971,26 +1011,22 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       gb[q][h] = b_row(2 * wave + q, h);
-      // activation operand row rho: route 2 (rho / 4) + (rho / 2) % 2 of the
-      // group, hi plane for even rho, lo plane for odd
-      const int rho = 8 * h + (lane >> 3);
-      const int rt = 2 * (rho >> 2) + ((rho >> 1) & 1);
-      const uint8_t* plane = (rho & 1) ? src.a_lo : src.a_hi;
-      ga[q][h] = plane + token_of((2 * wave + q) * 8 + rt) * K + load_piece_offset(lane, h);
+      // pair `wave`: hi rows (q = 0) or lo rows (q = 1); row rho is route 16 wave + rho
+      const uint8_t* plane = q ? src.a_lo : src.a_hi;
+      ga[q][h] = plane + token_of(16 * wave + 8 * h + (lane >> 3)) * K + load_piece_offset(lane, h);
     }
-  int na = groups - 2 * wave;  // wave-uniform: activation groups this wavefront loads
-  na = na < 0 ? 0 : (na > 2 ? 2 : na);
-  int ngw = (groups - (wave >> 2) + 1) >> 1;  // groups this wavefront multiplies: wr, wr + 2, ...
-  ngw = ngw < 0 ? 0 : (ngw > 8 ? 8 : ngw);
+  const bool loads_pair = wave < pairs;  // wave-uniform
+  int np = (pairs - (wave >> 2) + 1) >> 1;  // pairs this wavefront multiplies: wr, wr + 2, ...
+  np = np < 0 ? 0 : (np > 4 ? 4 : np);
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
 #define GLM53_WIDE(n) \
-  wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, gb, ga, na, lds, lds_addr, lds_sa, lds_sw, wave, lane)
-  // groups past the descriptor's routes hold stale activations: their
-  // products are computed when ngw rounds up, and never stored
-  if (ngw == 0) GLM53_WIDE(0);
-  else if (FIX || ngw > 4) GLM53_WIDE(8);
-  else if (ngw > 2) GLM53_WIDE(FIX ? 8 : 4);
-  else GLM53_WIDE(FIX ? 8 : 2);
+  wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, gb, ga, loads_pair, lds, lds_addr, lds_se, lds_sw, wave, lane)
+  // pairs past the descriptor's routes hold stale activations: their
+  // products are computed when np rounds up, and never stored
+  if (np == 0) GLM53_WIDE(0);
+  else if (FIX || np > 2) GLM53_WIDE(4);
+  else if (np == 2) GLM53_WIDE(2);
+  else GLM53_WIDE(1);
 #undef GLM53_WIDE
 }
 

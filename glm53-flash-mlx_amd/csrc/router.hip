@@ -11,7 +11,7 @@
 // Work item = 128 tokens x 96 experts x one K chunk, 4 wavefronts in a 2 x 2
 // grid (64 tokens x 48 experts each: 4 x 3 MFMA tiles).  Per 32-deep K step
 // the workgroup loads the tokens' BF16 rows (8 KB) and the experts' FP32 rows
-// (12 KB) once from global memory into registers, one step ahead, splits
+// (12 KB) once from global memory into registers, kAhead steps ahead, splits
 // the weights into their three BF16 parts on the way into LDS (18 KB), and
 // every wavefront reads its MFMA operands from LDS: each operand byte leaves
 // L2 once per workgroup (the register-operand form read the token rows once
@@ -37,6 +37,10 @@ constexpr int kRowBytes = kStep * 2;            // 64 B: one BF16 row of a step 
 constexpr int kXBytes = kTileTokens * kRowBytes;   // 8 KB
 constexpr int kPlaneBytes = kTileExperts * kRowBytes;  // 6 KB per BF16 part
 constexpr int kStageBytes = kXBytes + 3 * kPlaneBytes;  // 26 KB
+#ifndef GLM53_ROUTER_AHEAD
+#define GLM53_ROUTER_AHEAD 3
+#endif
+constexpr int kAhead = GLM53_ROUTER_AHEAD;       // steps of global loads in flight
 
 // Octet q (8 BF16 = 16 B) of LDS row r sits at slot q ^ ((r >> 2) & 3): the
 // 16 lanes reading octet q of rows r .. r + 15 then spread over all banks.
@@ -132,33 +136,44 @@ __global__ __launch_bounds__(256, 2) void router_tile_kernel(RouterGemmArgs a, c
 #pragma unroll
     for (int n = 0; n < 3; ++n) acc[m][n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  StepRegs regs;
-  load(regs, k_begin);
+  // kAhead register sets: step k's global loads are issued kAhead steps
+  // before its operands go into LDS, so several steps' loads are in flight
+  // behind each step's MFMAs (one step of 32 is too short to cover them).
+  StepRegs regs[kAhead];
+#pragma unroll
+  for (int d = 0; d < kAhead; ++d)
+    if (k_begin + d * kStep < k_end) load(regs[d], k_begin + d * kStep);
   int s = 0;
-  for (int64_t k = k_begin; k < k_end; k += kStep) {
-    uint8_t* stage = lds + s * kStageBytes;
-    store(regs, stage);
-    __syncthreads();  // the stage is complete; the other stage's readers are done
-    if (k + kStep < k_end) load(regs, k + kStep);  // next step's loads fly during the MFMAs
-    bf16x8_t xa[4];
+  for (int64_t k0 = k_begin; k0 < k_end; k0 += kAhead * kStep) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      xa[m] = __builtin_bit_cast(bf16x8_t,
-                                 *reinterpret_cast<const uint4*>(stage + slot_offset(64 * wm + 16 * m + r16, q)));
-#pragma unroll
-    for (int n = 0; n < 3; ++n) {
-      const int row = 48 * wn + 16 * n + r16;
-      bf16x8_t wb[3];
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-        wb[p] = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const uint4*>(stage + kXBytes + p * kPlaneBytes + slot_offset(row, q)));
+    for (int d = 0; d < kAhead; ++d) {
+      const int64_t k = k0 + d * kStep;
+      if (k >= k_end) break;
+      uint8_t* stage = lds + s * kStageBytes;
+      store(regs[d], stage);
+      __syncthreads();  // the stage is complete; the other stage's readers are done
+      if (k + kAhead * kStep < k_end) load(regs[d], k + kAhead * kStep);
+      bf16x8_t xa[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
+        xa[m] = __builtin_bit_cast(bf16x8_t,
+                                   *reinterpret_cast<const uint4*>(stage + slot_offset(64 * wm + 16 * m + r16, q)));
 #pragma unroll
-        for (int p = 0; p < 3; ++p) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[m], wb[p], acc[m][n], 0, 0, 0);
+      for (int n = 0; n < 3; ++n) {
+        const int row = 48 * wn + 16 * n + r16;
+        bf16x8_t wb[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          wb[p] = __builtin_bit_cast(
+              bf16x8_t, *reinterpret_cast<const uint4*>(stage + kXBytes + p * kPlaneBytes + slot_offset(row, q)));
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[m], wb[p], acc[m][n], 0, 0, 0);
+      }
+      s ^= 1;
     }
-    s ^= 1;
   }
   // D layout of the 16x16 MFMA: lane holds rows 4 (lane / 16) + i, column lane % 16.
   float* out = a.partial + split * a.tokens * a.experts;
