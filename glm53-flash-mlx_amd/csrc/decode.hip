@@ -386,29 +386,39 @@ __global__ __launch_bounds__(64 * kMaxGemvParts) void gemv_split_kernel(GemvArgs
 }
 
 // ------------------------------------------------------ per-token top-k ----
-// Every partial is requested before the first is added (splits <= 16).
+// Every partial and the bias are requested before the first partial is added
+// (splits <= 16); the selection is wave_topk_words_sorted over the token's
+// (sigmoid, key) words, the order and arithmetic of wave_topk_regs.
 template <int P>
-__device__ __forceinline__ void topk_token_partials(const TopkArgs& a, int64_t t, int lane) {
+__device__ __forceinline__ void topk_token_partials(const TopkArgs& a, int64_t t, int lane, TopkScratch& scratch) {
   const int splits = a.splits > 1 ? a.splits : 1;
   float part[P][kMaxRouterSplits];
+  float bias[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     const int64_t c = lane + 64 * i;
+    bias[i] = c < a.experts ? a.bias[c] : 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxRouterSplits; ++s)
       part[i][s] = s < splits && c < a.experts ? a.logits[s * a.split_stride + t * a.experts + c] : 0.0f;
   }
-  float lg[P];
+  unsigned long long wd[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     float v = part[i][0];
 #pragma unroll
     for (int s = 1; s < kMaxRouterSplits; ++s)
       if (s < splits) v += part[i][s];
-    lg[i] = v;
+    const int64_t c = lane + 64 * i;
+    wd[i] = 0ull;
+    if (c < a.experts) {
+      const float sg = router_sigmoid(v);
+      const uint32_t key = max(orderable_bits(__fadd_rn(sg, bias[i])), 1u);
+      wd[i] = (static_cast<unsigned long long>(__float_as_uint(sg)) << 32) | key;
+    }
   }
-  wave_topk_regs<P>(lg, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane,
-                    a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
+  wave_topk_words_sorted<P>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, a.ids_out + t * a.top_k,
+                            a.scores_out + t * a.top_k, scratch);
 }
 
 // kPartials: logits come as a.splits partial planes; otherwise whole.
@@ -418,9 +428,11 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= a.tokens) return;
   if constexpr (kPartials) {
-    if (a.experts <= 128) topk_token_partials<2>(a, t, lane);
-    else if (a.experts <= 320) topk_token_partials<5>(a, t, lane);
-    else topk_token_partials<kMaxRouterExperts / 64>(a, t, lane);
+    __shared__ TopkScratch scratch[4];
+    TopkScratch& sc = scratch[threadIdx.x >> 6];
+    if (a.experts <= 128) topk_token_partials<2>(a, t, lane, sc);
+    else if (a.experts <= 320) topk_token_partials<5>(a, t, lane, sc);
+    else topk_token_partials<kMaxRouterExperts / 64>(a, t, lane, sc);
   } else {
     wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
               lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);

@@ -53,15 +53,35 @@ __global__ __launch_bounds__(256) void route_count_kernel(RoutePlanArgs a) {
   if (threadIdx.x == 0) a.block_invalid[blockIdx.x] = bad;
 }
 
-// Inclusive Hillis-Steele scan of buf[0..n) in LDS (n <= 1024, 1024 threads).
-__device__ void block_scan_inclusive(unsigned* buf, int n) {
-  for (int off = 1; off < n; off <<= 1) {
-    unsigned v = 0;
-    if (threadIdx.x < n && threadIdx.x >= off) v = buf[threadIdx.x - off];
-    __syncthreads();
-    if (threadIdx.x < n) buf[threadIdx.x] += v;
-    __syncthreads();
+// Inclusive scans of a[0..n) and b[0..n) in LDS (n <= 1024, 1024 threads,
+// all of them calling): a shuffle scan inside each wavefront, then each
+// thread adds the totals of the wavefronts before it.
+__device__ void block_scan2_inclusive(unsigned* a, unsigned* b, int n) {
+  __shared__ unsigned wave_a[16], wave_b[16];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  unsigned x = t < n ? a[t] : 0u, y = t < n ? b[t] : 0u;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned xo = __shfl_up(x, off), yo = __shfl_up(y, off);
+    if (lane >= off) {
+      x += xo;
+      y += yo;
+    }
   }
+  if (lane == 63) {
+    wave_a[w] = x;
+    wave_b[w] = y;
+  }
+  __syncthreads();
+  for (int i = 0; i < w; ++i) {
+    x += wave_a[i];
+    y += wave_b[i];
+  }
+  if (t < n) {
+    a[t] = x;
+    b[t] = y;
+  }
+  __syncthreads();
 }
 
 __global__ __launch_bounds__(1024) void route_scan_kernel(RoutePlanArgs a) {
@@ -75,7 +95,17 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RoutePlanArgs a) {
   if (t < a.experts) {
     unsigned run = 0;
     int64_t b = 0;
-    for (; b + 8 <= a.blocks; b += 8) {  // 8 loads in flight per round trip
+    for (; b + 32 <= a.blocks; b += 32) {  // 32 loads in flight per round trip
+      unsigned c[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) c[j] = a.block_counts[(b + j) * a.experts + t];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        a.block_counts[(b + j) * a.experts + t] = run;
+        run += c[j];
+      }
+    }
+    for (; b + 8 <= a.blocks; b += 8) {
       unsigned c[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) c[j] = a.block_counts[(b + j) * a.experts + t];
@@ -95,8 +125,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RoutePlanArgs a) {
   }
   for (int64_t b = t; b < a.blocks; b += 1024) atomicAdd(&invalid_total, a.block_invalid[b]);
   __syncthreads();
-  block_scan_inclusive(route_cum, a.experts);
-  block_scan_inclusive(tile_cum, a.experts);
+  block_scan2_inclusive(route_cum, tile_cum, a.experts);
   if (t < a.experts) {
     a.route_offsets[t + 1] = route_cum[t];
     a.tile_offsets[t + 1] = tile_cum[t];
