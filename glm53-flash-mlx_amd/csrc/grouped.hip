@@ -919,7 +919,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
-  issue(0, 0);
+  // stage 0 was issued by wide_gemm_body, before the block scales
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
     stage_barrier<0>();  // stage kb landed; every wavefront is done reading the other slot
@@ -1007,16 +1007,6 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
     const int64_t route = start + (r < len ? r : len - 1);
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
-  load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_se);
-  const int64_t srows = (a.N + 127) / 128;
-  const int64_t s0 = MODE == GEMM_PLAIN ? 2 * ntile : ntile;
-  const int64_t s1 = MODE == GEMM_PLAIN ? (2 * ntile + 1 < srows ? 2 * ntile + 1 : srows - 1) : ntile;
-  const float* sc0 = src.scale + static_cast<int64_t>(expert) * a.s_expert_stride + s0 * a.s_cols;
-  const float* sc1 = (MODE == GEMM_PLAIN ? src.scale : src.scale_up) + static_cast<int64_t>(expert) * a.s_expert_stride +
-                     s1 * a.s_cols;
-  for (int64_t i = threadIdx.x; i < 2 * KB; i += 512) lds_sw[i] = i < KB ? sc0[i] : sc1[i - KB];
-  __syncthreads();
-
   // per-lane global sources of the direct loads: load h of a tile fills its
   // rows 8 h .. 8 h + 7, lane l reading row 8 h + l / 8
   auto b_row = [&](int t, int h) -> const uint8_t* {
@@ -1045,6 +1035,32 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
       ga[q][h] = plane + token_of(16 * wave + 8 * h + (lane >> 3)) * K + load_piece_offset(lane, h);
     }
   const bool loads_pair = wave < pairs;  // wave-uniform
+  // stage 0's direct loads fly while the block scales are gathered
+  {
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    const uint32_t sb = base + 2 * wave * kOperand;
+    lds_direct16(gb[0][0], sb);
+    lds_direct16(gb[0][1], sb + 1024);
+    lds_direct16(gb[1][0], sb + kOperand);
+    lds_direct16(gb[1][1], sb + kOperand + 1024);
+    if (loads_pair) {
+      const uint32_t sa = base + kWideStageB + 2 * wave * kOperand;
+      lds_direct16(ga[0][0], sa);
+      lds_direct16(ga[0][1], sa + 1024);
+      lds_direct16(ga[1][0], sa + kOperand);
+      lds_direct16(ga[1][1], sa + kOperand + 1024);
+    }
+  }
+  load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_se);
+  const int64_t srows = (a.N + 127) / 128;
+  const int64_t s0 = MODE == GEMM_PLAIN ? 2 * ntile : ntile;
+  const int64_t s1 = MODE == GEMM_PLAIN ? (2 * ntile + 1 < srows ? 2 * ntile + 1 : srows - 1) : ntile;
+  const float* sc0 = src.scale + static_cast<int64_t>(expert) * a.s_expert_stride + s0 * a.s_cols;
+  const float* sc1 = (MODE == GEMM_PLAIN ? src.scale : src.scale_up) + static_cast<int64_t>(expert) * a.s_expert_stride +
+                     s1 * a.s_cols;
+  for (int64_t i = threadIdx.x; i < 2 * KB; i += 512) lds_sw[i] = i < KB ? sc0[i] : sc1[i - KB];
+  __syncthreads();
+
   int np = (pairs - (wave >> 2) + 1) >> 1;  // pairs this wavefront multiplies: wr, wr + 2, ...
   np = np < 0 ? 0 : (np > 4 ? 4 : np);
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
