@@ -402,8 +402,8 @@ template <int GPW>
 constexpr int ring_stages() {
   return GPW == 1 ? 3 : 2;
 }
-// GPW 8-route groups per wavefront: descriptors of 32 GPW routes, 4 GPW
-// groups of activation rows per stage
+// Descriptors of 32 GPW routes: 2 GPW pairs of 16, i.e. 4 GPW activation
+// operand tiles (hi and lo rows of each pair) per stage
 template <int GPW>
 constexpr int stage_bytes() {
   return kStageB + 4 * GPW * kOperand;
