@@ -171,4 +171,91 @@ __device__ __forceinline__ uint16_t swiglu_mlx(float gate_acc, float up_acc, flo
   return swiglu_mlx_finish(ga, ua, sigmoid_mlx_bf16_fast(ga));
 }
 
+// swiglu_mlx as straight-line arithmetic on two values at once, for
+// epilogues that hold many values per lane.  Every BF16 rounding converts
+// both values with one v_cvt_pk_bf16_f32; the result holds value 0's bits
+// in its low half and value 1's in its high half.  Same bits as swiglu_mlx
+// for every input with 0 < L, |T(g)| <= 87, T(u) not NaN and T(g) != 0xC0DB:
+// `check` keeps the largest BF16 magnitudes of T(g) and T(u) and the smallest
+// XOR of T(g) with 0xC0DB, and when swiglu_straight_ok(check, L) is false the
+// caller recomputes its values with swiglu_mlx.  For such inputs the clamps
+// are v_min / v_med3 (no NaN operand; with 0 < L, +-0 stays itself), and the
+// sign select is a bit select (g' = -0 gives tail = upper = 0.5).
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Written as assembly: built as a two-element vector conversion, a pair of
+// accumulator elements became one 8-byte load that kept the accumulators in
+// scratch memory.  The compiler does not insert the wait state a VALU
+// instruction needs before it reads the result of a transcendental one
+// (v_exp_f32, v_rcp_f32) when the reader is inline assembly: the form for
+// such operands carries it.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_after_trans(float a, float b) {
+  uint32_t r;
+  asm("s_nop 0\n\tv_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float bf16x2_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16x2_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+struct SwigluCheck {
+  uint32_t mag = 0;           // max |T(g)| bits (low half), max |T(u)| bits (high half)
+  uint32_t key = 0xFFFFFFFFu;  // min T(g) ^ 0xC0DB (low half)
+};
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b)));
+}
+__device__ __forceinline__ uint32_t min_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b)));
+}
+
+// Written as assembly: on operands it cannot prove canonical the compiler
+// adds a canonicalising v_max before every min/max/med3, which these
+// operands (non-NaN whenever the result is used) do not need.
+__device__ __forceinline__ float min_f32(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float med3_f32(float a, float b, float c) {
+  float r;
+  asm("v_med3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// bits of t where the sign bit of x is set, of u elsewhere
+__device__ __forceinline__ float sign_select(float x, float t, float u) {
+  const uint32_t neg = static_cast<uint32_t>(static_cast<int32_t>(__float_as_uint(x)) >> 31);
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(neg), "v"(__float_as_uint(t)), "v"(__float_as_uint(u)));
+  return __uint_as_float(r);
+}
+
+__device__ __forceinline__ uint32_t swiglu_mlx_straight2(float gate0, float up0, float gate1, float up1, float limit,
+                                                         SwigluCheck& check) {
+  const uint32_t gu0 = f32x2_to_bf16x2(gate0, up0), gu1 = f32x2_to_bf16x2(gate1, up1);
+  check.mag = max_u16x2(check.mag, max_u16x2(gu0 & 0x7FFF7FFFu, gu1 & 0x7FFF7FFFu));
+  check.key = min_u16x2(check.key, min_u16x2(gu0 ^ 0xC0DBu, gu1 ^ 0xC0DBu));
+  // g' = T(min(T(g), L)) and u' = T(clip(T(u), -L, L)) of each value
+  const uint32_t p0 = f32x2_to_bf16x2(min_f32(bf16x2_lo(gu0), limit), med3_f32(bf16x2_hi(gu0), -limit, limit));
+  const uint32_t p1 = f32x2_to_bf16x2(min_f32(bf16x2_lo(gu1), limit), med3_f32(bf16x2_hi(gu1), -limit, limit));
+  const float g0 = bf16x2_lo(p0), u0 = bf16x2_hi(p0), g1 = bf16x2_lo(p1), u1 = bf16x2_hi(p1);
+  const uint32_t e = f32x2_to_bf16x2_after_trans(__expf(fabsf(g0)), __expf(fabsf(g1)));
+  const uint32_t d = f32x2_to_bf16x2(1.0f + bf16x2_lo(e), 1.0f + bf16x2_hi(e));
+  const uint32_t tail =
+      f32x2_to_bf16x2_after_trans(__builtin_amdgcn_rcpf(bf16x2_lo(d)), __builtin_amdgcn_rcpf(bf16x2_hi(d)));
+  const float t0 = bf16x2_lo(tail), t1 = bf16x2_hi(tail);
+  const uint32_t upper = f32x2_to_bf16x2(1.0f - t0, 1.0f - t1);
+  const float s0 = sign_select(g0, t0, bf16x2_lo(upper)), s1 = sign_select(g1, t1, bf16x2_hi(upper));
+  const uint32_t silu = f32x2_to_bf16x2(g0 * s0, g1 * s1);
+  return f32x2_to_bf16x2(bf16x2_lo(silu) * u0, bf16x2_hi(silu) * u1);
+}
+__device__ __forceinline__ bool swiglu_straight_ok(const SwigluCheck& c, float limit) {
+  // |T(g)| <= 87 (0x42AE), T(u) not NaN (<= 0x7F80), no 0xC0DB, 0 < L
+  return (c.mag & 0xFFFFu) <= 0x42AEu && (c.mag >> 16) <= 0x7F80u && (c.key & 0xFFFFu) != 0 && limit > 0.0f;
+}
+
 }  // namespace glm53

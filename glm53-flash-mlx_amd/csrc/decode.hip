@@ -504,13 +504,26 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(GenericLinearArgs a
 
 // packed.py:146-163 / grouped_fp8.py:265-270 elementwise SwiGLU on BF16
 // projections (gate row-block / up row-block with independent strides).
+// Each thread takes elements 2 t and 2 t + 1 (the last one twice when the
+// count is odd) through swiglu_mlx_straight2, the form of the grouped GEMM
+// epilogues, and recomputes them with swiglu_mlx where that form does not
+// apply, so this entry point pins that form on whatever inputs it is given.
 __global__ void swiglu_kernel(SwigluArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= a.rows * a.cols) return;
-  const int64_t r = i / a.cols, c = i % a.cols;
-  float g = bf16_to_f32(a.gate[r * a.gate_row_stride + c]);
-  float u = bf16_to_f32(a.up[r * a.up_row_stride + c]);
-  a.out[r * a.out_row_stride + c] = swiglu_mlx(g, u, a.limit);
+  const int64_t n = a.rows * a.cols;
+  const int64_t i0 = 2 * (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x);
+  if (i0 >= n) return;
+  const int64_t i1 = i0 + 1 < n ? i0 + 1 : i0;
+  const int64_t r0 = i0 / a.cols, c0 = i0 % a.cols, r1 = i1 / a.cols, c1 = i1 % a.cols;
+  const float g0 = bf16_to_f32(a.gate[r0 * a.gate_row_stride + c0]);
+  const float u0 = bf16_to_f32(a.up[r0 * a.up_row_stride + c0]);
+  const float g1 = bf16_to_f32(a.gate[r1 * a.gate_row_stride + c1]);
+  const float u1 = bf16_to_f32(a.up[r1 * a.up_row_stride + c1]);
+  SwigluCheck check;
+  uint32_t h = swiglu_mlx_straight2(g0, u0, g1, u1, a.limit, check);
+  if (!swiglu_straight_ok(check, a.limit))
+    h = swiglu_mlx(g0, u0, a.limit) | static_cast<uint32_t>(swiglu_mlx(g1, u1, a.limit)) << 16;
+  a.out[r0 * a.out_row_stride + c0] = static_cast<uint16_t>(h);
+  if (i1 != i0) a.out[r1 * a.out_row_stride + c1] = static_cast<uint16_t>(h >> 16);
 }
 
 // swiglu_mlx with every rounding point kept (the routed-stage diagnostic):
@@ -687,7 +700,7 @@ hipError_t launch_swiglu_stages(const SwigluArgs& a, uint16_t* sigma, uint16_t* 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t st) {
   int64_t n = a.rows * a.cols;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(static_cast<unsigned>(((n + 1) / 2 + 255) / 256)), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -515,30 +515,88 @@ struct ItemSource {
   int64_t out_row_stride;
 };
 
+// Stores a wavefront's BF16 results: v[j][t][i / 2] holds, in its low half
+// for even i and its high half for odd i, route 16 (p0 + pstep j) + 4 (l /
+// 16) + i of the item and output column c0 + 16 t + l % 16.  Buffer stores
+// against a record that ends after the item's len rows: a route past len
+// lies outside it, a column past N is given an offset outside it, and the
+// hardware drops both, so the stores need no branches.  (The host keeps
+// out_row_stride below 2^22, so every offset fits 32 bits.)
+template <int NP, int T>
+__device__ __forceinline__ void store_item_rows(const ItemSource& src, int32_t start, int32_t len, int p0, int pstep,
+                                                int64_t c0, int64_t N, const uint32_t (&v)[NP > 0 ? NP : 1][T][2],
+                                                int lane) {
+  const int n16 = lane & 15, kq = lane >> 4;
+  const uint32_t stride2 = 2u * static_cast<uint32_t>(src.out_row_stride);
+  const __amdgpu_buffer_rsrc_t rec = __builtin_amdgcn_make_buffer_rsrc(
+      src.out + static_cast<int64_t>(start) * src.out_row_stride, 0, static_cast<int>(stride2 * len), 0x00020000);
+  uint32_t coff[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t c = c0 + 16 * t + n16;
+    coff[t] = c < N ? 2u * static_cast<uint32_t>(c) : 0x80000000u;
+  }
+#pragma unroll
+  for (int j = 0; j < NP; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t roff = stride2 * static_cast<uint32_t>(16 * (p0 + pstep * j) + 4 * kq + i);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint16_t bits = static_cast<uint16_t>(i & 1 ? v[j][t][i >> 1] >> 16 : v[j][t][i >> 1]);
+        __builtin_amdgcn_raw_buffer_store_b16(bits, rec, static_cast<int>(roff + coff[t]), 0, 0);
+      }
+    }
+}
+
 // SWIGLU epilogue of a wavefront: pair j of the wavefront is descriptor
 // pair p0 + pstep j; lane l holds, for its routes 16 p + 4 (l / 16) + i,
 // gate tiles 0 .. T - 1 in acc[j][t] and the matching up tiles in
-// acc[j][t + T]; output column c0 + 16 t + l % 16.
+// acc[j][t + T]; output column c0 + 16 t + l % 16.  Every value takes the
+// straight-line form, two at a time; a wavefront with a value outside its
+// range (|T(g)| > 87, NaN or T(g) = 0xC0DB: rare) recomputes all of its
+// values with swiglu_mlx.
 template <int NP, int T>
 __device__ __forceinline__ void swiglu_epilogue(const GroupedGemmArgs& a, const ItemSource& src, int32_t start,
                                                 int32_t len, int p0, int pstep, int64_t c0,
                                                 const float (&acc)[NP > 0 ? NP : 1][2 * T][4], int lane) {
-  const int n16 = lane & 15, kq = lane >> 4;
+  uint32_t h[NP > 0 ? NP : 1][T][2];
+  SwigluCheck check;
 #pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    const int p = p0 + pstep * j;
+  for (int j = 0; j < NP; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = p * 16 + 4 * kq + i;
-      if (r >= len) continue;
-      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const int64_t c = c0 + 16 * t + n16;
-        if (c < a.N) orow[c] = swiglu_mlx(acc[j][t][i], acc[j][t + T][i], a.limit);
-      }
-    }
+      for (int q = 0; q < 2; ++q)
+        h[j][t][q] = swiglu_mlx_straight2(acc[j][t][2 * q], acc[j][t + T][2 * q], acc[j][t][2 * q + 1],
+                                          acc[j][t + T][2 * q + 1], a.limit, check);
+  if (__builtin_amdgcn_ballot_w64(!swiglu_straight_ok(check, a.limit)) != 0) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          h[j][t][q] = swiglu_mlx(acc[j][t][2 * q], acc[j][t + T][2 * q], a.limit) |
+                       static_cast<uint32_t>(swiglu_mlx(acc[j][t][2 * q + 1], acc[j][t + T][2 * q + 1], a.limit)) << 16;
   }
+  store_item_rows<NP, T>(src, start, len, p0, pstep, c0, a.N, h, lane);
+}
+
+// PLAIN epilogue of a wavefront: acc[j][t] holds output columns c0 + 16 t
+// + l % 16 of routes 16 (p0 + pstep j) + 4 (l / 16) + i, stored as BF16.
+template <int NP, int T>
+__device__ __forceinline__ void plain_epilogue(const GroupedGemmArgs& a, const ItemSource& src, int32_t start,
+                                               int32_t len, int p0, int pstep, int64_t c0,
+                                               const float (&acc)[NP > 0 ? NP : 1][T][4], int lane) {
+  uint32_t h[NP > 0 ? NP : 1][T][2];
+#pragma unroll
+  for (int j = 0; j < NP; ++j)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) h[j][t][q] = f32x2_to_bf16x2(acc[j][t][2 * q], acc[j][t][2 * q + 1]);
+  store_item_rows<NP, T>(src, start, len, p0, pstep, c0, a.N, h, lane);
 }
 
 // Wavefront w's share of a work item: it loads weight tiles 2 w, 2 w + 1 and
@@ -561,7 +619,6 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
   constexpr int T = GPW == 2 ? 8 : 4;         // weight tiles it multiplies
   const int pair = GPW == 2 ? wave : wave >> 1;
   const int half = wave & 1;
-  const int kq = lane >> 4;
   const OperandSlots slots = operand_slots(lane);
   auto issue = [&](int64_t kb, int slot) {
     const int64_t ko = kb * kBlock;
@@ -637,20 +694,9 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
   }
 
   // epilogue: lane holds routes 16 pair + 4 kq + i, column 16 tile + l % 16
-  if (NP > 0 && MODE == GEMM_PLAIN) {
-    const int n16 = lane & 15;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = pair * 16 + 4 * kq + i;
-      if (r >= len) continue;
-      uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
-#pragma unroll
-      for (int tt = 0; tt < T; ++tt) {
-        const int64_t c = ntile * kTileRows + tile_of(tt) * 16 + n16;
-        if (c < a.N) orow[c] = f32_to_bf16(acc[0][tt][i]);
-      }
-    }
-  }
+  // (PLAIN: the wavefront's tiles tile_of(tt) are contiguous from tile_of(0))
+  if (MODE == GEMM_PLAIN)
+    plain_epilogue<NP, T>(a, src, start, len, pair, 1, ntile * kTileRows + tile_of(0) * 16, acc, lane);
   if (MODE == GEMM_SWIGLU)
     swiglu_epilogue<NP, T / 2>(a, src, start, len, pair, 1, ntile * (kTileRows / 2) + (GPW == 2 ? 0 : 32 * half), acc,
                                lane);
@@ -661,8 +707,11 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
 // [kb][wr][r % 16][j] with r = 16 (wr + 2 j) + r % 16, so that a wavefront
 // of row wr reads the codes of its four pairs as one word.  THREADS / ROUTES
 // threads per route, each with its route's token row, eight loads in
-// flight per thread (indices clamped so that every load is unconditional),
-// then the stores.  Routes past the descriptor's end repeat its last route.
+// flight per thread, then the stores; indices past the last K block are
+// clamped to it, so every load and store is unconditional (a clamped store
+// writes the code that block's store writes) and the compiler's wait
+// tracking sees every load consumed before the K loop.  Routes past the
+// descriptor's end repeat its last route.
 template <int ROUTES, int THREADS, bool WIDE>
 __device__ __forceinline__ void load_activation_scales(const ItemSource& src, int32_t start, int32_t len,
                                                        int64_t KB, uint8_t* lds_se) {
@@ -684,7 +733,7 @@ __device__ __forceinline__ void load_activation_scales(const ItemSource& src, in
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int64_t kb = kb0 + u * TPR;
-      if (kb < KB) lds_se[kb * kStride + pos] = static_cast<uint8_t>(scale_e8m0(v[u]));
+      lds_se[(kb < KB ? kb : KB - 1) * kStride + pos] = static_cast<uint8_t>(scale_e8m0(v[u]));
     }
   }
 }
@@ -891,7 +940,6 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
                                                bool loads_pair, uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
                                                const float* lds_sw, int wave, int lane) {
   const int wr = wave >> 2, wc = wave & 3;
-  const int kq = lane >> 4;
   const OperandSlots slots = operand_slots(lane);
   auto issue = [&](int64_t kb, int slot) {
     const int64_t ko = kb * kBlock;
@@ -970,22 +1018,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 
   // epilogue: lane holds columns 16 tile + l % 16 of routes 16 p + 4 kq + i
   if (MODE == GEMM_PLAIN) {
-    const int n16 = lane & 15;
-#pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      const int pp = wr + 2 * j;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = pp * 16 + 4 * kq + i;
-        if (r >= len) continue;
-        uint16_t* orow = src.out + (static_cast<int64_t>(start) + r) * src.out_row_stride;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const int64_t col = ntile * 256 + 16 * (4 * wc + tt) + n16;
-          if (col < a.N) orow[col] = f32_to_bf16(acc[j][tt][i]);
-        }
-      }
-    }
+    plain_epilogue<NP, 4>(a, src, start, len, wr, 2, ntile * 256 + 64 * wc, acc, lane);
   } else {
     swiglu_epilogue<NP, 2>(a, src, start, len, wr, 2, ntile * 128 + 32 * wc, acc, lane);
   }
@@ -1278,6 +1311,10 @@ hipError_t launch_split_activations(const SplitArgs& a, hipStream_t st) {
 
 hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descriptors, hipStream_t st) {
   if (descriptors == 0 && a.x_descriptors == 0) return hipSuccess;
+  // the epilogues' buffer stores take 32-bit offsets of up to 128 rows
+  if (a.out_row_stride < a.N || a.out_row_stride >= (int64_t{1} << 22) ||
+      (a.x_descriptors > 0 && (a.x_out_row_stride < a.N || a.x_out_row_stride >= (int64_t{1} << 22))))
+    return hipErrorInvalidValue;
   if (a.tile_rows == kGemmWideRows) {
     GroupedGemmArgs g = a;
     g.n_tiles = mode == GEMM_PLAIN ? (a.N + 255) / 256 : (a.N + 127) / 128;

@@ -186,3 +186,30 @@ def test_swiglu_bit_exact_against_oracle(M, O, dev):
     for limit in (10.0, 3.0, 20.0):
         got = to_bits(M.swiglu(from_bits(gate, dev), from_bits(up, dev), limit))
         assert np.array_equal(got, O.swiglu(gate, up, limit)), limit
+
+
+def test_swiglu_every_gate_pattern_matches_oracle(M, O, dev):
+    """The straight-line SwiGLU (two values per conversion, the form of the
+    grouped GEMM epilogues) with its fall-back to the exact sequence, over
+    all 65,536 BF16 gate patterns (NaN, +-inf, |g| > 87 and 0xC0DB included)
+    against up values with +-0, +-inf, NaN and values past the clamp: equal
+    to the oracle bit for bit wherever the oracle's result is not NaN, NaN
+    where it is."""
+    rng = np.random.default_rng(12)
+    gate = np.arange(1 << 16, dtype=np.uint16)
+    up = O.f32_to_bf16(rng.normal(scale=12.0, size=gate.size).astype(np.float32))
+    special = np.array([0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x3F80, 0xBF80, 0x4120, 0xC120],
+                       dtype=np.uint16)
+    pick = rng.choice(gate.size, size=4096, replace=False)
+    up[pick] = special[rng.integers(0, special.size, size=pick.size)]
+    # an odd count: the last value is paired with itself
+    gate, up = gate[:-1], up[:-1]
+    for limit in (7.0, 10.0, float("inf")):
+        got = to_bits(M.swiglu(from_bits(gate, dev), from_bits(up, dev), limit))
+        want = O.swiglu(gate, up, limit)
+        nan_want = (want & 0x7F80) == 0x7F80
+        nan_want &= (want & 0x007F) != 0
+        bad = np.flatnonzero(~nan_want & (got != want))
+        assert bad.size == 0, (limit, [(hex(int(gate[i])), hex(int(up[i])), hex(int(got[i])), hex(int(want[i])))
+                                       for i in bad[:8]])
+        assert ((got[nan_want] & 0x7F80) == 0x7F80).all() and (got[nan_want] & 0x007F).all(), limit
