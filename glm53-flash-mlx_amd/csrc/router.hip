@@ -29,6 +29,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTileTokens = 128;
 constexpr int kTileExperts = 96;
@@ -47,8 +48,8 @@ constexpr int kAhead = GLM53_ROUTER_AHEAD;       // steps of global loads in fli
 __device__ __forceinline__ int slot_offset(int r, int q) { return r * kRowBytes + 16 * (q ^ ((r >> 2) & 3)); }
 
 // The three BF16 parts of four FP32 weights, packed two per word.
-__device__ __forceinline__ void split3(const float4& v, uint2& hi, uint2& mid, uint2& lo) {
-  const float in[4] = {v.x, v.y, v.z, v.w};
+__device__ __forceinline__ void split3(const f32x4_t& v, uint2& hi, uint2& mid, uint2& lo) {
+  const float in[4] = {v[0], v[1], v[2], v[3]};
   uint32_t h[4], m[4], l[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -67,9 +68,13 @@ __device__ __forceinline__ void split3(const float4& v, uint2& hi, uint2& mid, u
 
 // One step's global operands held by a thread: token rows (two 16-byte BF16
 // octets) and expert rows (three 16-byte FP32 quads).
+// ext_vector_type members: with HIP's uint4 / float4 the register copies
+// became memcpy's that kept the prefetched activations in scratch memory,
+// each written there right after its load was issued (that is, after
+// waiting for it), and the many-token router ran ~10% longer.
 struct StepRegs {
-  uint4 x[2];
-  float4 w[3];
+  u32x4_t x[2];
+  f32x4_t w[3];
 };
 
 __global__ __launch_bounds__(256, 2) void router_tile_kernel(RouterGemmArgs a, const float* __restrict__ weight) {
@@ -106,14 +111,14 @@ __global__ __launch_bounds__(256, 2) void router_tile_kernel(RouterGemmArgs a, c
     wsrc[j] = weight + (e < a.experts ? e : a.experts - 1) * H + 4 * wq[j];
   }
   auto load = [&](StepRegs& r, int64_t k) {
-    r.x[0] = *reinterpret_cast<const uint4*>(xsrc + k);
-    r.x[1] = *reinterpret_cast<const uint4*>(xsrc + k + 8);
+    r.x[0] = *reinterpret_cast<const u32x4_t*>(xsrc + k);
+    r.x[1] = *reinterpret_cast<const u32x4_t*>(xsrc + k + 8);
 #pragma unroll
-    for (int j = 0; j < 3; ++j) r.w[j] = *reinterpret_cast<const float4*>(wsrc[j] + k);
+    for (int j = 0; j < 3; ++j) r.w[j] = *reinterpret_cast<const f32x4_t*>(wsrc[j] + k);
   };
   auto store = [&](const StepRegs& r, uint8_t* stage) {
-    *reinterpret_cast<uint4*>(stage + slot_offset(xr, xq)) = r.x[0];
-    *reinterpret_cast<uint4*>(stage + slot_offset(xr, xq + 1)) = r.x[1];
+    *reinterpret_cast<u32x4_t*>(stage + slot_offset(xr, xq)) = r.x[0];
+    *reinterpret_cast<u32x4_t*>(stage + slot_offset(xr, xq + 1)) = r.x[1];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       uint2 hi, mid, lo;
