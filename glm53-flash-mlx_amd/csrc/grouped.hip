@@ -906,127 +906,168 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
 // ------------------------------------------ grouped GEMM, wide shape --
 //
 // For plans whose experts carry many routes: work item = one 128-route
-// descriptor (8 pairs of 16 routes) x 256 weight rows (PLAIN: 256 output
-// columns; SWIGLU: 128 gate rows and the matching 128 up rows), one
-// 512-thread workgroup per CU (8 wavefronts, two per SIMD; the 2-stage ring
-// of 64 KB stages takes 128 KB of LDS).  Against the 64-route x 128-row
-// item a weight tile streams once per 128 routes instead of 64 and an
-// activation row once per 256 weight rows instead of 128.  Wavefront w =
-// 4 wr + wc multiplies pairs wr, wr + 2, wr + 4, wr + 6 against four 16-row
-// weight tiles (PLAIN: tiles 4 wc .. 4 wc + 3; SWIGLU: gate tiles 2 wc,
-// 2 wc + 1 and up tiles 8 + 2 wc, 9 + 2 wc): the four B operands stay in
-// registers for the stage and each pair's hi and lo rows stream through
-// them, 32 MFMAs per stage from 12 operand reads.  Each wavefront issues
-// the direct loads of weight tiles 2 w, 2 w + 1 and of pair w's hi and lo
-// tiles (none when the pair holds no routes).  The arithmetic per output
-// element is that of the narrower shapes, so every shape gives the same
-// bits.
+// descriptor (8 pairs of 16 routes) x 384 weight rows (PLAIN: 384 output
+// columns; SWIGLU: 192 gate rows and the matching 192 up rows), one
+// 512-thread workgroup per CU (8 wavefronts, two per SIMD).  Against the
+// 64-route x 128-row item a heavy expert's weight tile streams once per 128
+// routes instead of 64 and an activation row once per 384 weight rows
+// instead of 128.  Wavefront w = 4 wr + wc multiplies pairs wr, wr + 2,
+// wr + 4, wr + 6 against six 16-row weight tiles (PLAIN: tiles 6 wc .. 6 wc
+// + 5; SWIGLU: gate tiles 3 wc .. 3 wc + 2 and up tiles 12 + 3 wc .. 12 + 3
+// wc + 2): per stage 12 KB of B and 16 KB of A operand reads for 48 MFMAs.
+// The LDS holds one B stage (24 tiles, 48 KB) and a 2-stage A ring (2 x 32
+// KB): each wavefront reads its six B tiles into registers at the start of
+// a stage, a second barrier then frees the B buffer and the next stage's
+// weight tiles stream into it behind this stage's MFMAs.  Each wavefront
+// issues the direct loads of weight tiles 3 w .. 3 w + 2 and of pair w's hi
+// and lo tiles (none when the pair holds no routes).  The arithmetic per
+// output element is that of the narrower shapes, so every shape gives the
+// same bits.
 namespace {
-constexpr int kWidePairs = kGemmWideRows / 16;                          // 8
-constexpr int kWideTiles = 16;                                          // 16-row weight tiles: 256 rows
-constexpr int kWideStageB = kWideTiles * kOperand;                      // 32 KB
-constexpr int kWideStage = kWideStageB + 2 * kWidePairs * kOperand;     // 64 KB
+constexpr int kWidePairs = kGemmWideRows / 16;            // 8
+constexpr int kWideTilesPerWave = 6;                      // weight tiles per wavefront
+constexpr int kWideBTiles = 4 * kWideTilesPerWave;        // 24 tiles: 384 rows
+constexpr int kWideBBytes = kWideBTiles * kOperand;       // 48 KB
+constexpr int kWideABytes = 2 * kWidePairs * kOperand;    // 32 KB per A stage
+constexpr int kWidePlainRows = kWideBTiles * 16;          // 384
+constexpr int kWideGateRows = kWidePlainRows / 2;         // 192
 }  // namespace
 
 size_t gemm_wide_lds_bytes(int64_t K) {
-  // 2-stage ring, activation scale codes [KB][128 routes], weight scales [2][KB]
-  return 2 * static_cast<size_t>(kWideStage) + (kGemmWideRows + 2 * sizeof(float)) * static_cast<size_t>(K / kBlock);
+  // B stage, 2-stage A ring, activation scale codes [KB][128 routes],
+  // weight scales [4][KB]
+  return static_cast<size_t>(kWideBBytes + 2 * kWideABytes) +
+         (kGemmWideRows + 4 * sizeof(float)) * static_cast<size_t>(K / kBlock);
 }
+
+// Direct-load sources of a wavefront, formed per load from few registers:
+// its three weight tiles' rows come from one matrix (wmat, wave-uniform)
+// starting at row row0 + 8 h + l / 8 (+ 16 q for tile q, clamped to the
+// last row), its pair's hi / lo rows from token rows tok[h].
+struct WideSources {
+  const uint8_t* wmat;     // the expert's gate, up or plain matrix
+  const uint8_t* a_hi;
+  const uint8_t* a_lo;
+  int64_t K;
+  int32_t rows;            // rows of the matrix (loads past it re-read the last row)
+  int32_t row0;            // first row of the wavefront's tiles, + lane / 8
+  int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 64)
+  int32_t tok[2];          // token rows of the pair's rows 8 h + lane / 8
+};
 
 template <int MODE, bool FIX, int NP>
 __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
-                                               int32_t start, int32_t len, int64_t KB,
-                                               const uint8_t* const (&gb)[2][2], const uint8_t* const (&ga)[2][2],
-                                               bool loads_pair, uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
-                                               const float* lds_sw, int wave, int lane) {
+                                                int32_t start, int32_t len, int64_t KB, const WideSources& ls,
+                                                bool loads_pair, uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
+                                                const float* lds_sw, int wave, int lane) {
   const int wr = wave >> 2, wc = wave & 3;
   const OperandSlots slots = operand_slots(lane);
-  auto issue = [&](int64_t kb, int slot) {
-    const int64_t ko = kb * kBlock;
-    const uint32_t sb = lds_addr + slot * kWideStage + 2 * wave * kOperand;
-    lds_direct16(gb[0][0] + ko, sb);
-    lds_direct16(gb[0][1] + ko, sb + 1024);
-    lds_direct16(gb[1][0] + ko, sb + kOperand);
-    lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
+  auto issue_b = [&](int64_t kb) {
+    const uint32_t sb = lds_addr + 3 * wave * kOperand;
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int32_t row = ls.row0 + 16 * q + 8 * h;
+        row = row < ls.rows ? row : ls.rows - 1;
+        lds_direct16(ls.wmat + static_cast<int64_t>(row) * ls.K + kb * kBlock + (ls.piece ^ (64 * h)),
+                     sb + q * kOperand + 1024 * h);
+      }
+  };
+  auto issue_a = [&](int64_t kb, int slot) {
     if (loads_pair) {
-      const uint32_t sa = lds_addr + slot * kWideStage + kWideStageB + 2 * wave * kOperand;
-      lds_direct16(ga[0][0] + ko, sa);
-      lds_direct16(ga[0][1] + ko, sa + 1024);
-      lds_direct16(ga[1][0] + ko, sa + kOperand);
-      lds_direct16(ga[1][1] + ko, sa + kOperand + 1024);
+      const uint32_t sa = lds_addr + kWideBBytes + slot * kWideABytes + 2 * wave * kOperand;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t off = static_cast<int64_t>(ls.tok[h]) * ls.K + kb * kBlock + (ls.piece ^ (64 * h));
+        lds_direct16(ls.a_hi + off, sa + 1024 * h);
+        lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
+      }
     }
   };
-  // the LDS tile of the wavefront's weight tile tt (0..3)
-  auto tile_of = [&](int tt) { return MODE == GEMM_PLAIN ? 4 * wc + tt : (tt < 2 ? 2 * wc + tt : 8 + 2 * wc + tt - 2); };
+  // the LDS tile of the wavefront's weight tile tt (0..5) and the weight
+  // scale row (of lds_sw) its rows lie in
+  auto tile_of = [&](int tt) {
+    return MODE == GEMM_PLAIN ? kWideTilesPerWave * wc + tt : (tt < 3 ? 3 * wc + tt : 12 + 3 * wc + tt - 3);
+  };
+  auto sw_row = [&](int tt) -> int {
+    if (MODE == GEMM_PLAIN) return (kWideTilesPerWave * wc + tt) >> 3;
+    const int g = 3 * wc + (tt < 3 ? tt : tt - 3);                   // gate tile of the output columns
+    const int rb = (64 * static_cast<int>(ntile & 1) + 16 * g) >> 7;  // its 128-row block in the item's first
+    return (tt < 3 ? 0 : 2) + rb;
+  };
 
-  float acc[NP > 0 ? NP : 1][4][4];
+  float acc[NP > 0 ? NP : 1][kWideTilesPerWave][4];
 #pragma unroll
   for (int j = 0; j < NP; ++j)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < kWideTilesPerWave; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
-  // stage 0 was issued by wide_gemm_body, before the block scales
+  // stage 0 (B and A) was issued by wide_gemm_body, before the block scales
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
-    stage_barrier<0>();  // stage kb landed; every wavefront is done reading the other slot
-    if (kb + 1 < KB) issue(kb + 1, slot ^ 1);
+    stage_barrier<0>();  // stage kb landed; every wavefront is done with stage kb - 1
+    if (kb + 1 < KB) issue_a(kb + 1, slot ^ 1);
+    i32x8 bq[kWideTilesPerWave];
+    float sw[kWideTilesPerWave];
+    int se = 0;
     if (NP > 0) {
-      const uint8_t* st = lds + slot * kWideStage;
-      // the wavefront's four weight tiles stay in registers for the stage;
-      // its pairs' hi and lo rows stream through them
-      i32x8 bq[4], bc[4];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        bq[tt] = lds_operand(st + tile_of(tt) * kOperand, slots);
-        weight_operand<FIX>(bq[tt], bc[tt]);
+      for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
+        bq[tt] = lds_operand(lds + tile_of(tt) * kOperand, slots);
+        sw[tt] = lds_sw[sw_row(tt) * KB + kb];
       }
-      const float sw0 = lds_sw[kb], sw1 = lds_sw[KB + kb];
-      // PLAIN: the wavefront's four tiles lie in one 128-row scale block;
-      // SWIGLU: tiles 0-1 are gate rows, 2-3 up rows
-      auto sw_of = [&](int tt) { return MODE == GEMM_PLAIN ? (wc >> 1 ? sw1 : sw0) : (tt < 2 ? sw0 : sw1); };
       // byte j: the E8M0 scale of this lane's route in pair wr + 2 j
-      const int se = *reinterpret_cast<const int*>(lds_se + kb * kGemmWideRows + (wr * 16 + (lane & 15)) * 4);
-      f32x4 c[4];
-      // c[tt] of pair j - 1 is folded just before pair j's hi pass on tile
-      // tt overwrites it (4 MFMAs after it was issued); each lo pass reads
-      // the hi pass issued 4 MFMAs before it
+      se = *reinterpret_cast<const int*>(lds_se + kb * kGemmWideRows + (wr * 16 + (lane & 15)) * 4);
+    }
+    // every wavefront holds its B operands: the B buffer takes the next stage
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kb + 1 < KB) issue_b(kb + 1);
+    if (NP > 0) {
+      const uint8_t* st = lds + kWideBBytes + slot * kWideABytes;
+      f32x4 c[kWideTilesPerWave];
       auto fold = [&](int j, int tt) {
-        const float sw = sw_of(tt);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[j][tt][i] = fmaf(c[tt][i], sw, acc[j][tt][i]);
+        for (int i = 0; i < 4; ++i) acc[j][tt][i] = fmaf(c[tt][i], sw[tt], acc[j][tt][i]);
       };
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
         const int pp = wr + 2 * j;
-        const i32x8 ahi = lds_operand(st + kWideStageB + (2 * pp) * kOperand, slots);
-        const i32x8 alo = lds_operand(st + kWideStageB + (2 * pp + 1) * kOperand, slots);
+        const i32x8 ahi = lds_operand(st + (2 * pp) * kOperand, slots);
+        const i32x8 alo = lds_operand(st + (2 * pp + 1) * kOperand, slots);
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
           if (j > 0) fold(j - 1, tt);
-          c[tt] = pair_pass_byte<FIX, 127>(j, ahi, bq[tt], bc[tt], (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
+          i32x8 b = bq[tt], bc;
+          weight_operand<FIX>(b, bc);
+          c[tt] = pair_pass_byte<FIX, 127>(j, ahi, b, bc, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
         }
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) c[tt] = pair_pass_byte<FIX, 123>(j, alo, bq[tt], bc[tt], c[tt], se);
+        for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
+          i32x8 b = bq[tt], bc;
+          weight_operand<FIX>(b, bc);
+          c[tt] = pair_pass_byte<FIX, 123>(j, alo, b, bc, c[tt], se);
+        }
       }
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) fold(NP - 1, tt);
+      for (int tt = 0; tt < kWideTilesPerWave; ++tt) fold(NP - 1, tt);
     }
     slot ^= 1;
   }
 
   // epilogue: lane holds columns 16 tile + l % 16 of routes 16 p + 4 kq + i
   if (MODE == GEMM_PLAIN) {
-    plain_epilogue<NP, 4>(a, src, start, len, wr, 2, ntile * 256 + 64 * wc, acc, lane);
+    plain_epilogue<NP, kWideTilesPerWave>(a, src, start, len, wr, 2, ntile * kWidePlainRows + 16 * kWideTilesPerWave * wc, acc, lane);
   } else {
-    swiglu_epilogue<NP, 2>(a, src, start, len, wr, 2, ntile * 128 + 32 * wc, acc, lane);
+    swiglu_epilogue<NP, kWideTilesPerWave / 2>(a, src, start, len, wr, 2, ntile * kWideGateRows + 48 * wc, acc, lane);
   }
 }
 
 template <int MODE, bool FIX>
 __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
-                                               int64_t d, uint8_t* lds) {
+                                                int64_t d, uint8_t* lds) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int32_t expert, start, len;
@@ -1034,75 +1075,75 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
   const int pairs = (len + 15) >> 4;
-  uint8_t* lds_se = lds + 2 * kWideStage;                                   // [KB][128]
-  float* lds_sw = reinterpret_cast<float*>(lds_se + kGemmWideRows * KB);    // [2][KB]
+  uint8_t* lds_se = lds + kWideBBytes + 2 * kWideABytes;                        // [KB][128]
+  float* lds_sw = reinterpret_cast<float*>(lds_se + kGemmWideRows * KB);    // [4][KB]
   auto token_of = [&](int r) -> int64_t {
     const int64_t route = start + (r < len ? r : len - 1);
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
-  // per-lane global sources of the direct loads: load h of a tile fills its
-  // rows 8 h .. 8 h + 7, lane l reading row 8 h + l / 8
-  auto b_row = [&](int t, int h) -> const uint8_t* {
-    const int rr = 8 * h + (lane >> 3);
-    int64_t row;
-    const uint8_t* w;
-    if (MODE == GEMM_PLAIN) {
-      row = ntile * 256 + t * 16 + rr;
-      w = src.weight;
-    } else {
-      row = ntile * 128 + (t & 7) * 16 + rr;
-      w = t < 8 ? src.weight : src.weight_up;
-    }
-    if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
-    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + load_piece_offset(lane, h);
-  };
-  const uint8_t* gb[2][2];
-  const uint8_t* ga[2][2];
+  // direct-load sources: load h of a weight tile fills its rows 8 h .. 8 h
+  // + 7, lane l reading row r = 8 h + l / 8 at piece (l % 8) ^ ((r >> 1) &
+  // 7), i.e. the h = 0 offset with bit 2 of the piece flipped for h = 1;
+  // the wavefront's tiles 3 w .. 3 w + 2 lie in one matrix
+  WideSources ls;
+  {
+    const bool up = MODE == GEMM_SWIGLU && wave >= 4;
+    ls.wmat = (up ? src.weight_up : src.weight) + static_cast<int64_t>(expert) * a.w_expert_stride;
+    const int t0 = MODE == GEMM_PLAIN ? 3 * wave : 3 * (wave & 3);
+    ls.row0 = static_cast<int32_t>(ntile * (MODE == GEMM_PLAIN ? kWidePlainRows : kWideGateRows)) + 16 * t0 + (lane >> 3);
+    ls.rows = static_cast<int32_t>(a.N);
+    ls.K = K;
+    ls.piece = load_piece_offset(lane, 0);
+    ls.a_hi = src.a_hi;
+    ls.a_lo = src.a_lo;
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      gb[q][h] = b_row(2 * wave + q, h);
-      // pair `wave`: hi rows (q = 0) or lo rows (q = 1); row rho is route 16 wave + rho
-      const uint8_t* plane = q ? src.a_lo : src.a_hi;
-      ga[q][h] = plane + token_of(16 * wave + 8 * h + (lane >> 3)) * K + load_piece_offset(lane, h);
-    }
+    for (int h = 0; h < 2; ++h) ls.tok[h] = static_cast<int32_t>(token_of(16 * wave + 8 * h + (lane >> 3)));
+  }
   const bool loads_pair = wave < pairs;  // wave-uniform
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   // stage 0's direct loads fly while the block scales are gathered
   {
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    const uint32_t sb = base + 2 * wave * kOperand;
-    lds_direct16(gb[0][0], sb);
-    lds_direct16(gb[0][1], sb + 1024);
-    lds_direct16(gb[1][0], sb + kOperand);
-    lds_direct16(gb[1][1], sb + kOperand + 1024);
+    const uint32_t sb = lds_addr + 3 * wave * kOperand;
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int32_t row = ls.row0 + 16 * q + 8 * h;
+        row = row < ls.rows ? row : ls.rows - 1;
+        lds_direct16(ls.wmat + static_cast<int64_t>(row) * K + (ls.piece ^ (64 * h)), sb + q * kOperand + 1024 * h);
+      }
     if (loads_pair) {
-      const uint32_t sa = base + kWideStageB + 2 * wave * kOperand;
-      lds_direct16(ga[0][0], sa);
-      lds_direct16(ga[0][1], sa + 1024);
-      lds_direct16(ga[1][0], sa + kOperand);
-      lds_direct16(ga[1][1], sa + kOperand + 1024);
+      const uint32_t sa = lds_addr + kWideBBytes + 2 * wave * kOperand;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t off = static_cast<int64_t>(ls.tok[h]) * K + (ls.piece ^ (64 * h));
+        lds_direct16(ls.a_hi + off, sa + 1024 * h);
+        lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
+      }
     }
   }
   load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_se);
+  // weight scale rows: PLAIN the item's three 128-row blocks; SWIGLU the
+  // (at most two) blocks its 192 gate rows span, then the same up blocks
   const int64_t srows = (a.N + 127) / 128;
-  const int64_t s0 = MODE == GEMM_PLAIN ? 2 * ntile : ntile;
-  const int64_t s1 = MODE == GEMM_PLAIN ? (2 * ntile + 1 < srows ? 2 * ntile + 1 : srows - 1) : ntile;
-  const float* sc0 = src.scale + static_cast<int64_t>(expert) * a.s_expert_stride + s0 * a.s_cols;
-  const float* sc1 = (MODE == GEMM_PLAIN ? src.scale : src.scale_up) + static_cast<int64_t>(expert) * a.s_expert_stride +
-                     s1 * a.s_cols;
-  for (int64_t i = threadIdx.x; i < 2 * KB; i += 512) lds_sw[i] = i < KB ? sc0[i] : sc1[i - KB];
+  const int64_t b0 = MODE == GEMM_PLAIN ? 3 * ntile : (ntile * kWideGateRows) >> 7;
+  for (int64_t i = threadIdx.x; i < 4 * KB; i += 512) {
+    const int64_t r = i / KB, k = i - r * KB;
+    int64_t blk = b0 + (MODE == GEMM_PLAIN ? r : (r & 1));
+    blk = blk < srows ? blk : srows - 1;
+    const float* sc = (MODE == GEMM_SWIGLU && r >= 2) ? src.scale_up : src.scale;
+    lds_sw[i] = sc[static_cast<int64_t>(expert) * a.s_expert_stride + blk * a.s_cols + k];
+  }
   __syncthreads();
 
   int np = (pairs - (wave >> 2) + 1) >> 1;  // pairs this wavefront multiplies: wr, wr + 2, ...
   np = np < 0 ? 0 : (np > 4 ? 4 : np);
-  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
 #define GLM53_WIDE(n) \
-  wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, gb, ga, loads_pair, lds, lds_addr, lds_se, lds_sw, wave, lane)
+  wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, ls, loads_pair, lds, lds_addr, lds_se, lds_sw, wave, lane)
   // pairs past the descriptor's routes hold stale activations: their
   // products are computed when np rounds up, and never stored
   if (np == 0) GLM53_WIDE(0);
-  else if (FIX || np > 2) GLM53_WIDE(4);
+  else if (np > 2) GLM53_WIDE(4);
   else if (np == 2) GLM53_WIDE(2);
   else GLM53_WIDE(1);
 #undef GLM53_WIDE
@@ -1317,7 +1358,7 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descr
     return hipErrorInvalidValue;
   if (a.tile_rows == kGemmWideRows) {
     GroupedGemmArgs g = a;
-    g.n_tiles = mode == GEMM_PLAIN ? (a.N + 255) / 256 : (a.N + 127) / 128;
+    g.n_tiles = mode == GEMM_PLAIN ? (a.N + kWidePlainRows - 1) / kWidePlainRows : (a.N + kWideGateRows - 1) / kWideGateRows;
     g.descriptors = descriptors;
     const int64_t items = g.n_tiles * (descriptors + g.x_descriptors);
     const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
