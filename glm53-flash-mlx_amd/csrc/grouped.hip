@@ -1140,10 +1140,11 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   np = np < 0 ? 0 : (np > 4 ? 4 : np);
 #define GLM53_WIDE(n) \
   wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, ls, loads_pair, lds, lds_addr, lds_se, lds_sw, wave, lane)
-  // pairs past the descriptor's routes hold stale activations: their
-  // products are computed when np rounds up, and never stored
+  // rows past the descriptor's routes (in its last pair) hold stale
+  // activations: their products are never stored
   if (np == 0) GLM53_WIDE(0);
-  else if (np > 2) GLM53_WIDE(4);
+  else if (np > 3) GLM53_WIDE(4);
+  else if (np == 3) GLM53_WIDE(3);
   else if (np == 2) GLM53_WIDE(2);
   else GLM53_WIDE(1);
 #undef GLM53_WIDE
