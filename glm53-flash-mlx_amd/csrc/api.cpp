@@ -1324,12 +1324,15 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   };
   size_t o_xf = take(router_space_bytes(T, experts)), o_logits = take(4 * T * experts), o_ids = take(4 * R),
          o_scores = take(4 * R);
-  size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(R, intermediate)), o_sq = take(split_bytes(T, Ism));
+  // a shared expert of the routed width keeps its hidden rows right after
+  // the routed ones (h and hq), so that one split launch covers both
+  const int64_t RH = shared_intermediate == intermediate ? R + T : R;
+  size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(RH, intermediate)), o_sq = take(split_bytes(T, Ism));
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
   size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
   size_t o_ro = take(4 * (experts + 1)), o_to = take(4 * (experts + 1)), o_status = take(8);
   size_t o_te = take(4 * p->capacity_max), o_ts = take(4 * p->capacity_max), o_tl = take(4 * p->capacity_max);
-  size_t o_h = take(2 * R * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
+  size_t o_h = take(2 * RH * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
   size_t o_so = take(2 * T * hidden), o_flags = take(32);
   p->arena_bytes = off;
   hipError_t e = hipMalloc(&p->arena, off);
@@ -1349,7 +1352,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->ids = reinterpret_cast<int32_t*>(b + o_ids);
   p->scores = reinterpret_cast<float*>(b + o_scores);
   p->xq = carve_split(b + o_xq, T, hidden);
-  p->hq = carve_split(b + o_hq, R, intermediate);
+  p->hq = carve_split(b + o_hq, RH, intermediate);
   p->sq = carve_split(b + o_sq, T, Ism);
   p->plan_ws = b + o_pws;
   p->sorted_route = reinterpret_cast<int32_t*>(b + o_sr);
@@ -1465,6 +1468,9 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   // tokens, identity rows) runs in the same launch as extra descriptors, so
   // its few items fill in beside the routed ones instead of running alone
   const bool merge_shared = shared != nullptr && Is == I;
+  // merged: the shared hidden rows are rows R .. R + T - 1 of h and of its split
+  uint16_t* const hs = merge_shared ? p->h + R * I : p->hs;
+  const SplitBuf sq = merge_shared ? SplitBuf{p->hq.hi + R * I, p->hq.lo + R * I, p->hq.scale + R * SI} : p->sq;
   GroupedGemmArgs g{};
   g.a_hi = p->xq.hi;
   g.a_lo = p->xq.lo;
@@ -1500,14 +1506,14 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
     g.x_weight_up = shared->up.weight;
     g.x_scale = shared->gate.scale_inv;
     g.x_scale_up = shared->up.scale_inv;
-    g.x_out = p->hs;
+    g.x_out = hs;
     g.x_out_row_stride = Is;
     g.x_fixup = shared_gate_flag;
     g.x_fixup_up = shared_up_flag;
   }
   HIP_TRY(launch_grouped_gemm(g, GEMM_SWIGLU, cap, st), "grouped gate/up launch");
   // 4. hidden -> split, 5. grouped down (+ the shared down when merged)
-  HIP_TRY(split(p->h, R, I, p->hq, st), "split hidden");
+  HIP_TRY(split(p->h, merge_shared ? R + T : R, I, p->hq, st), "split hidden");
   const int32_t* down_flag = bank->code_flags != nullptr ? bank->code_flags : p->flags + 1;
   GroupedGemmArgs d{};
   d.a_hi = p->hq.hi;
@@ -1531,12 +1537,11 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   d.out_row_stride = H;
   d.fixup = down_flag;
   if (merge_shared) {
-    HIP_TRY(split(p->hs, T, Is, p->sq, st), "split shared hidden");
     d.x_descriptors = cdiv(T, tile);
     d.x_routes = T;
-    d.x_a_hi = p->sq.hi;
-    d.x_a_lo = p->sq.lo;
-    d.x_a_scale = p->sq.scale;
+    d.x_a_hi = sq.hi;
+    d.x_a_lo = sq.lo;
+    d.x_a_scale = sq.scale;
     d.x_weight = shared->down.weight;
     d.x_scale = shared->down.scale_inv;
     d.x_out = p->shared_out;
