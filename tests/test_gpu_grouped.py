@@ -377,6 +377,24 @@ def test_prefill_shared_expert_merged_or_separate_matches_oracle(M, O, dev, shar
     assert_parity(to_bits(y).reshape(T, -1), want, O)
 
 
+def test_prefill_shared_rows_follow_each_calls_routes(M, O, dev):
+    """The merged shared expert's hidden rows sit right after the call's
+    routed rows (rows R .. R + T - 1, R = T k of that call) and share one
+    split launch with them: calls of 300, 96 and 300 tokens on one plan
+    (wide shape, 32-route shape, wide again), each against the oracle."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=512, intermediate=256, experts=32, top_k=8, limit=7.0, shared=1)
+    bank, shared, gate = syn.synth_layer(cfg, seed=71, device=dev)
+    moe = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)
+    for call, T in enumerate((300, 96, 300)):
+        x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(71, call), device=dev)
+        y = moe(x)
+        ids, sc = (t.reshape(T, 8).cpu().numpy() for t in gate(x))
+        xb = to_bits(x).reshape(T, -1)
+        want = O.direct_moe(xb, host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+        assert_parity(to_bits(y).reshape(T, -1), want, O)
+
+
 @pytest.mark.parametrize("which", ["gate", "up", "down"])
 @pytest.mark.parametrize("shared_experts", [1, 2])
 def test_prefill_480_codes_in_one_shared_weight(M, O, dev, shared_experts, which):
