@@ -52,6 +52,9 @@ def parse():
     p.add_argument("--prefill-only", action="store_true",
                    help="one synthetic layer, configs 4 and 5 prefill only (for profiling the grouped GEMM)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--layout", default="rows",
+                   help="expert-bank layout: rows (the reference's row-major layout, the library's default), "
+                        "tiled (16-row groups) or a row-group exponent 1..7")
     p.add_argument("--json-out", type=str, default="")
     p.add_argument("--traffic-run", action="store_true", help="short eager program for rocprofv3 --pmc passes")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -120,8 +123,9 @@ def main():
     # ------------------------------------------------------------ weights ---
     t0 = time.perf_counter()
     layers = []
+    layout = int(args.layout) if args.layout.isdigit() else args.layout
     for layer in range(L):
-        bank, shared, gate = syn.synth_layer(cfg, SEED, layer, dev)
+        bank, shared, gate = syn.synth_layer(cfg, SEED, layer, dev, layout=layout)
         plan = packed.DecodePlan(H, I, Is, E, k, cfg.swiglu_limit)
         bank.code_flags()
         layers.append(SimpleNamespace(bank=bank, shared=shared, gate=gate, plan=plan))
@@ -131,7 +135,8 @@ def main():
     log(f"generated {L} layers, {resident / 1e9:.1f} GB resident, in {gen_s:.1f} s")
 
     if args.prefill_only:
-        line = json.dumps({"prefill": bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn)})
+        line = json.dumps({"prefill": bench_prefill(args, layers[0], cfg, dev, torch, np, pkg, syn),
+                           "bank_layout": layers[0].bank.layout})
         print(line, flush=True)
         if args.json_out:
             Path(args.json_out).write_text(line + "\n")
@@ -240,6 +245,7 @@ def main():
                         "BF16 residual, fresh seeded token per step, HIP-graph replay",
             "layers": L, "hidden": H, "intermediate": I, "experts": E, "top_k": k, "shared_experts": 1,
             "resident_bytes": resident, "parallelism": "single GPU",
+            "bank_layout": layers[0].bank.layout,
         },
         "roofline": {
             "bound": "hbm",
@@ -369,10 +375,11 @@ def copy_probe(dev, torch):
 def host_layer_subset(layer, ids, torch, np):
     idx = torch.as_tensor(np.asarray(ids, dtype=np.int64), device=layer.bank.gate_up_weight.device)
     b = layer.bank
+    gate_up, down = b.reference_weights(idx)  # the oracle reads the reference row-major layout
     bank = SimpleNamespace(
-        gate_up_weight=b.gate_up_weight.index_select(0, idx).cpu().numpy(),
+        gate_up_weight=gate_up.cpu().numpy(),
         gate_up_scale_inv=b.gate_up_scale_inv.index_select(0, idx).cpu().numpy(),
-        down_weight=b.down_weight.index_select(0, idx).cpu().numpy(),
+        down_weight=down.cpu().numpy(),
         down_scale_inv=b.down_scale_inv.index_select(0, idx).cpu().numpy(),
         intermediate_size=b.intermediate_size)
     s = layer.shared

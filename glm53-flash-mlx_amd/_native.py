@@ -19,7 +19,11 @@ import torch
 _PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("GLM53_MOE_LIB", _PKG / "libglm53_moe.so"))
 
+ABI_VERSION = 2
 OK, INVALID_ARGUMENT, BAD_STATE, DEVICE_ERROR = 0, 1, 2, 3
+# Expert-matrix layouts (glm53_bank.row_group_log2): 0 = the reference's
+# row-major layout, g > 0 = row groups of 2^g rows; TILED is the library's.
+ROWS_LAYOUT, TILED_LAYOUT, MAX_ROW_GROUP_LOG2 = 0, 4, 7
 REDUCE_GROUPED, REDUCE_DIRECT = 0, 1
 STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN, STAGE_ALL = 1, 2, 4, 7
 
@@ -42,6 +46,7 @@ class Bank(ctypes.Structure):
         ("hidden", I64),
         ("intermediate", I64),
         ("code_flags", P),
+        ("row_group_log2", I32),
     ]
 
 
@@ -83,7 +88,9 @@ _SIGNATURES = {
     "glm53_abi_version": (ctypes.c_int, []),
     "glm53_e4m3_scan_codes": (ctypes.c_int, [P, I64, P, P]),
     "glm53_bank_create": (ctypes.c_int, [P, P, P]),
+    "glm53_bank_import": (ctypes.c_int, [P, I32, P, P]),
     "glm53_bank_destroy": (None, [P]),
+    "glm53_relayout_weights": (ctypes.c_int, [P, P, I64, I64, I64, I32, I32, P]),
     "glm53_fp8_linear_workspace_bytes": (SZ, [I64, I64, I64]),
     "glm53_fp8_linear": (ctypes.c_int, [P, I64, I64, P, I64, P, P, P, P, SZ, P]),
     "glm53_router_workspace_bytes": (SZ, [I64, I64, I64]),
@@ -104,7 +111,7 @@ _SIGNATURES = {
     "glm53_decode_moe_static": (ctypes.c_int, [I64, I64, I64, I64, F32, P, P, P, P, P, P, P]),
     "glm53_routed_diagnostic_create": (ctypes.c_int, [I64, I64, I64, I64, F32, P]),
     "glm53_routed_diagnostic_destroy": (None, [P]),
-    "glm53_routed_diagnostic_execute": (ctypes.c_int, [P, P, P, P, P, P]),
+    "glm53_routed_diagnostic_execute": (ctypes.c_int, [P, P, P, P, P, I32, P]),
     "glm53_routed_diagnostic_stage": (ctypes.c_int, [P, I32, P, P]),
     "glm53_routed_diagnostic_counters": (ctypes.c_int, [P, P, P]),
     "glm53_route_plan_workspace_bytes": (SZ, [I64, I64]),
@@ -127,7 +134,7 @@ _SIGNATURES = {
     "glm53_synth_fp8": (ctypes.c_int, [P, P, I64, I64, ctypes.c_uint64, F32, P]),
     "glm53_synth_f32": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, F32, F32, I32, P]),
     "glm53_synth_bf16": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, P]),
-    "glm53_synth_fp8_batched": (ctypes.c_int, [P, P, I64, I64, I64, I64, I64, ctypes.c_uint64, F32, P]),
+    "glm53_synth_fp8_batched": (ctypes.c_int, [P, P, I64, I64, I64, I64, I64, ctypes.c_uint64, F32, I32, P]),
     "glm53_synth_step_input": (ctypes.c_int, [P, I64, ctypes.c_uint64, F32, P, P]),
     "glm53_probe_read": (ctypes.c_int, [P, I64, P, I32, P]),
 }
@@ -187,6 +194,20 @@ def workspace(nbytes: int, device) -> torch.Tensor | None:
     if nbytes == 0:
         return None
     return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+def relayout(src: torch.Tensor, dst: torch.Tensor, from_log2: int, to_log2: int) -> None:
+    """Re-lay the expert matrices of a uint8 [E, rows, cols] tensor from one
+    layout to another into `dst` (same shape, no overlap) on the current
+    stream (glm53_relayout_weights)."""
+    require_device(src, dst)
+    if src.dtype != torch.uint8 or src.dim() != 3 or dst.shape != src.shape or dst.dtype != torch.uint8:
+        raise ValueError("relayout needs two uint8 [experts, rows, cols] tensors of one shape")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("relayout needs contiguous tensors")
+    experts, rows, cols = src.shape
+    check(lib().glm53_relayout_weights(ptr(src), ptr(dst), experts, rows, cols, int(from_log2), int(to_log2),
+                                       stream_handle(src.device)))
 
 
 def scan_codes(codes: torch.Tensor) -> torch.Tensor:

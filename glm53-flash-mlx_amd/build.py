@@ -19,7 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libglm53_moe.so"
 BUILD = PKG / "_build"
-SOURCES = ["decode.hip", "step.hip", "grouped.hip", "router.hip", "synth.hip", "api.cpp"]
+SOURCES = ["decode.hip", "step.hip", "grouped.hip", "router.hip", "layout.hip", "synth.hip", "api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -8,7 +8,8 @@ packs a layer's routed experts into the four bank buffers
 This module does the same from the files themselves: shard headers are
 parsed as JSON and tensor bytes are memory-mapped (nothing in a file is
 executed), checked, and copied expert by expert into device buffers of the
-reference layout, so host memory holds one expert at a time.
+reference layout, so host memory holds one expert at a time; the bank is
+then re-laid on the device when another layout is asked for.
 
 Tensor names are found by pattern, whatever their prefix:
 ``<p>layers.<L>.mlp.experts.<e>.{gate,up,down}_proj.weight`` (+
@@ -35,7 +36,7 @@ import torch
 from . import _native as N
 from .fp8 import ClampedMLP
 from .ownership import TensorLayout, owned_tensor
-from .packed import PackedFP8ExpertBank
+from .packed import DEFAULT_LAYOUT, PackedFP8ExpertBank
 from .router import Float32Gate
 
 BLOCK = 128
@@ -70,77 +71,104 @@ def _shard_header(path: Path):
     return header, length, path.stat().st_size
 
 
-def read_headers(root) -> tuple[dict[str, TensorHeader], list[str]]:
-    """Every tensor header of the checkpoint, and the validation failures
-    (manifest.py:300-350: known dtype, byte range = shape x dtype size, no
-    overlap, shard size = 8 + header + data, index and headers agree)."""
-    root = Path(root)
+def _shard_list(root: Path) -> tuple[dict[str, str] | None, list[str]]:
+    """The index's weight map (None for a single-file checkpoint) and the
+    shard files to read."""
     index_path = root / "model.safetensors.index.json"
     if index_path.is_file():
         weight_map = json.loads(index_path.read_text())["weight_map"]
-    elif (root / "model.safetensors").is_file():
-        weight_map = None
-    else:
-        raise CheckpointError(f"no model.safetensors.index.json or model.safetensors in {root}")
-    shards = sorted(set(weight_map.values())) if weight_map is not None else ["model.safetensors"]
+        return weight_map, sorted(set(weight_map.values()))
+    if (root / "model.safetensors").is_file():
+        return None, ["model.safetensors"]
+    raise CheckpointError(f"{root} holds neither model.safetensors.index.json nor model.safetensors")
+
+
+def _decode_entry(shard: str, key: str, meta, base: int) -> tuple[TensorHeader | None, list[str]]:
+    """One JSON header entry as a TensorHeader (absolute offsets), or None
+    and why it cannot be used."""
+    try:
+        dtype, shape = str(meta["dtype"]), tuple(int(d) for d in meta["shape"])
+        lo, hi = (int(v) for v in meta["data_offsets"])
+    except (KeyError, TypeError, ValueError):
+        return None, [f"{shard}: header entry {key} has no usable dtype / shape / data_offsets"]
+    if dtype not in _DTYPE_BYTES:
+        return None, [f"{key}: dtype {dtype} is not one this loader reads"]
+    need = math.prod(shape) * _DTYPE_BYTES[dtype]
+    problems = [] if 0 <= lo <= hi and hi - lo == need else [
+        f"{key}: data_offsets [{lo}, {hi}) do not hold the {need} bytes of {dtype}{list(shape)}"]
+    return TensorHeader(shard, dtype, shape, base + lo, base + hi), problems
+
+
+def _byte_accounting(shard: str, entries: list[TensorHeader], names: list[str], data_start: int,
+                     file_size: int) -> list[str]:
+    """Tensors of one shard must not share bytes, and the data section must
+    end where the file does."""
+    problems = []
+    order = sorted(range(len(entries)), key=lambda i: (entries[i].start, entries[i].end))
+    reach, holder = data_start, None  # end of the bytes claimed so far, and who claimed the last of them
+    for i in order:
+        if entries[i].start < reach and holder is not None:
+            problems.append(f"{shard}: tensors {names[holder]} and {names[i]} claim overlapping bytes")
+        if entries[i].end >= reach:
+            reach, holder = entries[i].end, i
+    if reach != file_size:
+        problems.append(f"{shard}: the header accounts for {reach} bytes but the file has {file_size}")
+    return problems
+
+
+def read_headers(root) -> tuple[dict[str, TensorHeader], list[str]]:
+    """Every tensor header of the checkpoint, and what is wrong with them:
+    the rules of the reference's header audit (manifest.py:300-350) -- a
+    known dtype, a byte range of exactly shape x element size, no two
+    tensors sharing bytes, a shard's data ending at its file's end, and
+    the index naming exactly the tensors the shards hold."""
+    root = Path(root)
+    weight_map, shards = _shard_list(root)
     tensors: dict[str, TensorHeader] = {}
-    failures: list[str] = []
+    problems: list[str] = []
     for shard in shards:
         header, length, size = _shard_header(root / shard)
-        base = 8 + length
-        ranges, data_end = [], 0
-        for key in sorted(k for k in header if k != "__metadata__"):
-            meta = header[key]
-            try:
-                dtype = str(meta["dtype"])
-                shape = tuple(int(d) for d in meta["shape"])
-                start, end = (int(v) for v in meta["data_offsets"])
-            except (KeyError, TypeError, ValueError):
-                failures.append(f"malformed tensor header {key} in {shard}")
+        names = sorted(k for k in header if k != "__metadata__")
+        kept, kept_names = [], []
+        for key in names:
+            entry, why = _decode_entry(shard, key, header[key], 8 + length)
+            problems += why
+            if entry is None:
                 continue
-            if dtype not in _DTYPE_BYTES:
-                failures.append(f"unsupported dtype {dtype} for {key}")
-                continue
-            if start < 0 or end < start or end - start != math.prod(shape) * _DTYPE_BYTES[dtype]:
-                failures.append(f"invalid data range for {key}")
             if key in tensors:
-                failures.append(f"duplicate tensor header {key}")
-            tensors[key] = TensorHeader(shard, dtype, shape, base + start, base + end)
-            ranges.append((start, end, key))
-            data_end = max(data_end, end)
-        ranges.sort()
-        for (_, prev_end, prev_key), (cur_start, _, cur_key) in zip(ranges, ranges[1:]):
-            if prev_end > cur_start:
-                failures.append(f"overlapping tensors {prev_key} and {cur_key}")
-        if base + data_end != size:
-            failures.append(f"shard size/header mismatch: {shard}")
+                problems.append(f"{key}: declared in two headers ({tensors[key].shard}, {shard})")
+            tensors[key] = entry
+            kept.append(entry)
+            kept_names.append(key)
+        problems += _byte_accounting(shard, kept, kept_names, 8 + length, size)
     if weight_map is not None:
-        mapped, present = set(weight_map), set(tensors)
-        if mapped - present:
-            failures.append(f"{len(mapped - present)} indexed tensor(s) absent from headers: {min(mapped - present)}")
-        if present - mapped:
-            failures.append(f"{len(present - mapped)} unindexed tensor(s) in headers: {min(present - mapped)}")
-    return tensors, failures
+        for label, names in (("the index names {} tensor(s) no shard header holds", set(weight_map) - set(tensors)),
+                             ("shard headers hold {} tensor(s) the index does not name", set(tensors) - set(weight_map))):
+            if names:
+                problems.append(label.format(len(names)) + f", first {min(names)}")
+    return tensors, problems
 
 
 def validate_fp8_pairs(tensors: dict[str, TensorHeader]) -> list[str]:
-    """manifest.py:352-374: each F8_E4M3 tensor is a 2-D .weight whose
-    .weight_scale_inv is F32 [ceil(rows/128), ceil(cols/128)]."""
-    failures = []
-    for key, t in tensors.items():
-        if t.dtype != "F8_E4M3":
+    """The FP8 pair rule of the reference's audit (manifest.py:352-374):
+    each F8_E4M3 tensor is a 2-D ``.weight`` with an F32 ``.weight_scale_inv``
+    of shape [ceil(rows/128), ceil(cols/128)].  The wrong-scale message keeps
+    the reference's wording, which its test asserts
+    (tests/test_manifest.py:230-244)."""
+    problems = []
+    for key in (k for k, t in tensors.items() if t.dtype == "F8_E4M3"):
+        shape = tensors[key].shape
+        if len(shape) != 2 or not key.endswith(".weight"):
+            problems.append(f"{key}: an F8_E4M3 tensor must be a 2-D '.weight', got shape {list(shape)}")
             continue
-        if not key.endswith(".weight") or len(t.shape) != 2:
-            failures.append(f"unexpected FP8 tensor without 2-D weight semantics: {key}")
-            continue
-        scale = tensors.get(key + "_scale_inv")
+        scale_key = key + "_scale_inv"
+        scale = tensors.get(scale_key)
+        want = (math.ceil(shape[0] / BLOCK), math.ceil(shape[1] / BLOCK))
         if scale is None:
-            failures.append(f"missing FP8 scale tensor: {key}_scale_inv")
-            continue
-        want = (math.ceil(t.shape[0] / BLOCK), math.ceil(t.shape[1] / BLOCK))
-        if scale.dtype != "F32" or scale.shape != want:
-            failures.append(f"invalid FP8 scale {key}_scale_inv: {scale.dtype}{scale.shape}, expected F32{want}")
-    return failures
+            problems.append(f"{key}: its block scales {scale_key} are missing")
+        elif (scale.dtype, scale.shape) != ("F32", want):
+            problems.append(f"invalid FP8 scale {scale_key}: {scale.dtype}{scale.shape}, expected F32{want}")
+    return problems
 
 
 def moe_layer_keys(tensors: dict[str, TensorHeader], layer: int) -> SimpleNamespace:
@@ -208,9 +236,12 @@ def layer_config(root) -> SimpleNamespace:
                            norm_topk_prob=bool(text.get("norm_topk_prob", True)))
 
 
-def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = None):
+def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = None, *, layout=None):
     """(bank, shared expert or None, gate) of one layer on `device`, after
-    header, FP8-pair and shape validation (CheckpointError lists failures)."""
+    header, FP8-pair and shape validation (CheckpointError lists failures).
+    The bank is re-laid into `layout` (the package's DEFAULT_LAYOUT when
+    None; "rows" keeps the checkpoint's row-major layout) once its bytes are
+    on the device."""
     N.require_device(torch.empty(0, device=device))
     root = Path(root)
     config = config or layer_config(root)
@@ -259,6 +290,9 @@ def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = No
     rm = TensorLayout.ROW_MAJOR_CONTIGUOUS
     bank = PackedFP8ExpertBank(owned_tensor(gate_up, layout=rm), owned_tensor(gate_up_s, layout=rm),
                                owned_tensor(down, layout=rm), owned_tensor(down_s, layout=rm), intermediate_size=I)
+    layout = DEFAULT_LAYOUT if layout is None else layout
+    if layout != "rows" and H % BLOCK == 0 and I % BLOCK == 0:
+        bank.relayout_(layout)
     shared = None
     if keys.shared is not None:
         Is = tensors[keys.shared["gate"]].shape[0]

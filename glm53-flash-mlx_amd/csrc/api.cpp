@@ -16,6 +16,7 @@
 
 #include "grouped.h"
 #include "kernels.h"
+#include "layout.h"
 #include "synth.h"
 
 using namespace glm53;
@@ -102,6 +103,36 @@ int check_bank(const glm53_bank* b, int64_t H, int64_t I, int64_t E) {
   CHECK_ARG(b->hidden == H && b->intermediate == I && b->experts == E,
             "bank shape (E=%lld, H=%lld, I=%lld) != plan (E=%lld, H=%lld, I=%lld)", (long long)b->experts,
             (long long)b->hidden, (long long)b->intermediate, (long long)E, (long long)H, (long long)I);
+  CHECK_ARG(b->row_group_log2 >= 0 && b->row_group_log2 <= GLM53_MAX_ROW_GROUP_LOG2,
+            "bank row_group_log2 %d outside [0, %d]", (int)b->row_group_log2, GLM53_MAX_ROW_GROUP_LOG2);
+  CHECK_ARG(b->row_group_log2 == 0 || (H % 128 == 0 && I % 128 == 0),
+            "a row-group bank needs hidden and intermediate multiples of 128 (H=%lld, I=%lld)", (long long)H,
+            (long long)I);
+  return GLM53_OK;
+}
+
+// A bank handle: the descriptor handed out (first, so the pointer returned
+// is the handle's) and the device buffers the handle owns -- the code flag,
+// and for an imported bank the re-laid weights and the copied scales.
+struct BankHandle {
+  glm53_bank pub;
+  void* owned[5];
+};
+
+int check_layout_args(int64_t matrices, int64_t rows, int64_t cols, int32_t from_log2, int32_t to_log2) {
+  CHECK_ARG(matrices >= 0 && rows >= 0 && cols >= 0, "invalid dimensions");
+  CHECK_ARG(from_log2 >= 0 && from_log2 <= GLM53_MAX_ROW_GROUP_LOG2 && to_log2 >= 0 &&
+                to_log2 <= GLM53_MAX_ROW_GROUP_LOG2,
+            "row_group_log2 must lie in [0, %d]", GLM53_MAX_ROW_GROUP_LOG2);
+  CHECK_ARG((rows * cols) % 16 == 0, "rows * cols must be a multiple of 16");
+  if (from_log2 > 0 || to_log2 > 0) {
+    const int64_t group = int64_t{1} << std::max(from_log2, to_log2);
+    CHECK_ARG(cols % 128 == 0, "a row-group layout needs cols % 128 == 0 (cols=%lld)", (long long)cols);
+    CHECK_ARG(rows % group == 0, "rows (%lld) must be a multiple of the row group (%lld)", (long long)rows,
+              (long long)group);
+  } else {
+    CHECK_ARG(cols % 16 == 0, "cols must be a multiple of 16");
+  }
   return GLM53_OK;
 }
 
@@ -191,6 +222,22 @@ int glm53_e4m3_scan_codes(const uint8_t* codes, int64_t n, int32_t* flag, void* 
   return GLM53_OK;
 }
 
+int glm53_relayout_weights(const uint8_t* src, uint8_t* dst, int64_t matrices, int64_t rows, int64_t cols,
+                           int32_t from_log2, int32_t to_log2, void* stream) {
+  int rc = check_layout_args(matrices, rows, cols, from_log2, to_log2);
+  if (rc) return rc;
+  const int64_t bytes = matrices * rows * cols;
+  if (bytes == 0) return GLM53_OK;
+  CHECK_ARG(src && dst, "null pointer argument");
+  CHECK_ARG(aligned(src, 16) && aligned(dst, 16), "weights must be 16-byte aligned");
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+  CHECK_ARG(s0 + static_cast<uintptr_t>(bytes) <= d0 || d0 + static_cast<uintptr_t>(bytes) <= s0,
+            "source and destination overlap (the re-lay is out of place)");
+  RelayoutArgs a{src, dst, rows, cols, matrices, rows * cols, from_log2, to_log2};
+  HIP_TRY(launch_relayout(a, S(stream)), "relayout launch");
+  return GLM53_OK;
+}
+
 int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out) {
   CHECK_ARG(desc != nullptr && out != nullptr, "null pointer argument");
   *out = nullptr;
@@ -199,6 +246,8 @@ int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out) {
   CHECK_ARG(desc->experts > 0 && desc->hidden > 0 && desc->intermediate > 0, "invalid bank dimensions");
   CHECK_ARG(aligned(desc->gate_up_weight, 16) && aligned(desc->down_weight, 16),
             "bank weights must be 16-byte aligned");
+  int rc = check_bank(desc, desc->hidden, desc->intermediate, desc->experts);
+  if (rc) return rc;
   int32_t* flag = nullptr;
   HIP_TRY(hipMalloc(&flag, sizeof(int32_t)), "bank code flag hipMalloc");
   const int64_t gu = desc->experts * 2 * desc->intermediate * desc->hidden;
@@ -209,16 +258,76 @@ int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out) {
     (void)hipFree(flag);
     return hip_fail(e, "bank code scan");
   }
-  auto* b = new glm53_bank(*desc);
-  b->code_flags = flag;
-  *out = b;
+  auto* b = new BankHandle{};
+  b->pub = *desc;
+  b->pub.code_flags = flag;
+  b->owned[0] = flag;
+  *out = &b->pub;
+  return GLM53_OK;
+}
+
+int glm53_bank_import(const glm53_bank* desc, int32_t row_group_log2, void* stream, glm53_bank** out) {
+  CHECK_ARG(desc != nullptr && out != nullptr, "null pointer argument");
+  *out = nullptr;
+  CHECK_ARG(desc->gate_up_weight && desc->gate_up_scale_inv && desc->down_weight && desc->down_scale_inv,
+            "null bank tensor");
+  CHECK_ARG(desc->experts > 0 && desc->hidden > 0 && desc->intermediate > 0, "invalid bank dimensions");
+  const int64_t E = desc->experts, H = desc->hidden, I = desc->intermediate;
+  int rc = check_bank(desc, H, I, E);
+  if (rc) return rc;
+  glm53_bank want = *desc;
+  want.row_group_log2 = row_group_log2;
+  if ((rc = check_bank(&want, H, I, E))) return rc;
+  if ((rc = check_layout_args(E, 2 * I, H, desc->row_group_log2, row_group_log2))) return rc;
+  if ((rc = check_layout_args(E, H, I, desc->row_group_log2, row_group_log2))) return rc;
+  CHECK_ARG(aligned(desc->gate_up_weight, 16) && aligned(desc->down_weight, 16),
+            "bank weights must be 16-byte aligned");
+  const size_t gu = static_cast<size_t>(E * 2 * I * H), dn = static_cast<size_t>(E * H * I);
+  const size_t gus = sizeof(float) * static_cast<size_t>(E * 2 * cdiv(I, 128) * cdiv(H, 128));
+  const size_t dns = sizeof(float) * static_cast<size_t>(E * cdiv(H, 128) * cdiv(I, 128));
+  hipStream_t st = S(stream);
+  auto* b = new BankHandle{};
+  auto cleanup = [&](int code) {
+    for (void* q : b->owned)
+      if (q) (void)hipFree(q);
+    delete b;
+    return code;
+  };
+  const size_t sizes[5] = {sizeof(int32_t), gu, gus, dn, dns};
+  for (int i = 0; i < 5; ++i) {
+    hipError_t e = hipMalloc(&b->owned[i], sizes[i]);
+    if (e != hipSuccess) return cleanup(hip_fail(e, "bank import hipMalloc"));
+  }
+  uint8_t* gw = static_cast<uint8_t*>(b->owned[1]);
+  uint8_t* dw = static_cast<uint8_t*>(b->owned[3]);
+  RelayoutArgs r1{desc->gate_up_weight, gw, 2 * I, H, E, 2 * I * H, desc->row_group_log2, row_group_log2};
+  RelayoutArgs r2{desc->down_weight, dw, H, I, E, H * I, desc->row_group_log2, row_group_log2};
+  hipError_t e = launch_relayout(r1, st);
+  if (e == hipSuccess) e = launch_relayout(r2, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(b->owned[2], desc->gate_up_scale_inv, gus, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(b->owned[4], desc->down_scale_inv, dns, hipMemcpyDeviceToDevice, st);
+  int32_t* flag = static_cast<int32_t*>(b->owned[0]);
+  if (e == hipSuccess) e = launch_scan_480(gw, static_cast<int64_t>(gu), flag, true, st);
+  if (e == hipSuccess) e = launch_scan_480(dw, static_cast<int64_t>(dn), flag, false, st);
+  // the caller's buffers may be released once this returns
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return cleanup(hip_fail(e, "bank import"));
+  b->pub = want;
+  b->pub.gate_up_weight = gw;
+  b->pub.gate_up_scale_inv = static_cast<const float*>(b->owned[2]);
+  b->pub.down_weight = dw;
+  b->pub.down_scale_inv = static_cast<const float*>(b->owned[4]);
+  b->pub.code_flags = flag;
+  *out = &b->pub;
   return GLM53_OK;
 }
 
 void glm53_bank_destroy(glm53_bank* bank) {
   if (bank == nullptr) return;
-  (void)hipFree(const_cast<int32_t*>(bank->code_flags));
-  delete bank;
+  auto* b = reinterpret_cast<BankHandle*>(bank);
+  for (void* q : b->owned)
+    if (q) (void)hipFree(q);
+  delete b;
 }
 
 int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight, int64_t N, const float* scale_inv,
@@ -498,7 +607,7 @@ bool decode_fast_ok(int64_t H, int64_t I, int64_t Is, const glm53_bank* bank, co
 int generic_linear(const void* x, int64_t x_group_stride, int64_t M, int64_t G, const uint8_t* w,
                    int64_t w_expert_stride, int64_t w_row_offset, const float* s, int64_t s_expert_stride,
                    int64_t s_row_offset, int64_t s_cols, const int32_t* ids, int64_t experts, int64_t N, int64_t K,
-                   uint16_t* y, int64_t y_group_stride, int* err, hipStream_t st) {
+                   uint16_t* y, int64_t y_group_stride, int* err, hipStream_t st, int wg = 0) {
   CHECK_ARG(K <= 16384, "generic path supports K <= 16384");
   GenericLinearArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -507,6 +616,7 @@ int generic_linear(const void* x, int64_t x_group_stride, int64_t M, int64_t G, 
   a.weight = w;
   a.w_expert_stride = w_expert_stride;
   a.w_row_offset = w_row_offset;
+  a.w_group_log2 = wg;
   a.scale = s;
   a.s_expert_stride = s_expert_stride;
   a.s_row_offset = s_row_offset;
@@ -555,6 +665,7 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
     g.experts = p->E;
     g.gate_up_weight = bank->gate_up_weight;
     g.gate_up_scale = bank->gate_up_scale_inv;
+    g.bank_group_log2 = bank->row_group_log2;
     if (shared != nullptr) {
       g.shared_gate_weight = shared->gate.weight;
       g.shared_gate_scale = shared->gate.scale_inv;
@@ -583,6 +694,7 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
     d.experts = p->E;
     d.down_weight = bank->down_weight;
     d.down_scale = bank->down_scale_inv;
+    d.bank_group_log2 = bank->row_group_log2;
     if (shared != nullptr) {
       d.shared_down_weight = shared->down.weight;
       d.shared_down_scale = shared->down.scale_inv;
@@ -610,11 +722,12 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
   // (packed.py:473-655): gate, up, SwiGLU, down, weighted reduction, shared.
   const int64_t SR = cdiv(I, 128), SC = cdiv(H, 128), SH = cdiv(H, 128), SI = cdiv(I, 128);
   int rc;
+  const int bg = bank->row_group_log2;
   if ((rc = generic_linear(x, 0, 1, k, bank->gate_up_weight, 2 * I * H, 0, bank->gate_up_scale_inv, 2 * SR * SC, 0,
-                           SC, ids, p->E, I, H, p->gate, I, p->err, st)))
+                           SC, ids, p->E, I, H, p->gate, I, p->err, st, bg)))
     return rc;
   if ((rc = generic_linear(x, 0, 1, k, bank->gate_up_weight, 2 * I * H, I, bank->gate_up_scale_inv, 2 * SR * SC, SR,
-                           SC, ids, p->E, I, H, p->up, I, p->err, st)))
+                           SC, ids, p->E, I, H, p->up, I, p->err, st, bg)))
     return rc;
   SwigluArgs sw{};
   sw.gate = p->gate;
@@ -628,7 +741,7 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
   sw.out_row_stride = I;
   HIP_TRY(launch_swiglu(sw, st), "swiglu launch");
   if ((rc = generic_linear(p->hidden, I, 1, k, bank->down_weight, H * I, 0, bank->down_scale_inv, SH * SI, 0, SI, ids,
-                           p->E, H, I, p->down, H, p->err, st)))
+                           p->E, H, I, p->down, H, p->err, st, bg)))
     return rc;
   WeightedReductionArgs wr{};
   wr.down = p->down;
@@ -717,6 +830,7 @@ int run_step(const StepContext& c, const glm53_bank* bank, const glm53_shared_ex
   a.gate_up_scale = bank->gate_up_scale_inv;
   a.down_weight = bank->down_weight;
   a.down_scale = bank->down_scale_inv;
+  a.bank_group_log2 = bank->row_group_log2;
   a.routed_flags = bank->code_flags;
   if (shared != nullptr) {
     a.shared_gate_weight = shared->gate.weight;
@@ -1020,18 +1134,22 @@ void glm53_routed_diagnostic_destroy(glm53_routed_diagnostic* diag) {
 }
 
 int glm53_routed_diagnostic_execute(glm53_routed_diagnostic* d, const void* x, const int32_t* expert_ids,
-                                    const uint8_t* gate_up_weight, const float* gate_up_scale_inv, void* stream) {
+                                    const uint8_t* gate_up_weight, const float* gate_up_scale_inv,
+                                    int32_t row_group_log2, void* stream) {
   CHECK_ARG(d != nullptr, "diagnostic is null");
   CHECK_ARG(x && expert_ids && gate_up_weight && gate_up_scale_inv, "null pointer argument");
-  hipStream_t st = S(stream);
   const int64_t H = d->H, I = d->I, k = d->k;
+  CHECK_ARG(row_group_log2 >= 0 && row_group_log2 <= GLM53_MAX_ROW_GROUP_LOG2 &&
+                (row_group_log2 == 0 || (H % 128 == 0 && I % 128 == 0)),
+            "invalid row_group_log2 %d for H=%lld, I=%lld", (int)row_group_log2, (long long)H, (long long)I);
+  hipStream_t st = S(stream);
   const int64_t SR = cdiv(I, 128), SC = cdiv(H, 128);
   int rc;
   if ((rc = generic_linear(x, 0, 1, k, gate_up_weight, 2 * I * H, 0, gate_up_scale_inv, 2 * SR * SC, 0, SC,
-                           expert_ids, d->E, I, H, d->stage[0], I, d->err, st)))
+                           expert_ids, d->E, I, H, d->stage[0], I, d->err, st, row_group_log2)))
     return rc;
   if ((rc = generic_linear(x, 0, 1, k, gate_up_weight, 2 * I * H, I, gate_up_scale_inv, 2 * SR * SC, SR, SC,
-                           expert_ids, d->E, I, H, d->stage[1], I, d->err, st)))
+                           expert_ids, d->E, I, H, d->stage[1], I, d->err, st, row_group_log2)))
     return rc;
   SwigluArgs a{};
   a.gate = d->stage[0];
@@ -1314,7 +1432,12 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->k = top_k;
   p->max_tokens = max_tokens;
   p->limit = swiglu_limit;
-  const int64_t T = max_tokens, R = T * top_k, Ism = std::max<int64_t>(shared_intermediate, 128);
+  const int64_t T = max_tokens, R = T * top_k;
+  // the separate shared hidden rows (hs) and their split (sq) serve only a
+  // shared expert of another width than the routed one: one of the routed
+  // width runs merged into the routed buffers (below)
+  const bool separate_shared = shared_intermediate > 0 && shared_intermediate != intermediate;
+  const int64_t Ism = separate_shared ? shared_intermediate : 0;
   p->capacity_max = cdiv(R, kGemmMinTileRows) + experts;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -1327,7 +1450,8 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   // a shared expert of the routed width keeps its hidden rows right after
   // the routed ones (h and hq), so that one split launch covers both
   const int64_t RH = shared_intermediate == intermediate ? R + T : R;
-  size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(RH, intermediate)), o_sq = take(split_bytes(T, Ism));
+  size_t o_xq = take(split_bytes(T, hidden)), o_hq = take(split_bytes(RH, intermediate));
+  size_t o_sq = take(separate_shared ? split_bytes(T, Ism) : 0);
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
   size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
   size_t o_ro = take(4 * (experts + 1)), o_to = take(4 * (experts + 1)), o_status = take(8);
@@ -1353,7 +1477,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->scores = reinterpret_cast<float*>(b + o_scores);
   p->xq = carve_split(b + o_xq, T, hidden);
   p->hq = carve_split(b + o_hq, RH, intermediate);
-  p->sq = carve_split(b + o_sq, T, Ism);
+  p->sq = separate_shared ? carve_split(b + o_sq, T, Ism) : SplitBuf{nullptr, nullptr, nullptr};
   p->plan_ws = b + o_pws;
   p->sorted_route = reinterpret_cast<int32_t*>(b + o_sr);
   p->inverse = reinterpret_cast<int32_t*>(b + o_inv);
@@ -1368,7 +1492,7 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   p->tile_len = reinterpret_cast<int32_t*>(b + o_tl);
   p->h = reinterpret_cast<uint16_t*>(b + o_h);
   p->down = reinterpret_cast<uint16_t*>(b + o_down);
-  p->hs = reinterpret_cast<uint16_t*>(b + o_hs);
+  p->hs = separate_shared ? reinterpret_cast<uint16_t*>(b + o_hs) : nullptr;
   p->shared_out = reinterpret_cast<uint16_t*>(b + o_so);
   p->flags = reinterpret_cast<int32_t*>(b + o_flags);
   *out = p;
@@ -1485,8 +1609,9 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   g.used_descriptors = p->status + 1;
   g.experts = E;
   g.weight = bank->gate_up_weight;
-  g.weight_up = bank->gate_up_weight + I * H;
+  g.weight_up = bank->gate_up_weight + I * H;  // row I: a whole number of row groups
   g.w_expert_stride = 2 * I * H;
+  g.w_group_log2 = bank->row_group_log2;
   g.scale = bank->gate_up_scale_inv;
   g.scale_up = bank->gate_up_scale_inv + SR * SC;
   g.s_expert_stride = 2 * SR * SC;
@@ -1529,6 +1654,7 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   d.experts = E;
   d.weight = bank->down_weight;
   d.w_expert_stride = H * I;
+  d.w_group_log2 = bank->row_group_log2;
   d.scale = bank->down_scale_inv;
   d.s_expert_stride = (H / 128) * SI;
   d.s_cols = SI;
@@ -1700,15 +1826,19 @@ int glm53_sigmoid_bf16(const void* gate, int64_t n, void* out, void* stream) {
 
 int glm53_synth_fp8(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, uint64_t seed, float std,
                     void* stream) {
-  return glm53_synth_fp8_batched(codes, scale_inv, rows, cols, 1, 0, 0, seed, std, stream);
+  return glm53_synth_fp8_batched(codes, scale_inv, rows, cols, 1, 0, 0, seed, std, 0, stream);
 }
 
 int glm53_synth_fp8_batched(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, int64_t batch,
-                            int64_t codes_stride, int64_t scale_stride, uint64_t seed, float std, void* stream) {
+                            int64_t codes_stride, int64_t scale_stride, uint64_t seed, float std,
+                            int32_t row_group_log2, void* stream) {
   CHECK_ARG(rows >= 0 && cols >= 0 && batch >= 0 && batch < 65536, "invalid dimensions");
+  CHECK_ARG(row_group_log2 >= 0 && row_group_log2 <= GLM53_MAX_ROW_GROUP_LOG2, "invalid row_group_log2");
+  CHECK_ARG(row_group_log2 == 0 || (cols % 128 == 0 && rows % (int64_t{1} << row_group_log2) == 0),
+            "a row-group layout needs cols % 128 == 0 and whole row groups");
   if (rows == 0 || cols == 0 || batch == 0) return GLM53_OK;
   CHECK_ARG(codes && scale_inv, "null pointer argument");
-  SynthFp8Args a{codes, scale_inv, rows, cols, seed, std, batch, codes_stride, scale_stride};
+  SynthFp8Args a{codes, scale_inv, rows, cols, seed, std, batch, codes_stride, scale_stride, row_group_log2};
   HIP_TRY(launch_synth_fp8(a, S(stream)), "synth launch");
   return GLM53_OK;
 }
@@ -1784,12 +1914,19 @@ StaticLayout static_layout(int64_t H, int64_t I, int64_t E, int64_t k) {
   return l;
 }
 
-// The current GPU's copy of the scratch: its address is looked up, and the
-// whole array cleared with a fill kernel on `st`, on the first call made on
-// that GPU.
+// The copy of the scratch on the GPU of `st`, which must be the current
+// device (hipGetSymbolAddress resolves the current device's copy, and the
+// kernels run on the stream's).  The first call on a GPU looks the address
+// up and clears the whole array with a fill kernel on `st`, then waits for
+// that kernel, so calls on any stream of that GPU start from the cleared
+// array (that first call cannot be under graph capture, where waiting is not
+// allowed).
 int static_scratch_base(hipStream_t st, uint8_t** out) {
-  int dev = 0;
+  int dev = 0, stream_dev = 0;
   HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  HIP_TRY(hipStreamGetDevice(st, &stream_dev), "hipStreamGetDevice");
+  CHECK_ARG(stream_dev == dev, "the stream belongs to device %d but device %d is current; make the stream's device "
+            "current before calling glm53_decode_moe_static", stream_dev, dev);
   CHECK_ARG(dev >= 0 && dev < kStaticMaxDevices, "device %d is beyond the static scratch table (%d devices)", dev,
             kStaticMaxDevices);
   std::lock_guard<std::mutex> lock(g_static_mutex);
@@ -1799,6 +1936,7 @@ int static_scratch_base(hipStream_t st, uint8_t** out) {
     hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, static_cast<uint32_t*>(ptr),
                        static_cast<int64_t>(GLM53_DECODE_STATIC_SCRATCH_BYTES / 4));
     HIP_TRY(hipGetLastError(), "static scratch clear launch");
+    HIP_TRY(hipStreamSynchronize(st), "static scratch clear (first call on this GPU; not under graph capture)");
     g_static_base[dev] = static_cast<uint8_t*>(ptr);
   }
   *out = g_static_base[dev];

@@ -10,6 +10,26 @@ namespace glm53 {
 constexpr int kBlock = 128;   // FP8 scale block edge (weight_scale_inv is per 128x128)
 constexpr int kWave = 64;
 
+// ------------------------------------------------------- weight layouts ---
+//
+// An E4M3 matrix [N, K] is stored either row-major (g = 0: the checkpoint
+// layout, element (n, k) at n K + k) or in row groups (g = 1 .. 7, K a
+// multiple of 128): the 2^g rows of group n >> g are stored together, their
+// K span as K / 128 consecutive blocks of 2^g rows x 128 bytes, so that
+//   (n, k) -> (n >> g) 2^g K + (k >> 7) 2^g 128 + (n mod 2^g) 128 + k mod 128.
+// A 128-row MFMA weight stage then reads 128 / 2^g contiguous runs of
+// 2^g x 128 bytes instead of 128 runs of 128 bytes, and a group's whole K
+// span (2^g K bytes) is one contiguous run for the decode GEMV.  g = 0 is
+// the same formula, so every kernel takes g as an argument.
+constexpr int kMaxRowGroupLog2 = 7;
+
+__host__ __device__ __forceinline__ int64_t group_row_base(int64_t n, int64_t K, int g) {
+  return ((n >> g) << g) * K + ((n & ((int64_t{1} << g) - 1)) << 7);
+}
+__host__ __device__ __forceinline__ int64_t group_col(int64_t k, int g) {
+  return ((k >> 7) << (7 + g)) | (k & 127);
+}
+
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------ BF16 ---

@@ -34,9 +34,10 @@ template <int VB, int CH, bool HW>
 __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const uint8_t* __restrict__ gate_w,
                                              const uint8_t* __restrict__ up_w, const float* __restrict__ gate_s,
                                              const float* __restrict__ up_s, uint16_t* __restrict__ out,
-                                             int64_t r0, int64_t r_end, int lane) {
+                                             int64_t r0, int64_t r_end, int g, int lane) {
   const int64_t K = a.hidden;
   const int64_t SC = (K + kBlock - 1) / kBlock;
+  const RowWalk walk = row_walk<VB>(lane, g);
   XRaw<VB, CH> raw;
   load_x_raw<VB, CH>(a.x, lane, raw);
   XSlice<VB, CH, HW> xs;
@@ -44,10 +45,11 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const uint8_t*
   int64_t r = r0;
   for (; r + 1 < r_end; r += 2) {
     WRow<VB, CH> g0, u0, g1, u1;
-    load_wrow<VB, CH>(g0, gate_w + r * K, gate_s + (r >> 7) * SC, lane);
-    load_wrow<VB, CH>(u0, up_w + r * K, up_s + (r >> 7) * SC, lane);
-    load_wrow<VB, CH>(g1, gate_w + (r + 1) * K, gate_s + ((r + 1) >> 7) * SC, lane);
-    load_wrow<VB, CH>(u1, up_w + (r + 1) * K, up_s + ((r + 1) >> 7) * SC, lane);
+    const int64_t o0 = group_row_base(r, K, g), o1 = group_row_base(r + 1, K, g);
+    load_wrow_walk<VB, CH>(g0, gate_w + o0, gate_s + (r >> 7) * SC, lane, walk);
+    load_wrow_walk<VB, CH>(u0, up_w + o0, up_s + (r >> 7) * SC, lane, walk);
+    load_wrow_walk<VB, CH>(g1, gate_w + o1, gate_s + ((r + 1) >> 7) * SC, lane, walk);
+    load_wrow_walk<VB, CH>(u1, up_w + o1, up_s + ((r + 1) >> 7) * SC, lane, walk);
     if (!packed) {
       pack_x_raw<VB, CH, HW>(raw, xs);
       packed = true;
@@ -61,8 +63,9 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const uint8_t*
   }
   if (r < r_end) {
     WRow<VB, CH> g0, u0;
-    load_wrow<VB, CH>(g0, gate_w + r * K, gate_s + (r >> 7) * SC, lane);
-    load_wrow<VB, CH>(u0, up_w + r * K, up_s + (r >> 7) * SC, lane);
+    const int64_t o0 = group_row_base(r, K, g);
+    load_wrow_walk<VB, CH>(g0, gate_w + o0, gate_s + (r >> 7) * SC, lane, walk);
+    load_wrow_walk<VB, CH>(u0, up_w + o0, up_s + (r >> 7) * SC, lane, walk);
     if (!packed) pack_x_raw<VB, CH, HW>(raw, xs);
     float tg0 = wave_sum(wrow_partial<VB, CH, HW>(g0, xs));
     float tu0 = wave_sum(wrow_partial<VB, CH, HW>(u0, xs));
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
     }
     const int64_t SR = (a.intermediate + kBlock - 1) / kBlock;
     gate_w = a.gate_up_weight + static_cast<int64_t>(e) * 2 * a.intermediate * K;
-    up_w = gate_w + a.intermediate * K;
+    up_w = gate_w + a.intermediate * K;  // row I: a whole number of row groups (I % 128 == 0 when g > 0)
     gate_s = a.gate_up_scale + static_cast<int64_t>(e) * 2 * SR * SC;
     up_s = gate_s + SR * SC;
   } else {
@@ -141,11 +144,12 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
   }
 
   const int64_t r_end = (r0 + a.rows_per_wave < rows) ? r0 + a.rows_per_wave : rows;
+  const int g = slot < slots_routed ? a.bank_group_log2 : 0;
   if (slot < slots_routed ? hw_decode_ok(a.routed_flags)
                            : (hw_decode_ok(a.shared_flags) && hw_decode_ok(a.shared_flags2)))
-    gate_up_rows<VB, CH, true>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, lane);
+    gate_up_rows<VB, CH, true>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, g, lane);
   else
-    gate_up_rows<VB, CH, false>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, lane);
+    gate_up_rows<VB, CH, false>(a, gate_w, up_w, gate_s, up_s, out, r0, r_end, g, lane);
 }
 
 // ------------------------------------- fused down + reduction + shared add --
@@ -162,9 +166,10 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
 template <int VB, int CH, bool HW>
 __device__ __forceinline__ void down_rows(const DownArgs& a, const uint8_t* __restrict__ w,
                                           const float* __restrict__ s, float* parked_row, int slot, int64_t h0,
-                                          int64_t h_end, int lane) {
+                                          int64_t h_end, int g, int lane) {
   const int64_t K = a.intermediate;
   const int64_t SC = (K + kBlock - 1) / kBlock;
+  const RowWalk walk = row_walk<VB>(lane, g);
   XRaw<VB, CH> raw;
   load_x_raw<VB, CH>(a.hidden_in + static_cast<int64_t>(slot) * K, lane, raw);
   XSlice<VB, CH, HW> xs;
@@ -173,7 +178,8 @@ __device__ __forceinline__ void down_rows(const DownArgs& a, const uint8_t* __re
     WRow<VB, CH> rowsv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (hb + j < h_end) load_wrow<VB, CH>(rowsv[j], w + (hb + j) * K, s + ((hb + j) >> 7) * SC, lane);
+      if (hb + j < h_end)
+        load_wrow_walk<VB, CH>(rowsv[j], w + group_row_base(hb + j, K, g), s + ((hb + j) >> 7) * SC, lane, walk);
     if (!packed) {
       pack_x_raw<VB, CH, HW>(raw, xs);
       packed = true;
@@ -217,10 +223,11 @@ __global__ __launch_bounds__(64 * (kMaxTopK + 1)) void down_reduce_kernel(DownAr
   }
   if (ok) {
     const int32_t* flag = slot < a.top_k ? a.routed_flags : a.shared_flags;
+    const int g = slot < a.top_k ? a.bank_group_log2 : 0;
     if (hw_decode_ok(flag))
-      down_rows<VB, CH, true>(a, w, s, parked[slot], slot, h0, h_end, lane);
+      down_rows<VB, CH, true>(a, w, s, parked[slot], slot, h0, h_end, g, lane);
     else
-      down_rows<VB, CH, false>(a, w, s, parked[slot], slot, h0, h_end, lane);
+      down_rows<VB, CH, false>(a, w, s, parked[slot], slot, h0, h_end, g, lane);
   } else {
     for (int64_t h = h0 + lane; h < h_end; h += 64) parked[slot][h - h0] = __builtin_nanf("");
   }
@@ -466,7 +473,6 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(GenericLinearArgs a
     w += static_cast<int64_t>(e) * a.w_expert_stride;
     s += static_cast<int64_t>(e) * a.s_expert_stride;
   }
-  w += a.w_row_offset * K;
   s += a.s_row_offset * a.s_cols;
   const uint16_t* xg = a.x + g * a.x_group_stride;
   for (int64_t m0 = 0; m0 < a.M; m0 += a.tile_rows) {
@@ -483,10 +489,10 @@ __global__ __launch_bounds__(256) void linear_generic_kernel(GenericLinearArgs a
       float acc[kGenericRows];
 #pragma unroll
       for (int m = 0; m < kGenericRows; ++m) acc[m] = 0.0f;
-      const uint8_t* wr = w + n * K;
+      const uint8_t* wr = w + group_row_base(a.w_row_offset + n, K, a.w_group_log2);
       const float* sr = s + (n >> 7) * a.s_cols;
       for (int64_t k = lane; k < K; k += 64) {
-        uint32_t b = wr[k];
+        uint32_t b = wr[group_col(k, a.w_group_log2)];
         float wv = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(
                        ((b & 0x7Fu) << 7) | ((b & 0x80u) << 8)))) * 256.0f * sr[k >> 7];
 #pragma unroll

@@ -61,6 +61,7 @@ struct GroupedGemmArgs {
   const uint8_t* weight;      // expert e rows at weight + e * w_expert_stride, [rows, K]
   const uint8_t* weight_up;   // SwiGLU mode: up rows, same strides
   int64_t w_expert_stride;
+  int w_group_log2;           // row groups of each expert matrix (common.h; 0 = row-major)
   const float* scale;         // expert e block scales, [ceil(rows/128), s_cols]
   const float* scale_up;
   int64_t s_expert_stride;
@@ -88,6 +89,7 @@ struct GroupedGemmArgs {
   const float* x_a_scale;
   const uint8_t* x_weight;
   const uint8_t* x_weight_up;
+  int x_w_group_log2;         // row groups of the dense problem's weights
   const float* x_scale;
   const float* x_scale_up;
   uint16_t* x_out;

@@ -509,6 +509,7 @@ struct ItemSource {
   int64_t experts;
   const uint8_t* weight;
   const uint8_t* weight_up;
+  int wg;  // row groups of the weight matrices (common.h)
   const float* scale;
   const float* scale_up;
   uint16_t* out;
@@ -621,12 +622,13 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
   const int half = wave & 1;
   const OperandSlots slots = operand_slots(lane);
   auto issue = [&](int64_t kb, int slot) {
-    const int64_t ko = kb * kBlock;
+    const int64_t ko = kb * kBlock;        // activation rows: row-major
+    const int64_t kw = kb << (7 + src.wg);  // weight rows: K block kb of the row group
     const uint32_t sb = lds_addr + slot * kStage + 2 * wave * kOperand;
-    lds_direct16(gb[0][0] + ko, sb);
-    lds_direct16(gb[0][1] + ko, sb + 1024);
-    lds_direct16(gb[1][0] + ko, sb + kOperand);
-    lds_direct16(gb[1][1] + ko, sb + kOperand + 1024);
+    lds_direct16(gb[0][0] + kw, sb);
+    lds_direct16(gb[0][1] + kw, sb + 1024);
+    lds_direct16(gb[1][0] + kw, sb + kOperand);
+    lds_direct16(gb[1][1] + kw, sb + kOperand + 1024);
     const uint32_t sa = lds_addr + slot * kStage + kStageB + GPW * wave * kOperand;
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
@@ -781,7 +783,8 @@ __device__ __forceinline__ void grouped_gemm_body(const GroupedGemmArgs& a, cons
       w = t < 4 ? src.weight : src.weight_up;
     }
     if (row >= a.N) row = a.N - 1;  // rows past the matrix: valid bytes, results never stored
-    return w + static_cast<int64_t>(expert) * a.w_expert_stride + row * K + load_piece_offset(lane, h);
+    return w + static_cast<int64_t>(expert) * a.w_expert_stride + group_row_base(row, K, src.wg) +
+           load_piece_offset(lane, h);
   };
   const uint8_t* gb[2][2];
 #pragma unroll
@@ -837,6 +840,7 @@ __device__ __forceinline__ ItemSource item_source(const GroupedGemmArgs& a, int6
   src.experts = dense ? 1 : a.experts;
   src.weight = dense ? a.x_weight : a.weight;
   src.weight_up = dense ? a.x_weight_up : a.weight_up;
+  src.wg = dense ? a.x_w_group_log2 : a.w_group_log2;
   src.scale = dense ? a.x_scale : a.scale;
   src.scale_up = dense ? a.x_scale_up : a.scale_up;
   src.out = dense ? a.x_out : a.out;
@@ -949,6 +953,7 @@ struct WideSources {
   const uint8_t* a_hi;
   const uint8_t* a_lo;
   int64_t K;
+  int32_t wg;              // row groups of wmat (common.h)
   int32_t rows;            // rows of the matrix (loads past it re-read the last row)
   int32_t row0;            // first row of the wavefront's tiles, + lane / 8
   int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 64)
@@ -970,7 +975,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       for (int h = 0; h < 2; ++h) {
         int32_t row = ls.row0 + 16 * q + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + static_cast<int64_t>(row) * ls.K + kb * kBlock + (ls.piece ^ (64 * h)),
+        lds_direct16(ls.wmat + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (64 * h)),
                      sb + q * kOperand + 1024 * h);
       }
   };
@@ -1093,6 +1098,7 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
     ls.row0 = static_cast<int32_t>(ntile * (MODE == GEMM_PLAIN ? kWidePlainRows : kWideGateRows)) + 16 * t0 + (lane >> 3);
     ls.rows = static_cast<int32_t>(a.N);
     ls.K = K;
+    ls.wg = src.wg;
     ls.piece = load_piece_offset(lane, 0);
     ls.a_hi = src.a_hi;
     ls.a_lo = src.a_lo;
@@ -1110,7 +1116,7 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
       for (int h = 0; h < 2; ++h) {
         int32_t row = ls.row0 + 16 * q + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + static_cast<int64_t>(row) * K + (ls.piece ^ (64 * h)), sb + q * kOperand + 1024 * h);
+        lds_direct16(ls.wmat + group_row_base(row, K, ls.wg) + (ls.piece ^ (64 * h)), sb + q * kOperand + 1024 * h);
       }
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + 2 * wave * kOperand;

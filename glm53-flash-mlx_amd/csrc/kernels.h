@@ -20,6 +20,7 @@ struct GateUpArgs {
   int64_t experts;
   const uint8_t* gate_up_weight;  // [E, 2I, H]
   const float* gate_up_scale;     // [E, 2*ceil(I/128), ceil(H/128)]
+  int bank_group_log2;            // row groups of gate_up_weight (common.h; 0 = row-major)
   const uint8_t* shared_gate_weight;  // [Is, H] or null
   const float* shared_gate_scale;
   const uint8_t* shared_up_weight;
@@ -51,6 +52,7 @@ struct DownArgs {
   int64_t experts;
   const uint8_t* down_weight;     // [E, H, I]
   const float* down_scale;        // [E, ceil(H/128), ceil(I/128)]
+  int bank_group_log2;            // row groups of down_weight (common.h; 0 = row-major)
   const uint8_t* shared_down_weight;  // [H, I] or null
   const float* shared_down_scale;
   int64_t hidden, intermediate;
@@ -83,6 +85,7 @@ struct StepArgs {
   const float* gate_up_scale;
   const uint8_t* down_weight;
   const float* down_scale;
+  int bank_group_log2;            // row groups of both bank matrices (common.h; 0 = row-major)
   const uint8_t* shared_gate_weight;  // null: no shared expert
   const float* shared_gate_scale;
   const uint8_t* shared_up_weight;
@@ -123,6 +126,7 @@ struct GenericLinearArgs {
   int64_t x_row_stride, x_group_stride;
   const uint8_t* weight;
   int64_t w_expert_stride, w_row_offset;
+  int w_group_log2;           // row groups of each expert matrix (common.h; 0 = row-major)
   const float* scale;
   int64_t s_expert_stride, s_row_offset, s_cols;
   const int32_t* expert_ids;  // [G] or null

@@ -126,9 +126,10 @@ __device__ __forceinline__ float half_chunk_dot(const u32x4& w, const HalfSlice<
   return acc;
 }
 
-// Rows [h0, h0 + 2 * PAIRS) of W [*, K = 512 CH] (row-major E4M3 with
-// 128 x 128 scales, SC = K / 128 per scale row; the rows must lie in one
-// 128-row scale block): half-wavefront `half` owns rows h0 + 2 j + half.
+// Rows [h0, h0 + 2 * PAIRS) of W [*, K = 512 CH] (E4M3 in row groups of
+// 2^g rows, common.h, with 128 x 128 scales, SC = K / 128 per scale row; the
+// rows must lie in one 128-row scale block): half-wavefront `half` owns rows
+// h0 + 2 j + half.
 // issue() puts every load in flight (weights and the block's scales in one
 // batch); finish() reduces, returning T(dot) of pair j in t[j][half] (valid
 // on lanes 0 and 32).
@@ -138,16 +139,19 @@ struct HalfRows {
   float sc[CH];
 
   __device__ __forceinline__ void issue(const uint8_t* __restrict__ w, const float* __restrict__ s, int64_t h0,
-                                        int lane) {
+                                        int lane, int g) {
     constexpr int64_t K = 512 * CH;
     constexpr int64_t SC = K / 128;
     const int half = lane >> 5, hl = lane & 31;
+    // half-lane hl's 16 bytes of chunk c: column 16 hl + 512 c
+    const int64_t lane_off = group_col(16 * hl, g), stride = int64_t{512} << g;
 #pragma unroll
-    for (int j = 0; j < PAIRS; ++j)
+    for (int j = 0; j < PAIRS; ++j) {
+      const uint8_t* row = w + group_row_base(h0 + 2 * j + half, K, g) + lane_off;
 #pragma unroll
       for (int c = 0; c < CH; ++c)
-        q[j][c] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(w + (h0 + 2 * j + half) * K + 16 * hl + 512 * c));
+        q[j][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + c * stride));
+    }
 #pragma unroll
     for (int c = 0; c < CH; ++c) sc[c] = s[(h0 >> 7) * SC + ((16 * hl + 512 * c) >> 7)];
   }
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(256) void step_gate_up_kernel(StepArgs a) {
     HalfRaw<CHI> raw;
     load_half_raw<CHI>(a.hidden_act + static_cast<int64_t>(a.top_k) * I, lane & 31, raw);
     HalfRows<CHI, 8> rows;
-    rows.issue(a.shared_down_weight, a.shared_down_scale, h0, lane);
+    rows.issue(a.shared_down_weight, a.shared_down_scale, h0, lane, 0);
     auto run = [&](auto hw) {
       constexpr bool HW = decltype(hw)::value;
       HalfSlice<CHI, HW> xs;
@@ -346,6 +350,8 @@ __global__ __launch_bounds__(256) void step_gate_up_kernel(StepArgs a) {
   const int64_t u_end = (gw + 1) * units / waves;
   if (u_begin >= u_end) return;
   const int64_t K = a.hidden, SC = K / kBlock, SR = I / kBlock;
+  const int g = a.bank_group_log2;
+  const RowWalk walk = row_walk<VBH>(lane, g);
   auto unit_ptrs = [&](int64_t u, const uint8_t*& gw_row, const uint8_t*& uw_row, const float*& gs, const float*& us,
                        int64_t& out_index, bool& ok) {
     const int slot = static_cast<int>(u / I);
@@ -355,8 +361,8 @@ __global__ __launch_bounds__(256) void step_gate_up_kernel(StepArgs a) {
     ok = e >= 0 && e < a.experts;
     const int64_t ee = ok ? e : 0;
     const uint8_t* base = a.gate_up_weight + ee * 2 * I * K;
-    gw_row = base + r * K;
-    uw_row = base + (I + r) * K;
+    gw_row = base + group_row_base(r, K, g);
+    uw_row = gw_row + I * K;  // up row I + r: I is a whole number of row groups
     const float* sbase = a.gate_up_scale + ee * 2 * SR * SC;
     gs = sbase + (r >> 7) * SC;
     us = sbase + (SR + (r >> 7)) * SC;
@@ -369,11 +375,11 @@ __global__ __launch_bounds__(256) void step_gate_up_kernel(StepArgs a) {
     const float *gsa, *usa, *gsb, *usb;
     int64_t oa, ob;
     bool oka, okb;
-    auto load = [&](GateUpUnit<VBH, CHH>& U, const uint8_t* g, const uint8_t* up, const float* gs, const float* us,
+    auto load = [&](GateUpUnit<VBH, CHH>& U, const uint8_t* gr, const uint8_t* up, const float* gs, const float* us,
                     bool ok) {
       if (ok) {
-        load_wrow<VBH, CHH>(U.g, g, gs, lane);
-        load_wrow<VBH, CHH>(U.u, up, us, lane);
+        load_wrow_walk<VBH, CHH>(U.g, gr, gs, lane, walk);
+        load_wrow_walk<VBH, CHH>(U.u, up, us, lane, walk);
       }
     };
     auto finish = [&](const GateUpUnit<VBH, CHH>& U, int64_t o, bool ok) {
@@ -434,7 +440,7 @@ __global__ __launch_bounds__(512) void step_down_kernel(StepArgs a) {
       HalfRaw<CHI> raw;
       load_half_raw<CHI>(a.hidden_act + static_cast<int64_t>(slot) * I, lane & 31, raw);
       HalfRows<CHI, 8> rows;
-      rows.issue(w, s, h0, lane);
+      rows.issue(w, s, h0, lane, a.bank_group_log2);
       auto run = [&](auto hw) {
         constexpr bool HW = decltype(hw)::value;
         HalfSlice<CHI, HW> xs;

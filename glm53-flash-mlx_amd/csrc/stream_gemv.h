@@ -152,6 +152,31 @@ __device__ __forceinline__ void load_wrow(WRow<VB, CH>& r, const uint8_t* __rest
   for (int c = 0; c < CH; ++c) r.s[c] = srow[(VB * lane + 64 * VB * c) >> 7];
 }
 
+// Where a lane's chunks of one row lie in a matrix of row groups of 2^g rows
+// (common.h): chunk c at lane_off + c * stride bytes from the row's base
+// group_row_base(n, K, g).  A lane's VB bytes never straddle a 128-byte
+// block (VB divides 128) and a chunk spans 64 VB bytes, a multiple of 128,
+// so the offsets split into a lane part and a chunk part.
+struct RowWalk {
+  int32_t lane_off;
+  int32_t stride;
+};
+
+template <int VB>
+__device__ __forceinline__ RowWalk row_walk(int lane, int g) {
+  static_assert(VB >= 2 && 128 % VB == 0, "a lane's bytes stay inside one 128-byte block");
+  return {static_cast<int32_t>(group_col(VB * lane, g)), (64 * VB) << g};
+}
+
+template <int VB, int CH>
+__device__ __forceinline__ void load_wrow_walk(WRow<VB, CH>& r, const uint8_t* __restrict__ row,
+                                               const float* __restrict__ srow, int lane, RowWalk walk) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) r.c[c].load(row + walk.lane_off + c * walk.stride);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) r.s[c] = srow[(VB * lane + 64 * VB * c) >> 7];
+}
+
 template <int VB, int CH, bool HW>
 __device__ __forceinline__ float wrow_partial(const WRow<VB, CH>& r, const XSlice<VB, CH, HW>& xs) {
   float acc = 0.0f;

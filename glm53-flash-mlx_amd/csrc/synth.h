@@ -15,6 +15,7 @@ struct SynthFp8Args {
   int64_t batch;            // matrices
   int64_t codes_stride;     // bytes between matrices
   int64_t scale_stride;     // floats between matrices
+  int group_log2;           // code layout: row groups of 2^group_log2 rows (common.h; 0 = row-major)
 };
 
 hipError_t launch_synth_fp8(const SynthFp8Args& a, hipStream_t st);

@@ -26,8 +26,9 @@ from .router import Float32Gate
 
 
 class _PackedLinearView:
-    """One projection of one bank expert; row slices of a contiguous bank are
-    themselves contiguous, so no copy is made."""
+    """One projection of one bank expert.  In a row-major bank its rows are a
+    contiguous slice (no copy); in a row-group bank `weight` returns the
+    expert's rows re-laid into the reference row-major layout (a copy)."""
 
     def __init__(self, weight, scale_inv, *, expert_id: int, row_offset: int, scale_row_offset: int,
                  out_features: int, bank=None):
@@ -41,6 +42,9 @@ class _PackedLinearView:
 
     @property
     def weight(self):
+        if self._bank is not None and self._bank.row_group_log2 != 0:
+            rows = _reference_rows(self._bank_weight[self.expert_id:self.expert_id + 1], self._bank.row_group_log2)
+            return rows[0, self.row_offset:self.row_offset + self.out_features]
         return self._bank_weight[self.expert_id, self.row_offset:self.row_offset + self.out_features]
 
     @property
@@ -72,10 +76,40 @@ class _PackedExpertView:
 
 
 def _bank_lease(value, name: str) -> ResidentTensor:
-    if isinstance(value, torch.Tensor):
-        raise TypeError(f"{name}: resident tensors require an explicit TensorLease; bare arrays have no storage "
-                        "lifetime contract (wrap with ownership.owned_tensor or borrowed_stable_tensor)")
-    return require_resident(value)
+    try:
+        return require_resident(value)
+    except TypeError as exc:
+        raise TypeError(f"PackedFP8ExpertBank {name}: {exc}") from None
+
+
+LAYOUTS = {"rows": N.ROWS_LAYOUT, "tiled": N.TILED_LAYOUT}
+# The layout the package's own banks are built in (pack, the synthetic and
+# checkpoint loaders).  Row-major: on MI355X the batch-1 decode step, the
+# headline workload, streams it 0.6-1.4 us per layer faster than any row-group
+# layout (41.75 against 42.36-43.12 us at 16-row to 2-row groups), which
+# outweighs the grouped prefill's 1-3% gain from 4- or 8-row groups.
+DEFAULT_LAYOUT = "rows"
+
+
+def _layout_log2(layout, hidden: int, intermediate: int) -> int:
+    """Row-group exponent of a bank layout name ("rows", "tiled") or an
+    explicit exponent 0..7 (glm53_bank.row_group_log2)."""
+    g = LAYOUTS.get(layout, layout) if isinstance(layout, str) else layout
+    if not isinstance(g, int) or isinstance(g, bool) or not 0 <= g <= N.MAX_ROW_GROUP_LOG2:
+        raise ValueError(f"bank layout must be one of {sorted(LAYOUTS)} or a row-group exponent 0..."
+                         f"{N.MAX_ROW_GROUP_LOG2}, got {layout!r}")
+    if g and (hidden % BLOCK_SIZE or intermediate % BLOCK_SIZE):
+        raise ValueError(f"a row-group bank layout needs hidden and intermediate multiples of {BLOCK_SIZE}, got "
+                         f"hidden={hidden}, intermediate={intermediate}")
+    return g
+
+
+def _reference_rows(weight: torch.Tensor, g: int) -> torch.Tensor:
+    """uint8 [E, rows, cols] expert matrices in row groups of 2^g rows,
+    re-laid into the reference row-major layout (a new tensor)."""
+    out = torch.empty_like(weight)
+    N.relayout(weight.contiguous(), out, g, N.ROWS_LAYOUT)
+    return out
 
 
 class PackedFP8ExpertBank(torch.nn.Module):
@@ -88,9 +122,21 @@ class PackedFP8ExpertBank(torch.nn.Module):
     borrowed-stable with its owner kept referenced by the bank; an
     ephemeral lease or a bare tensor is refused, because native plans and
     captured graphs keep the bank's device pointers.
+
+    `layout` names how the two weight tensors hold each expert matrix:
+    "rows" (the default) is the reference's row-major layout, the
+    checkpoint's and the import / export format; "tiled" holds row groups
+    of 16 rows whose K span is stored as consecutive 16-row x 128-byte
+    blocks, and an integer g any row-group size 2^g (glm53_moe.h,
+    glm53_bank).  Every entry point reads every layout with the same bits.
+    ``pack``, the synthetic banks and the checkpoint loader build
+    DEFAULT_LAYOUT banks unless told otherwise; ``relayout_`` converts an
+    owned bank in place and ``reference_weights`` exports the row-major
+    bytes.  The tensor shapes and block scales are the same in all layouts.
     """
 
-    def __init__(self, gate_up_weight, gate_up_scale_inv, down_weight, down_scale_inv, *, intermediate_size: int):
+    def __init__(self, gate_up_weight, gate_up_scale_inv, down_weight, down_scale_inv, *, intermediate_size: int,
+                 layout="rows"):
         super().__init__()
         names = ("gate_up_weight", "gate_up_scale_inv", "down_weight", "down_scale_inv")
         resident = {n: _bank_lease(v, n) for n, v in zip(names, (gate_up_weight, gate_up_scale_inv, down_weight,
@@ -106,9 +152,9 @@ class PackedFP8ExpertBank(torch.nn.Module):
         inter = int(intermediate_size)
         n_exp, _, hidden = values["gate_up_weight"].shape
         ri, rh = math.ceil(inter / BLOCK_SIZE), math.ceil(hidden / BLOCK_SIZE)
-        layout = {"gate_up_weight": (n_exp, 2 * inter, hidden), "gate_up_scale_inv": (n_exp, 2 * ri, rh),
+        shapes = {"gate_up_weight": (n_exp, 2 * inter, hidden), "gate_up_scale_inv": (n_exp, 2 * ri, rh),
                   "down_weight": (n_exp, hidden, inter), "down_scale_inv": (n_exp, rh, ri)}
-        wrong = [f"{n} {tuple(values[n].shape)} (want {shape})" for n, shape in layout.items()
+        wrong = [f"{n} {tuple(values[n].shape)} (want {shape})" for n, shape in shapes.items()
                  if tuple(values[n].shape) != shape]
         if wrong:
             raise ValueError("bank layout mismatch: " + "; ".join(wrong))
@@ -118,16 +164,63 @@ class PackedFP8ExpertBank(torch.nn.Module):
             self.register_buffer(n, v)
         self.storage_contracts = {n: storage_descriptor(r) for n, r in resident.items()}
         self._storage_owners = tuple(r.owner for r in resident.values() if r.owner is not None)
+        self._weights_writable = all(resident[n].writable for n in ("gate_up_weight", "down_weight"))
         self.intermediate_size = inter
         self.intermediate_scale_rows = ri
+        self.row_group_log2 = _layout_log2(layout, hidden, inter)
+
+    @property
+    def layout(self) -> str:
+        """"rows", "tiled", or "groups<n>" for another row-group size."""
+        names = {g: n for n, g in LAYOUTS.items()}
+        return names.get(self.row_group_log2, f"groups{1 << self.row_group_log2}")
+
+    def relayout_(self, layout="tiled") -> "PackedFP8ExpertBank":
+        """Re-lay both weight tensors in place into `layout` ("rows",
+        "tiled" or a row-group exponent).  Only owned weights are rewritten:
+        a borrowed lease's storage belongs to its owner.  Runs on the current
+        stream through a staging copy of at most 256 MB at a time; plans and
+        graphs made with the old layout must not run afterwards (the layout
+        is part of every call's bank descriptor)."""
+        target = _layout_log2(layout, self.hidden_size, self.intermediate_size)
+        if target == self.row_group_log2:
+            return self
+        if not self._weights_writable:
+            raise ValueError("relayout_() rewrites the weights in place, but this bank borrows them; build it from "
+                             "owned leases (or materialize_owned copies) to re-lay it")
+        for name in ("gate_up_weight", "down_weight"):
+            weight = getattr(self, name)
+            per_expert = weight[0].numel()
+            step = max(1, (256 << 20) // per_expert)
+            for e0 in range(0, weight.shape[0], step):
+                part = weight[e0:e0 + step]
+                N.relayout(part.clone(), part, self.row_group_log2, target)
+        self.row_group_log2 = target
+        return self
+
+    def reference_weights(self, expert_ids=None) -> tuple[torch.Tensor, torch.Tensor]:
+        """(gate_up_weight, down_weight) of the experts `expert_ids` (all by
+        default) in the reference row-major layout: the tensors themselves
+        (or an index_select) for a row-major bank, a re-laid copy for a
+        row-group bank."""
+        gu, dw = self.gate_up_weight, self.down_weight
+        if expert_ids is not None:
+            idx = torch.as_tensor(expert_ids, dtype=torch.int64, device=gu.device).reshape(-1)
+            gu, dw = gu.index_select(0, idx), dw.index_select(0, idx)
+        if self.row_group_log2 == 0:
+            return gu, dw
+        return _reference_rows(gu, self.row_group_log2), _reference_rows(dw, self.row_group_log2)
 
     @classmethod
-    def pack(cls, experts) -> "PackedFP8ExpertBank":
+    def pack(cls, experts, *, layout=None) -> "PackedFP8ExpertBank":
         """Stack separate experts (each with gate_proj / up_proj / down_proj
         block-FP8 linears) into one owned bank, expert-major, gate rows
-        before up rows (packed.py:782-850 layout).  Every projection must
-        keep uint8 E4M3 weights and float32 block scales of one shape per
-        projection kind."""
+        before up rows (packed.py:782-850), then re-lay it on the device
+        into `layout` (DEFAULT_LAYOUT when None; "rows" is the reference
+        layout; a bank in host memory, or of a shape whose hidden or
+        intermediate width is not a multiple of 128, stays row-major).
+        Every projection must keep uint8 E4M3 weights and float32 block
+        scales of one shape per projection kind."""
         experts = list(experts)
         if not experts:
             raise ValueError("pack() needs at least one expert")
@@ -148,9 +241,13 @@ class PackedFP8ExpertBank(torch.nn.Module):
             flat = resident_concatenate(parts, axis=0).value
             return owned_tensor(flat.view(len(experts), -1, flat.shape[-1]), layout=TensorLayout.ROW_MAJOR_CONTIGUOUS)
 
-        return cls(stack(("gate_proj", "up_proj"), "weight"), stack(("gate_proj", "up_proj"), "weight_scale_inv"),
+        bank = cls(stack(("gate_proj", "up_proj"), "weight"), stack(("gate_proj", "up_proj"), "weight_scale_inv"),
                    stack(("down_proj",), "weight"), stack(("down_proj",), "weight_scale_inv"),
                    intermediate_size=inter)
+        layout = DEFAULT_LAYOUT if layout is None else layout
+        if layout != "rows" and bank.gate_up_weight.is_cuda and hidden % BLOCK_SIZE == 0 and inter % BLOCK_SIZE == 0:
+            bank.relayout_(layout)
+        return bank
 
     @property
     def expert_count(self) -> int:
@@ -185,13 +282,13 @@ class PackedFP8ExpertBank(torch.nn.Module):
     def as_c_struct(self) -> N.Bank:
         return N.Bank(self.gate_up_weight.data_ptr(), self.gate_up_scale_inv.data_ptr(), self.down_weight.data_ptr(),
                       self.down_scale_inv.data_ptr(), self.expert_count, self.hidden_size, self.intermediate_size,
-                      self.code_flags().data_ptr())
+                      self.code_flags().data_ptr(), self.row_group_log2)
 
 
 class BankHandle:
-    """Native bank handle (glm53_bank_create): the bank's reference layout
-    validated once and its 0x7F/0xFF code flag scanned once and owned by the
-    handle.  `ptr` is a `glm53_bank*` for the C ABI's entry points; the bank
+    """Native bank handle (glm53_bank_create): the bank's descriptor (either
+    layout) validated once and its 0x7F/0xFF code flag scanned once and owned
+    by the handle.  `ptr` is a `glm53_bank*` for the C ABI's entry points; the bank
     object (and so its weights) stays referenced while the handle lives."""
 
     def __init__(self, bank: "PackedFP8ExpertBank", device: torch.device | None = None):
@@ -394,7 +491,8 @@ class DecodePlan:
             flags += [shared.gate_proj.code_flags(), shared.up_proj.code_flags(), shared.down_proj.code_flags()]
         tensors = self._bound_tensors(bank, shared, router)
         # the weight objects, the bound tensors and the scanned flag tensors the plan points at stay referenced
-        self._bound = ((bank, shared, router, flags), tensors, [(t.data_ptr(), t._version) for t in tensors])
+        self._bound = ((bank, shared, router, flags), tensors, [(t.data_ptr(), t._version) for t in tensors],
+                       bank.row_group_log2)
 
     def _check_bound(self):
         if self._bound is None:
@@ -402,6 +500,17 @@ class DecodePlan:
         tensors = self._bound_tensors(*self._bound[0][:3])  # what the weight objects hold now
         if [(t.data_ptr(), t._version) for t in tensors] != self._bound[2]:
             raise RuntimeError("decode plan bound weight identity changed")
+        if self._bound[0][0].row_group_log2 != self._bound[3]:
+            raise RuntimeError("the bound bank was re-laid since binding; bind a new plan")
+
+    def _check_x(self, x, who: str) -> None:
+        """x must be BF16 on the bound weights' device (the kernels read its
+        bytes as BF16 there)."""
+        if x.dtype != torch.bfloat16:
+            raise ValueError(f"{who}: x must be bfloat16, got {x.dtype}")
+        device = self._bound[1][0].device
+        if x.device != device:
+            raise ValueError(f"{who}: x is on {x.device} but the bound weights are on {device}")
 
     def _out_for(self, x, out):
         if out is not None:
@@ -419,6 +528,7 @@ class DecodePlan:
         modified in place since binding."""
         self._check_bound()
         N.require_device(x, expert_ids, scores)
+        self._check_x(x, "execute_bound")
         flat = x.reshape(-1)
         ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
         sc = scores.reshape(-1).to(torch.float32).contiguous()
@@ -436,6 +546,7 @@ class DecodePlan:
         if self._bound[0][2] is None:
             raise RuntimeError("decode plan was bound without a router")
         N.require_device(x)
+        self._check_x(x, "execute_bound_router")
         flat = x.reshape(-1)
         if flat.numel() != self.hidden_size:
             raise ValueError(f"execute_bound_router expects x [{self.hidden_size}]")
@@ -479,8 +590,11 @@ class RoutedDiagnostic:
             self._lib.glm53_routed_diagnostic_destroy(handle)
             self.handle = None
 
-    def execute(self, x, expert_ids, gate_up_weight, gate_up_scale_inv) -> torch.Tensor:
+    def execute(self, x, expert_ids, gate_up_weight, gate_up_scale_inv, *, layout="rows") -> torch.Tensor:
+        """`layout`: that of gate_up_weight ("rows" for the reference's raw
+        arrays; a bank's own ``layout`` when passing its tensors)."""
         N.require_device(x, expert_ids, gate_up_weight, gate_up_scale_inv)
+        g = _layout_log2(layout, self.hidden_size, self.intermediate_size)
         flat = x.reshape(-1).contiguous()
         ids = expert_ids.reshape(-1).to(torch.int32).contiguous()
         if flat.numel() != self.hidden_size or ids.numel() != self.top_k:
@@ -490,7 +604,7 @@ class RoutedDiagnostic:
             raise ValueError("gate_up_weight must be uint8 [E, 2I, H]")
         N.check(self._lib.glm53_routed_diagnostic_execute(self.handle, N.ptr(flat), N.ptr(ids),
                                                           N.ptr(gate_up_weight.contiguous()),
-                                                          N.ptr(gate_up_scale_inv.contiguous()),
+                                                          N.ptr(gate_up_scale_inv.contiguous()), g,
                                                           N.stream_handle(x.device)))
         return self.hidden
 

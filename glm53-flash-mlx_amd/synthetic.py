@@ -17,7 +17,7 @@ import torch
 from . import _native as N
 from .fp8 import BLOCK_SIZE, ClampedMLP
 from .ownership import TensorLayout, owned_tensor
-from .packed import PackedFP8ExpertBank
+from .packed import DEFAULT_LAYOUT, PackedFP8ExpertBank
 from .router import Float32Gate
 
 _MASK = (1 << 64) - 1
@@ -69,7 +69,15 @@ def normal_bf16(shape, seed: int, std: float = 1.0, device="cuda") -> torch.Tens
 
 
 def synth_bank(experts: int, hidden: int, intermediate: int, seed: int, layer: int = 0,
-               device="cuda", std: float = 0.02) -> PackedFP8ExpertBank:
+               device="cuda", std: float = 0.02, layout=None) -> PackedFP8ExpertBank:
+    """A seeded bank written straight into `layout` (the package's
+    DEFAULT_LAYOUT when None, "rows", "tiled" or a row-group exponent;
+    shapes whose widths are not multiples of 128 are always row-major).  The
+    expert values do not depend on the layout."""
+    layout = DEFAULT_LAYOUT if layout is None else layout
+    if hidden % BLOCK_SIZE or intermediate % BLOCK_SIZE:
+        layout = "rows"
+    g = {"rows": N.ROWS_LAYOUT, "tiled": N.TILED_LAYOUT}.get(layout, layout)
     sr, sh = math.ceil(intermediate / BLOCK_SIZE), math.ceil(hidden / BLOCK_SIZE)
     gu = torch.empty((experts, 2 * intermediate, hidden), dtype=torch.uint8, device=device)
     gus = torch.empty((experts, 2 * sr, sh), dtype=torch.float32, device=device)
@@ -79,16 +87,19 @@ def synth_bank(experts: int, hidden: int, intermediate: int, seed: int, layer: i
     stream = N.stream_handle(gu.device)
     # one launch per projection over all experts; expert e of a projection
     # draws from the key derived from (projection key, e)
+    # (the up rows start at row I, a whole number of row groups, so the up
+    # matrix is written at byte offset I * H in either layout)
     N.check(lib.glm53_synth_fp8_batched(N.ptr(gu), N.ptr(gus), intermediate, hidden, experts,
-                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "gate"), std, stream))
+                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "gate"), std, g,
+                                        stream))
     N.check(lib.glm53_synth_fp8_batched(N.ctypes.c_void_p(gu.data_ptr() + intermediate * hidden),
                                         N.ctypes.c_void_p(gus.data_ptr() + 4 * sr * sh), intermediate, hidden, experts,
-                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "up"), std, stream))
+                                        2 * intermediate * hidden, 2 * sr * sh, key(seed, layer, "up"), std, g, stream))
     N.check(lib.glm53_synth_fp8_batched(N.ptr(dw), N.ptr(dws), hidden, intermediate, experts, hidden * intermediate,
-                                        sh * sr, key(seed, layer, "down"), std, stream))
+                                        sh * sr, key(seed, layer, "down"), std, g, stream))
     rm = TensorLayout.ROW_MAJOR_CONTIGUOUS
     return PackedFP8ExpertBank(owned_tensor(gu, layout=rm), owned_tensor(gus, layout=rm), owned_tensor(dw, layout=rm),
-                               owned_tensor(dws, layout=rm), intermediate_size=intermediate)
+                               owned_tensor(dws, layout=rm), intermediate_size=intermediate, layout=g)
 
 
 def synth_shared(hidden: int, intermediate: int, limit: float, seed: int, layer: int = 0, device="cuda",
@@ -114,9 +125,11 @@ def layer_config(hidden=4096, intermediate=1536, experts=288, top_k=8, limit=10.
                            n_routed_experts=experts, num_experts_per_tok=top_k, n_shared_experts=shared)
 
 
-def synth_layer(config, seed: int, layer: int = 0, device="cuda", bias: torch.Tensor | None = None):
+def synth_layer(config, seed: int, layer: int = 0, device="cuda", bias: torch.Tensor | None = None,
+                layout=None):
     """(bank, shared expert, gate) of one synthetic MoE layer."""
-    bank = synth_bank(config.n_routed_experts, config.hidden_size, config.moe_intermediate_size, seed, layer, device)
+    bank = synth_bank(config.n_routed_experts, config.hidden_size, config.moe_intermediate_size, seed, layer, device,
+                      layout=layout)
     shared = None
     if config.n_shared_experts:
         shared = synth_shared(config.hidden_size, config.moe_intermediate_size * config.n_shared_experts,

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define GLM53_ABI_VERSION 1
+#define GLM53_ABI_VERSION 2
 
 #define GLM53_OK 0
 #define GLM53_INVALID_ARGUMENT 1
@@ -43,11 +43,27 @@ extern "C" {
 #define GLM53_REDUCE_GROUPED 0 /* FP32 slot order, grouped_fp8.py:273-276 */
 #define GLM53_REDUCE_DIRECT 1  /* BF16 ascending expert, fp8.py:384-397 */
 
-/* Packed per-layer expert bank, reference layout (packed.py:782-850):
+/* Packed per-layer expert bank (packed.py:782-850):
  *   gate_up_weight    u8  [E, 2I, H]  rows 0..I-1 gate, I..2I-1 up
  *   gate_up_scale_inv f32 [E, 2*ceil(I/128), ceil(H/128)]  (up from row ceil(I/128))
  *   down_weight       u8  [E, H, I]
- *   down_scale_inv    f32 [E, ceil(H/128), ceil(I/128)]                      */
+ *   down_scale_inv    f32 [E, ceil(H/128), ceil(I/128)]
+ * Each expert matrix [N, K] of the two weight tensors is stored in the
+ * layout row_group_log2 = g names:
+ *   g = 0      row-major, byte (n, k) at n K + k: the reference's layout and
+ *              the checkpoint's, the import / export format;
+ *   g = 1..7   row groups (needs H % 128 == 0 and I % 128 == 0): the 2^g
+ *              rows of group n >> g are stored together, their K span as K /
+ *              128 consecutive blocks of 2^g rows x 128 bytes, so byte (n, k)
+ *              sits at (n >> g) 2^g K + (k >> 7) 2^g 128 + (n mod 2^g) 128 +
+ *              k mod 128.  A 128-row MFMA weight stage of the grouped GEMM
+ *              then reads 128 / 2^g contiguous runs instead of 128 lines,
+ *              and a row group's K span is one contiguous run for the decode
+ *              GEMV.  GLM53_TILED_ROW_GROUP_LOG2 is the layout the library's
+ *              own banks use.
+ * Block scales have one layout (as above) whatever g is.                     */
+#define GLM53_MAX_ROW_GROUP_LOG2 7
+#define GLM53_TILED_ROW_GROUP_LOG2 4
 typedef struct glm53_bank {
   const uint8_t* gate_up_weight;
   const float* gate_up_scale_inv;
@@ -59,21 +75,41 @@ typedef struct glm53_bank {
   /* device int32, nonzero when the weights hold E4M3 codes 0x7F / 0xFF
    * (glm53_e4m3_scan_codes); NULL makes every prefill call scan the bank */
   const int32_t* code_flags;
+  int32_t row_group_log2; /* weight layout, above (0 = reference row-major) */
 } glm53_bank;
 
 /* Bank handle -- the native side of PackedFP8ExpertBank(...)
- * (packed.py:747-876).  Validates the reference layout in `desc` (pointers,
- * dimensions, 16-byte aligned weights), copies it, and owns a device code
- * flag: both weight tensors are scanned once on `stream` for E4M3 codes
- * 0x7F / 0xFF, so calls made with the handle never scan again (desc's own
- * code_flags is ignored).  The layout is consumed as it is -- every kernel
- * reads the [rows, K] row-major weights with whole 128-byte lines -- so no
- * re-laid copy is made.  Weights stay borrowed: the caller keeps them alive
- * and unchanged while the handle is in use.  The returned pointer is used
- * wherever a `const glm53_bank*` is taken; destroy it (which frees the flag)
- * only after the work that uses it has completed. */
+ * (packed.py:747-876).  Validates `desc` (pointers, dimensions, layout,
+ * 16-byte aligned weights), copies it, and owns a device code flag: both
+ * weight tensors are scanned once on `stream` for E4M3 codes 0x7F / 0xFF, so
+ * calls made with the handle never scan again (desc's own code_flags is
+ * ignored).  Weights stay borrowed, in the layout desc names: the caller
+ * keeps them alive and unchanged while the handle is in use.  The returned
+ * pointer is used wherever a `const glm53_bank*` is taken; destroy it (which
+ * frees what the handle owns) only after the work that uses it has
+ * completed. */
 int glm53_bank_create(const glm53_bank* desc, void* stream, glm53_bank** out);
+
+/* Bank import (PackedFP8ExpertBank.pack, packed.py:782-850, with the re-lay
+ * of this build): allocates device buffers owned by the handle, copies the
+ * bank of `desc` (any layout, usually the reference row-major one) into
+ * them re-laid as row_group_log2 (GLM53_TILED_ROW_GROUP_LOG2 for the
+ * library's layout), copies the block scales, scans the codes, and waits for
+ * `stream`, so the caller may free desc's buffers when this returns.  Costs
+ * one bank of device memory (5.44 GB at H = 4096, I = 1536, E = 288) beside
+ * the caller's copy until that is freed. */
+int glm53_bank_import(const glm53_bank* desc, int32_t row_group_log2, void* stream, glm53_bank** out);
 void glm53_bank_destroy(glm53_bank* bank);
+
+/* Out-of-place re-lay of `matrices` consecutive E4M3 matrices [rows, cols]
+ * (rows * cols bytes apart) from the layout from_log2 to the layout to_log2
+ * (glm53_bank): the bank import above, and its export back to the
+ * reference layout (to_log2 = 0).  Needs (rows * cols) % 16 == 0, 16-byte
+ * aligned, non-overlapping buffers, and for a row-group layout cols % 128 ==
+ * 0 and rows a multiple of the group.  HBM-bound: each byte read and written
+ * once. */
+int glm53_relayout_weights(const uint8_t* src, uint8_t* dst, int64_t matrices, int64_t rows, int64_t cols,
+                           int32_t from_log2, int32_t to_log2, void* stream);
 
 /* One BlockFP8Linear (fp8.py:302-326): weight u8 [out, in], scale
  * f32 [ceil(out/128), ceil(in/128)]. */
@@ -267,7 +303,8 @@ int glm53_decode_plan_identities(const glm53_decode_plan* plan, int32_t which, u
  * `NativePackedMoERoutedDiagnostic` (bindings.cpp:634-649): one decode's
  * routed gate/up/SwiGLU boundary with every stage kept, for localising
  * numerics.  execute(x bf16 [H], expert_ids int32 [top_k], the bank's
- * gate_up_weight u8 [E, 2I, H] and gate_up_scale_inv) fills five bf16
+ * gate_up_weight u8 [E, 2I, H] in the layout row_group_log2 (glm53_bank)
+ * and gate_up_scale_inv) fills five bf16
  * [top_k, I] stages owned by the object (fixed addresses from creation):
  * 0 gate = T(x . W_gate[e]^T), 1 up = T(x . W_up[e]^T), 2 sigmoid =
  * T(sigmoid(g')), 3 silu = T(g' * sigmoid), 4 hidden = T(silu * u') with
@@ -281,7 +318,7 @@ int glm53_routed_diagnostic_create(int64_t hidden, int64_t intermediate, int64_t
 void glm53_routed_diagnostic_destroy(glm53_routed_diagnostic* diag);
 int glm53_routed_diagnostic_execute(glm53_routed_diagnostic* diag, const void* x, const int32_t* expert_ids,
                                     const uint8_t* gate_up_weight, const float* gate_up_scale_inv,
-                                    void* stream);
+                                    int32_t row_group_log2, void* stream);
 int glm53_routed_diagnostic_stage(glm53_routed_diagnostic* diag, int32_t which, void** ptr, size_t* bytes);
 int glm53_routed_diagnostic_counters(const glm53_routed_diagnostic* diag, uint64_t* execution_count,
                                      uint64_t* scratch_bytes);
@@ -294,9 +331,11 @@ int glm53_routed_diagnostic_counters(const glm53_routed_diagnostic* diag, uint64
  * and residual), the same kernels and bits as the plan form.  It calls no
  * hipMalloc / hipFree: its scratch is a static device array of
  * GLM53_DECODE_STATIC_SCRATCH_BYTES, one copy per GPU held until the process
- * ends; the first call on a GPU looks up that copy's address and clears it
- * with a fill kernel on `stream` (make that first call outside graph capture
- * to keep the clear out of the graph).  Limits: the fused step shapes
+ * ends; the first call on a GPU looks up that copy's address, clears it
+ * with a fill kernel on `stream` and waits for the clear, so calls on any
+ * stream of that GPU start from it (make that first call outside graph
+ * capture: it synchronises `stream`).  `stream` must belong to the current
+ * device (GLM53_INVALID_ARGUMENT otherwise).  Limits: the fused step shapes
  * (H, I) in {(4096, 1536), (4096, 2048), (7168, 2048), (6144, 2048),
  * (2048, 1024), (2048, 1536), (1024, 512), (1024, 1024)}, at most 320
  * experts, top_k <= 8, a shared expert (if any) of width I, 16-byte aligned
@@ -446,10 +485,12 @@ int glm53_synth_f32(float* out, int64_t n, uint64_t seed, float std, float lo, f
                     int32_t uniform, void* stream);
 int glm53_synth_bf16(void* out, int64_t n, uint64_t seed, float std, void* stream);
 /* batch matrices at codes + b * codes_stride / scale_inv + b * scale_stride;
- * matrix b draws from a key derived from (seed, b), matrix 0 from seed. */
+ * matrix b draws from a key derived from (seed, b), matrix 0 from seed.  The
+ * codes are written in the layout row_group_log2 (glm53_bank); the values
+ * do not depend on it. */
 int glm53_synth_fp8_batched(uint8_t* codes, float* scale_inv, int64_t rows, int64_t cols, int64_t batch,
                             int64_t codes_stride, int64_t scale_stride, uint64_t seed, float std,
-                            void* stream);
+                            int32_t row_group_log2, void* stream);
 /* out bf16 [n] = N(0, std) under key (seed, *counter), then ++*counter
  * (device uint32): a fresh decode input per replay of a captured graph. */
 int glm53_synth_step_input(void* out, int64_t n, uint64_t seed, float std, uint32_t* counter,

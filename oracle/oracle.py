@@ -493,6 +493,32 @@ def grouped_moe(x_bits, bank, ids, scores, limit, shared=None, reduction="groupe
     return result.reshape(x.shape)
 
 
+def moe_reductions(x_bits, bank, ids, scores, limit, shared=None):
+    """{"direct": direct_moe(...), "grouped": grouped_moe(..., "grouped")}
+    from one pass over the experts: both reductions combine the same
+    per-route outputs (each route's expert output is the exactly rounded
+    sum in either contraction tree), Direct in ascending expert order with
+    BF16 accumulation (fp8.py:384-397), grouped as the FP32 slot-order sum
+    (grouped_fp8.py:273-276), then T(+ shared) (packed.py:922)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    h = x.shape[-1]
+    flat = x.reshape(-1, h)
+    k = np.asarray(ids).shape[-1]
+    routes = np.asarray(ids).reshape(-1, k)
+    flat_scores = np.asarray(scores, dtype=np.float32).reshape(-1, k)
+    t = flat.shape[0]
+    route_out = np.zeros((t * k, h), dtype=np.uint16)
+    for e in np.unique(routes):
+        rows, slots = np.nonzero(routes == e)
+        route_out[rows * k + slots] = expert_forward(flat[rows], expert_matrices(bank, int(e)), limit)
+    out = {"direct": direct_order_reduce(route_out, routes, flat_scores),
+           "grouped": restore_and_reduce(route_out, flat_scores.reshape(-1), np.arange(t * k), t, k)}
+    if shared is not None:
+        sh = shared_forward(flat, shared, limit)
+        out = {name: add_bf16(v, sh) for name, v in out.items()}
+    return {name: v.reshape(x.shape) for name, v in out.items()}
+
+
 # ------------------------------------------------------------- metrics ---
 
 def compare(actual_bits, expected_bits):

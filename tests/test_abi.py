@@ -160,3 +160,55 @@ def test_product_does_not_import_the_oracle():
             text = path.read_text()
             assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), path
             assert "glm53o_" not in text, path
+
+
+def test_bound_decode_refuses_x_of_another_dtype_or_device(N):
+    """DecodePlan.execute_bound / execute_bound_router check x against the
+    bound weights before any native call: BF16 only (a float32 or float16 x
+    of H elements would otherwise be read as BF16 bytes), on the weights'
+    device.  Exercised on a plan object without a native handle."""
+    import torch
+
+    packed = submodule("packed")
+    plan = object.__new__(packed.DecodePlan)
+    plan._bound = (None, [torch.empty(8, dtype=torch.uint8, device="meta")], [], 0)
+    with pytest.raises(ValueError, match="bfloat16"):
+        plan._check_x(torch.zeros(4096, dtype=torch.float32, device="meta"), "execute_bound")
+    with pytest.raises(ValueError, match="bound weights are on meta"):
+        plan._check_x(torch.zeros(4096, dtype=torch.bfloat16), "execute_bound")
+    plan._check_x(torch.zeros(4096, dtype=torch.bfloat16, device="meta"), "execute_bound")
+
+
+def test_abi_version_two_and_layout_constants(N, libso):
+    """ABI 2: glm53_bank gained row_group_log2 and the layout entry points."""
+    assert libso.glm53_abi_version() == 2 == N.ABI_VERSION
+    assert (N.ROWS_LAYOUT, N.TILED_LAYOUT, N.MAX_ROW_GROUP_LOG2) == (
+        0, header_define("GLM53_TILED_ROW_GROUP_LOG2"), header_define("GLM53_MAX_ROW_GROUP_LOG2"))
+
+
+def test_layout_entry_points_refuse_bad_arguments_without_device_work(N, libso):
+    """glm53_relayout_weights / glm53_bank_create / glm53_bank_import check
+    layouts and shapes before touching a device (status 1 on this GPU-less
+    host): overlap, an exponent out of range, a row-group layout of a width
+    that is not a multiple of 128 or of a partial group."""
+    import ctypes
+
+    P = ctypes.c_void_p
+    a, b = P(1 << 20), P((1 << 20) + 64)  # never dereferenced: refused before any device call
+    assert libso.glm53_relayout_weights(a, b, 1, 16, 128, 0, 4, None) == N.INVALID_ARGUMENT
+    assert "overlap" in libso.glm53_last_error().decode()
+    far = P(1 << 30)
+    assert libso.glm53_relayout_weights(a, far, 1, 16, 128, 0, 9, None) == N.INVALID_ARGUMENT
+    assert libso.glm53_relayout_weights(a, far, 1, 16, 200, 0, 4, None) == N.INVALID_ARGUMENT
+    assert "cols % 128" in libso.glm53_last_error().decode()
+    assert libso.glm53_relayout_weights(a, far, 1, 24, 128, 0, 4, None) == N.INVALID_ARGUMENT
+    assert "row group" in libso.glm53_last_error().decode()
+    bank = N.Bank(1 << 20, 1 << 21, 1 << 22, 1 << 23, 4, 256, 129, 0, 4)  # I = 129 cannot be tiled
+    out = ctypes.POINTER(N.Bank)()
+    assert libso.glm53_bank_create(ctypes.byref(bank), None, ctypes.byref(out)) == N.INVALID_ARGUMENT
+    assert "multiples of 128" in libso.glm53_last_error().decode()
+    bank.intermediate, bank.row_group_log2 = 128, 8
+    assert libso.glm53_bank_create(ctypes.byref(bank), None, ctypes.byref(out)) == N.INVALID_ARGUMENT
+    bank.row_group_log2 = 0
+    assert libso.glm53_bank_import(ctypes.byref(bank), 9, None, ctypes.byref(out)) == N.INVALID_ARGUMENT
+    assert not out

@@ -83,10 +83,10 @@ def test_fp8_pair_rules(C, tmp_path):
     tensors, failures = C.read_headers(root)
     assert failures == []
     got = C.validate_fp8_pairs(tensors)
-    assert any("missing FP8 scale tensor" in f and "experts.1.up_proj" in f for f in got)
+    assert any("block scales" in f and "are missing" in f and "experts.1.up_proj" in f for f in got)
     assert any("invalid FP8 scale" in f and "experts.2.down_proj" in f and "(2, 1)" in f for f in got)
     assert any("invalid FP8 scale" in f and "experts.0.gate_proj" in f and "F64" in f for f in got)
-    assert any("without 2-D weight semantics" in f and "stray_fp8" in f for f in got)
+    assert any("must be a 2-D '.weight'" in f and "stray_fp8" in f for f in got)
     assert len(got) == 4
 
 
@@ -101,8 +101,8 @@ def test_header_rules(C, tmp_path):
     index["weight_map"]["model.language_model.layers.3.mlp.not_there"] = shard.name
     (root / "model.safetensors.index.json").write_text(json.dumps(index))
     _, failures = C.read_headers(root)
-    assert any("shard size/header mismatch" in f for f in failures)
-    assert any("absent from headers" in f and "not_there" in f for f in failures)
+    assert any("the header accounts for" in f and shard.name in f for f in failures)
+    assert any("no shard header holds" in f and "not_there" in f for f in failures)
 
 
 def test_overlapping_and_bad_ranges(C, tmp_path):
@@ -114,8 +114,9 @@ def test_overlapping_and_bad_ranges(C, tmp_path):
     raw = json.dumps(header).encode()
     (root / "model.safetensors").write_bytes(struct.pack("<Q", len(raw)) + raw + bytes(16))
     _, failures = C.read_headers(root)
-    assert any("overlapping tensors a and b" in f for f in failures)
-    assert any("invalid data range for c" in f for f in failures)
+    assert any("tensors a and b claim overlapping bytes" in f for f in failures)
+    assert any(f.startswith("c: data_offsets [12, 16) do not hold the 6 bytes") for f in failures)
+    assert len(failures) == 2
 
 
 def test_layer_discovery_errors(C, tmp_path):

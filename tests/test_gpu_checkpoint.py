@@ -21,8 +21,9 @@ def _host(t):
 def _as_tensors(bank, shared, gate, layer):
     sh = {p: (_host(getattr(shared, f"{p}_proj").weight), _host(getattr(shared, f"{p}_proj").weight_scale_inv))
           for p in ("gate", "up", "down")}
-    return layer_tensors("model.language_model.", layer, _host(bank.gate_up_weight), _host(bank.gate_up_scale_inv),
-                         _host(bank.down_weight), _host(bank.down_scale_inv), sh, _host(gate.weight),
+    gate_up, down = bank.reference_weights()  # a checkpoint holds the row-major layout
+    return layer_tensors("model.language_model.", layer, _host(gate_up), _host(bank.gate_up_scale_inv),
+                         _host(down), _host(bank.down_scale_inv), sh, _host(gate.weight),
                          _host(gate.e_score_correction_bias))
 
 
@@ -40,8 +41,13 @@ def test_imported_layer_matches_source(M, O, dev, tmp_path):
               "norm_topk_prob": gate.norm_topk_prob}
     root = write_checkpoint(tmp_path / "ck", tensors, config, shards=3)
     b2, s2, g2 = C.load_moe_layer(root, 5, dev)
+    assert b2.layout == bank.layout  # both the package's default layout
     for name in ("gate_up_weight", "gate_up_scale_inv", "down_weight", "down_scale_inv"):
         assert torch.equal(getattr(b2, name), getattr(bank, name)), name
+    tiled, _, _ = C.load_moe_layer(root, 5, dev, layout="tiled")
+    assert tiled.layout == "tiled" and not torch.equal(tiled.gate_up_weight, tiled.reference_weights()[0])
+    for got, want in zip(tiled.reference_weights(), bank.reference_weights()):
+        assert torch.equal(got, want)
     for p in ("gate", "up", "down"):
         assert torch.equal(getattr(s2, f"{p}_proj").weight, getattr(shared, f"{p}_proj").weight)
         assert torch.equal(getattr(s2, f"{p}_proj").weight_scale_inv, getattr(shared, f"{p}_proj").weight_scale_inv)

@@ -15,7 +15,8 @@ oracle on the device's own input:
 * x_out against O.add_bf16(x_in, O.decode_moe(x_in, touched experts,
   device ids / scores, shared)) -- the reference's decode composition
   (packed.py:896-923) plus the decoder's BF16 residual add -- under the
-  BASELINE gates and a floor on bit-identical outputs;
+  BASELINE gates, a floor on bit-identical outputs, and the reference's
+  elementwise gate on the summed parts (conftest.assert_residual_parity);
 * the plan's error flag stays clear.
 
 Then the 42-layer step is captured in a HIP graph and replayed: every
@@ -30,7 +31,7 @@ from types import SimpleNamespace
 import numpy as np
 import pytest
 
-from conftest import assert_parity, host_shared, submodule, to_bits
+from conftest import assert_residual_parity, host_bank, host_shared, submodule, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -60,14 +61,7 @@ def stack(dev):
 
 
 def _touched(bank, ids):
-    import torch
-
-    idx = torch.as_tensor(np.asarray(ids, dtype=np.int64), device=bank.gate_up_weight.device)
-    return SimpleNamespace(gate_up_weight=bank.gate_up_weight.index_select(0, idx).cpu().numpy(),
-                           gate_up_scale_inv=bank.gate_up_scale_inv.index_select(0, idx).cpu().numpy(),
-                           down_weight=bank.down_weight.index_select(0, idx).cpu().numpy(),
-                           down_scale_inv=bank.down_scale_inv.index_select(0, idx).cpu().numpy(),
-                           intermediate_size=bank.intermediate_size)
+    return host_bank(bank, ids)
 
 
 def _run_step(layers, x, dev, N):
@@ -98,9 +92,11 @@ def test_config3_in_place_residual_stack_matches_oracle(stack, dev, O):
             _router_check(O, l.gate, x_in[None], ids[None], scores[None])
             if li not in hosts:
                 hosts[li] = host_shared(l.shared)
-            moe = O.decode_moe(x_in, _touched(l.bank, ids), np.arange(8), scores, cfg.swiglu_limit, hosts[li])
+            moe, parts = O.decode_moe(x_in, _touched(l.bank, ids), np.arange(8), scores, cfg.swiglu_limit, hosts[li],
+                                      return_stages=True)
             want = O.add_bf16(x_in, moe)
-            st = assert_parity(to_bits(x).reshape(-1), want, O, exact_fraction=0.9)
+            st = assert_residual_parity(to_bits(x).reshape(-1), want, x_in, (parts.routed, parts.shared, moe), O,
+                                        exact_fraction=0.9)
             worst = min(worst, st["bit_exact_fraction"])
         finals.append((x0, x.clone()))
     assert all(l.plan.error_flag() == 0 for l in layers)

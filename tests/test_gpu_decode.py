@@ -128,11 +128,12 @@ def test_router_matches_oracle(O, config2_layer, dev, tokens):
                                                    (100, 1024, 200), (77, 512, 512), (40, 256, 320), (50, 384, 64),
                                                    (5, 200, 16), (3, 201, 16)])
 def test_router_many_tokens_matches_oracle(M, O, dev, tokens, hidden, experts):
-    """Many-token router: up to 1024 tokens BF16 MFMA over the exact
-    three-way BF16 split of the FP32 weights, K-chunk partial sums added by
-    the selection (hidden a multiple of 128); more tokens (2048) or hidden 200
-    and 201 take the widened input and the FP32 library GEMM (201: the
-    element-wise widening).  Shapes cover tail tokens and experts, a last
+    """Many-token router: for any token count (2048 included) the
+    hand-written BF16 MFMA tile kernel over the exact three-way BF16 split of
+    the FP32 weights, K-chunk partial sums added in chunk order by the
+    selection (hidden a multiple of 128, 16-byte aligned rows); hidden 200
+    and 201 take the FP32 per-(expert, token) logit kernel instead (201:
+    rows not 16-byte aligned).  Shapes cover tail tokens and experts, a last
     expert group of 2 tiles (288 experts), 512 experts, a single partial
     plane wider than the activation space (40 x 256 x 320) and few tiles."""
     import torch
@@ -273,7 +274,7 @@ def test_bank_handle_scans_once_and_decodes_like_the_bank(M, O, dev, small_layer
                                         own.borrowed_stable_tensor(bank.gate_up_scale_inv, owner=bank),
                                         own.borrowed_stable_tensor(bank.down_weight, owner=bank),
                                         own.borrowed_stable_tensor(bank.down_scale_inv, owner=bank),
-                                        intermediate_size=bank.intermediate_size)
+                                        intermediate_size=bank.intermediate_size, layout=bank.row_group_log2)
     marked.gate_up_weight[3, 5, 7] = 0x7F
     with packed.BankHandle(marked, dev) as handle:
         assert _device_int32(handle.ptr.contents.code_flags) != 0
@@ -370,16 +371,7 @@ def test_config2_decode_matches_oracle(M, O, dev, config2_layer):
 
 def _touched_bank(bank, ids):
     """Read back only the selected experts (the oracle never holds 5.4 GB)."""
-    import torch
-
-    idx = torch.as_tensor(np.asarray(ids, dtype=np.int64), device=bank.gate_up_weight.device)
-    return SimpleNamespace(
-        gate_up_weight=bank.gate_up_weight.index_select(0, idx).cpu().numpy(),
-        gate_up_scale_inv=bank.gate_up_scale_inv.index_select(0, idx).cpu().numpy(),
-        down_weight=bank.down_weight.index_select(0, idx).cpu().numpy(),
-        down_scale_inv=bank.down_scale_inv.index_select(0, idx).cpu().numpy(),
-        intermediate_size=bank.intermediate_size,
-    )
+    return host_bank(bank, ids)
 
 
 def test_out_of_range_expert_id_sets_flag_not_fault(M, dev, small_layer):
@@ -475,6 +467,11 @@ def test_bound_plan_matches_unbound_and_checks_weight_identity(M, dev):
     out = routed_plan.execute_bound_router(x)
     assert torch.equal(out, want)
     assert len(routed_plan.bound_weight_identities) == 12
+    with pytest.raises(ValueError, match="bfloat16"):  # same byte count, other dtype: refused, not read as BF16
+        routed_plan.execute_bound(x.view(torch.float16), other_ids, other_sc)
+    with pytest.raises(ValueError, match="bfloat16"):
+        routed_plan.execute_bound_router(x.float())
+    assert routed_plan.execution_count == 1
 
     shared.down_proj.weight_scale_inv.mul_(1.0)  # in place: a new version of a bound tensor
     assert not plan.bound_weight_identities_stable
@@ -503,7 +500,7 @@ def test_routed_diagnostic_stages_match_oracle(M, O, dev, small_layer):
     diag = M.RoutedDiagnostic(cfg.n_routed_experts, hidden_size=H, intermediate_size=I, swiglu_limit=cfg.swiglu_limit)
     x = syn.normal_bf16((H,), syn.key(7, "diag"), device=dev)
     ids = torch.tensor([5, 0, 31, 7, 12, 3, 30, 19], dtype=torch.int32, device=dev)
-    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv)
+    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv, layout=bank.layout)
     torch.cuda.synchronize()
     assert diag.execution_count == 1 and diag.scratch_bytes >= 5 * 2 * 8 * I
     xb = to_bits(x).reshape(1, -1)
@@ -532,5 +529,5 @@ def test_routed_diagnostic_stages_match_oracle(M, O, dev, small_layer):
     plan_hidden = to_bits(plan.debug_scratch(0)).reshape(9, I)[:8]
     assert_parity(plan_hidden.reshape(-1), hid.reshape(-1), O, exact_fraction=0.9)
     ident = diag.buffer_identities
-    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv)
+    diag.execute(x, ids, bank.gate_up_weight, bank.gate_up_scale_inv, layout=bank.layout)
     assert diag.buffer_identities == ident and diag.execution_count == 2

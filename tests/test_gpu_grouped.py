@@ -226,16 +226,8 @@ def _touched(bank, experts):
     import torch
 
     e = np.unique(experts)
-    idx = torch.as_tensor(e, device=bank.gate_up_weight.device)
     remap = {int(v): i for i, v in enumerate(e)}
-    sub = SimpleNamespace(
-        gate_up_weight=bank.gate_up_weight.index_select(0, idx).cpu().numpy(),
-        gate_up_scale_inv=bank.gate_up_scale_inv.index_select(0, idx).cpu().numpy(),
-        down_weight=bank.down_weight.index_select(0, idx).cpu().numpy(),
-        down_scale_inv=bank.down_scale_inv.index_select(0, idx).cpu().numpy(),
-        intermediate_size=bank.intermediate_size,
-    )
-    return sub, np.vectorize(remap.get)(experts).astype(np.int32)
+    return host_bank(bank, e), np.vectorize(remap.get)(experts).astype(np.int32)
 
 
 @pytest.mark.parametrize("reduction", ["grouped", "direct"])
@@ -331,18 +323,22 @@ class WeightedGate:
                 torch.from_numpy(sc).to(x.device).reshape(*x.shape[:-1], self.top_k))
 
 
-@pytest.mark.parametrize("codes_480", [False, True])
-def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, codes_480):
-    """The wide GEMM shape (128-route descriptors x 256 weight rows, taken
-    when experts average at least 48 routes): 300 tokens x top-4 over 8
-    experts with skewed counts (descriptors full, part-filled and single
-    groups), hidden 640 (the down GEMM's last 256-row tile half past the
-    matrix, its second scale row clamped), intermediate 384, the shared
-    expert as dense descriptors in the same launches; with 0x7F / 0xFF codes
-    in the routed gate/up and down weights, the fixup path of both modes.
-    Against the oracle's Direct MoE."""
+@pytest.mark.parametrize("inter,codes_480", [(384, False), (384, True), (256, True)])
+def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, inter, codes_480):
+    """The wide GEMM shape (128-route descriptors x 384 weight rows: 192 gate
+    rows with the matching 192 up rows for gate/up, 384 output columns for
+    down; taken when experts average at least 48 routes): 300 tokens x top-4
+    over 8 experts with skewed counts (descriptors full, part-filled and
+    single groups), hidden 640 (the down GEMM's second item ends 128 rows
+    past the matrix, its last scale block clamped), intermediate 384 (two
+    whole gate/up items) or 256 (the second gate/up item half past the
+    matrix: a partial last gate tile), the shared expert as dense
+    descriptors in the same launches; with 0x7F / 0xFF codes in the routed
+    gate/up and down weights, the fixup path of both modes (also on the
+    partial gate tile at intermediate 256).  Against the oracle's Direct
+    MoE."""
     syn = submodule("synthetic")
-    cfg = syn.layer_config(hidden=640, intermediate=384, experts=8, top_k=4, limit=7.0)
+    cfg = syn.layer_config(hidden=640, intermediate=inter, experts=8, top_k=4, limit=7.0)
     bank, shared, _ = syn.synth_layer(cfg, seed=131, device=dev)
     if codes_480:
         bank.gate_up_weight[1, ::7, ::13] = 0x7F
@@ -535,9 +531,10 @@ def test_config5_zipf_2048_tokens_matches_oracle(M, O, dev, config5):
     10 routes; the
     many-token router above 1,024 tokens.  Every token's selection is
     checked against the oracle's router (near-tie rule); the MoE output of
-    every 4th token against the oracle's Direct MoE and, for the grouped
-    reduction, its grouped restatement (grouped_fp8.py:279-328), on the
-    device's selection and the touched experts."""
+    every token against the oracle's Direct MoE (BASELINE gates) and, for
+    each reduction, against the oracle's same-order combine with the
+    elementwise gate as well (grouped_fp8.py:279-328), on the device's
+    selection and the touched experts."""
     cfg, bank, shared, gate, x, tokens = config5
     ids_d, sc_d = gate(x.reshape(tokens, -1))
     ids, sc = ids_d.cpu().numpy(), sc_d.cpu().numpy()
@@ -548,16 +545,13 @@ def test_config5_zipf_2048_tokens_matches_oracle(M, O, dev, config5):
     from test_gpu_decode import _router_check
 
     _router_check(O, gate, xb, ids, sc)
-    sel = np.arange(0, tokens, 4)
-    sub, local = _touched(bank, ids[sel])
-    hs = host_shared(shared)
-    want_d = O.direct_moe(xb[sel], sub, local, sc[sel], cfg.swiglu_limit, hs)
-    want_g = O.grouped_moe(xb[sel], sub, local, sc[sel], cfg.swiglu_limit, hs)
-    for reduction, want in (("grouped", want_g), ("direct", want_d)):
+    sub, local = _touched(bank, ids)
+    want = O.moe_reductions(xb, sub, local, sc, cfg.swiglu_limit, host_shared(shared))
+    for reduction in ("grouped", "direct"):
         y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared, reduction=reduction)(x)
-        got = to_bits(y).reshape(tokens, -1)[sel]
-        assert_parity(got, want_d, O)
-        stats = assert_parity(got, want, O, exact_fraction=0.75)
+        got = to_bits(y).reshape(tokens, -1)
+        assert_parity(got, want["direct"], O, elementwise=reduction == "direct")
+        stats = assert_parity(got, want[reduction], O, exact_fraction=0.75)
         print(f"config 5 {reduction}: {stats}")
 
 

@@ -45,5 +45,11 @@ def test_prefill_at_checkpoint_width_matches_oracle(M, O, dev, hidden, inter):
     x = syn.normal_bf16((1, T, hidden), syn.key(hidden, inter, "prefill"), device=dev)
     y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)(x)
     ids, sc = (v.reshape(T, 8).cpu().numpy() for v in gate(x))
-    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
-    assert_parity(to_bits(y).reshape(T, -1), want, O)
+    want = O.moe_reductions(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit,
+                            host_shared(shared))
+    got = to_bits(y).reshape(T, -1)
+    # BASELINE gates against Direct; elementwise against the same (FP32
+    # slot-order) reduction: Direct's BF16 accumulation differs from it by a
+    # few ulps of the running total (README.md:801-807 of the reference)
+    assert_parity(got, want["direct"], O, elementwise=False)
+    assert_parity(got, want["grouped"], O, exact_fraction=0.75)

@@ -445,6 +445,30 @@ def test_grouped_equals_direct_and_decode_fallback(O):
     assert np.array_equal(one[0], O.decode_moe(x[0], bank, routes[0], scores[0], L))
 
 
+def test_moe_reductions_equal_the_separate_compositions(O):
+    """moe_reductions (one pass over the experts, both combines) equals
+    direct_moe and grouped_moe(reduction="grouped") bit for bit, with a
+    shared expert and uneven routes; the two reductions differ somewhere,
+    so the comparison is not of one array with itself."""
+    from types import SimpleNamespace
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(29)
+    E, H, I, L, T = 8, 256, 128, 3.0, 24
+    bank = _bank(O, rng, E, H, I)
+    shared_bank = _bank(O, rng, 1, H, I)
+    mats = O.expert_matrices(shared_bank, 0)
+    shared = SimpleNamespace(gate=mats.gate, up=mats.up, down=mats.down)
+    routes = np.stack([rng.choice(E, size=4, replace=False) for _ in range(T)])
+    scores = rng.uniform(0.05, 1.5, size=(T, 4)).astype(np.float32)
+    x = oracle.f32_to_bf16((rng.normal(size=(T, H)) * 3).astype(np.float32))
+    both = O.moe_reductions(x, bank, routes, scores, L, shared)
+    assert np.array_equal(both["direct"], O.direct_moe(x, bank, routes, scores, L, shared))
+    assert np.array_equal(both["grouped"], O.grouped_moe(x, bank, routes, scores, L, shared, reduction="grouped"))
+    assert not np.array_equal(both["direct"], both["grouped"])
+
+
 def test_hc_expand_special_cases_and_float64_restatement(O):
     """Hyper-connection expand (metal:2362-2388): comb = identity with post =
     0 returns the residual streams bit for bit; comb = 0 with post = 1
