@@ -46,7 +46,8 @@ def parse():
     p.add_argument("--layers", type=int, default=42)
     p.add_argument("--kernel-steps", type=int, default=8, help="stage-graph replays (x8) for per-launch timing")
     p.add_argument("--prefill-iters", type=int, default=10)
-    p.add_argument("--cpu-steps", type=int, default=24, help="tokens through all layers for the CPU oracle timing")
+    p.add_argument("--cpu-reps", type=int, default=5,
+                   help="timed calls per config of the CPU comparator (median, after 2 warm-ups)")
     p.add_argument("--parity-layers", type=int, default=3)
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--prefill-only", action="store_true",
@@ -224,7 +225,11 @@ def main():
     # --------------------------------------------------------- CPU baseline ---
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(args, layers, cfg, dev, torch, np)
+        cpu = cpu_baseline(args, layers, cfg, dev, torch, np, syn)
+        linear["cpu_us"] = {"value": cpu["configs"]["1"], "kind": cpu["kind"], "cores": cpu["cores"]}
+        for name, key in (("config4_256_tokens", "4"), ("config5_2048_tokens_zipf", "5")):
+            if name in prefill:
+                prefill[name]["cpu_us"] = {"value": cpu["configs"][key], "kind": cpu["kind"], "cores": cpu["cores"]}
 
     result = {
         "metric": "µs per MoE layer @ batch-1 decode (HBM GB/s %peak); prefill routes/s (%FP8 MFMA)",
@@ -466,38 +471,75 @@ def bench_prefill(args, layer, cfg, dev, torch, np, pkg, syn):
     return out
 
 
-def cpu_baseline(args, layers, cfg, dev, torch, np):
-    """CPU oracle (C + OpenMP restatement of Direct decode) on the host cores:
-    `cpu_steps` tokens through all layers (x += moe(x), as on the GPU), each
-    layer timed from router to output on its touched experts, which are
-    copied to host memory before the timer starts (the 229 GB of banks do
-    not fit host RAM)."""
-    from oracle import oracle as O
+def cpu_baseline(args, layers, cfg, dev, torch, np, syn):
+    """The CPU comparator on the host cores: oracle/cpu_direct.py, the
+    reference's Direct path (fp8.py:343-400 with the FP32 router of
+    patch.py:131-142) in C with FP32 accumulation, OpenMP threads and AVX2
+    FMA -- the role the task gives to MLX's CPU stream -- on the inputs the
+    GPU legs run: BASELINE config 1 (one [1, 4096] x [4096, 4096] linear,
+    bench_linear's first matrix), config 2 (one batch-1 decode layer: layer
+    0 of the stack, router included; config 3's layers are 42 such), config
+    4 (256 tokens) and config 5 (2,048 tokens, Zipf router bias) on layer
+    0.  Each is the median of `cpu_reps` calls after 2 warm-ups
+    (scripts/probe_grouped_fp8_moe.py:46-60 of the reference), with the bank
+    already in host memory (the reference layout, copied once)."""
+    from oracle import cpu_direct as C
 
-    syn = importlib.import_module("glm53-flash-mlx_amd.synthetic")
-    host_router = [(l.gate.weight.cpu().numpy(), l.gate.e_score_correction_bias.cpu().numpy()) for l in layers]
-    samples = []
-    warm = 2
-    for step in range(args.cpu_steps):
-        x = syn.normal_bf16((cfg.hidden_size,), syn.key(SEED, "cpu", step), device=dev)
-        xb = bits(x, torch, np)
-        for li, l in enumerate(layers):
-            w, b = host_router[li]
-            ids, _ = O.router(xb[None], w, b)
-            hb, hs = host_layer_subset(l, ids[0], torch, np)
+    H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    l0 = layers[0]
+    gu, dw = l0.bank.reference_weights()
+    bank = SimpleNamespace(gate_up_weight=gu.cpu().numpy(), gate_up_scale_inv=l0.bank.gate_up_scale_inv.cpu().numpy(),
+                           down_weight=dw.cpu().numpy(), down_scale_inv=l0.bank.down_scale_inv.cpu().numpy(),
+                           intermediate_size=I)
+    del gu, dw
+    s = l0.shared
+    shared = SimpleNamespace(gate=(s.gate_proj.weight.cpu().numpy(), s.gate_proj.weight_scale_inv.cpu().numpy()),
+                             up=(s.up_proj.weight.cpu().numpy(), s.up_proj.weight_scale_inv.cpu().numpy()),
+                             down=(s.down_proj.weight.cpu().numpy(), s.down_proj.weight_scale_inv.cpu().numpy()))
+    rw = l0.gate.weight.cpu().numpy()
+    biases = {"4": l0.gate.e_score_correction_bias.cpu().numpy(), "5": syn.zipf_bias(E).numpy()}
+    limit = cfg.swiglu_limit
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        samples = []
+        for _ in range(args.cpu_reps):
             t0 = time.perf_counter()
-            ids2, sc2 = O.router(xb[None], w, b)
-            y = O.decode_moe(xb, hb, np.arange(8), sc2[0], cfg.swiglu_limit, hs)
+            fn()
             samples.append(time.perf_counter() - t0)
-            xb = O.add_bf16(xb, y)
-    timed = samples[warm:]
-    us = statistics.median(timed) * 1e6
-    cores = O.num_threads()
-    return {"value": round(us, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"{args.cpu_steps} tokens x {len(layers)} config-2 layers of batch-1 decode with residual "
-                      f"(router + 8 routed + shared per layer), {len(timed)} layer evaluations timed "
-                      f"({sum(timed):.1f} s of CPU work), median per layer; touched experts copied to host "
-                      f"before each timer; OpenMP threads={cores}; CPU {cpu_model()}"}
+        return statistics.median(samples) * 1e6, sum(samples)
+
+    lin_w = torch.empty((4096, 4096), dtype=torch.uint8, device=dev)
+    lin_s = torch.empty((32, 32), dtype=torch.float32, device=dev)
+    syn.fill_fp8(lin_w, lin_s, syn.key(91, 0), 0.02)
+    lin_w, lin_s = lin_w.cpu().numpy(), lin_s.cpu().numpy()
+    x_lin = bits(syn.normal_bf16((1, 4096), syn.key(91, "x"), device=dev), torch, np)
+    x_dec = bits(syn.normal_bf16((H,), syn.key(SEED, "cpu", 0), device=dev), torch, np)[None]
+    xs = {"4": bits(syn.normal_bf16((256, H), syn.key(SEED, "config4_256_tokens"), device=dev), torch, np),
+          "5": bits(syn.normal_bf16((2048, H), syn.key(SEED, "config5_2048_tokens_zipf"), device=dev), torch, np)}
+
+    def moe(x, bias):
+        ids, sc = C.router(x, rw, bias, top_k=k)
+        return C.direct_moe(x, bank, ids, sc, limit, shared)
+
+    out, work = {}, 0.0
+    out["1"], w = timed(lambda: C.linear(x_lin, lin_w, lin_s))
+    work += w
+    out["2"], w = timed(lambda: moe(x_dec, biases["4"]))
+    work += w
+    for key in ("4", "5"):
+        out[key], w = timed(lambda key=key: moe(xs[key], biases[key]))
+        work += w
+    cores = C.num_threads()
+    return {"value": round(out["2"], 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "configs": {key: round(v, 1) for key, v in out.items()},
+            "sample": f"the reference's Direct path restated in C (oracle/glm53_cpu_direct.c: FP32 accumulation, "
+                      f"OpenMP x {cores} threads, AVX2 FMA) at BASELINE config 2 (value: one batch-1 decode layer, "
+                      f"router + 8 routed + shared, layer 0 of the stack; config 3 = 42 such layers), and in "
+                      f"'configs' (us per call) also config 1 (one 4096 x 4096 linear), 4 (256 tokens) and 5 "
+                      f"(2,048 tokens, Zipf bias); median of {args.cpu_reps} calls after 2 warm-ups each "
+                      f"({work:.1f} s of timed CPU work), bank in host memory; CPU {cpu_model()}"}
 
 
 def traffic_run(args):

@@ -494,3 +494,42 @@ def test_hc_expand_special_cases_and_float64_restatement(O):
         branch = (post[:, b, None].astype(np.float64) * m).astype(np.float32)
         want[:, b] = O.f32_to_bf16((branch.astype(np.float64) + mixed.astype(np.float64)).astype(np.float32))
     assert np.array_equal(O.hc_expand(moe, res, post, comb), want)
+
+
+def test_cpu_comparator_matches_the_oracle(O):
+    """The benchmark's CPU comparator (oracle/cpu_direct.py: Direct with FP32
+    accumulation, timed as bench.py's cpu_baseline) computes the same
+    function as the float64 oracle: linear within the BASELINE gates with
+    most outputs bit-identical, the router's picks equal (no near-ties at
+    these scales), decode and prefill MoE (with a shared expert) within the
+    gates and the reference's elementwise tolerance."""
+    from types import SimpleNamespace
+
+    from oracle import cpu_direct as C
+    from oracle import oracle
+
+    from conftest import assert_parity
+
+    codes = np.arange(256, dtype=np.uint8)
+    assert np.array_equal(C.decode_codes(codes).view(np.uint32), O.e4m3_lut().view(np.uint32))
+    rng = np.random.default_rng(31)
+    E, H, I, L, T = 8, 256, 128, 3.0, 20
+    bank = _bank(O, rng, E, H, I)
+    mats = O.expert_matrices(_bank(O, rng, 1, H, I), 0)
+    shared = SimpleNamespace(gate=mats.gate, up=mats.up, down=mats.down)
+    x = oracle.f32_to_bf16(rng.normal(size=(T, H)).astype(np.float32))
+    w, s = bank.gate_up_weight[3], bank.gate_up_scale_inv[3]
+    assert_parity(C.linear(x, w, s), O.fp8_linear(x, w, s), O, exact_fraction=0.97)
+    rw = (rng.normal(size=(E, H)) * 0.05).astype(np.float32)
+    rb = rng.uniform(-0.01, 0.01, size=E).astype(np.float32)
+    ids, sc = C.router(x, rw, rb, top_k=4)
+    ids_o, sc_o = O.router(x, rw, rb, top_k=4)
+    assert np.array_equal(ids, ids_o)
+    np.testing.assert_allclose(sc, sc_o, rtol=2e-6)
+    got = C.direct_moe(x, bank, ids, sc, L, shared)
+    assert_parity(got, O.direct_moe(x, bank, ids, sc, L, shared), O, exact_fraction=0.75)
+    ids8 = np.stack([rng.choice(E, size=8, replace=False)]).astype(np.int32)
+    sc8 = rng.uniform(0.05, 0.3, size=(1, 8)).astype(np.float32)
+    got1 = C.direct_moe(x[:1], bank, ids8, sc8, L, shared)
+    assert_parity(got1, O.direct_moe(x[:1], bank, ids8, sc8, L, shared), O, exact_fraction=0.75)
+    assert C.num_threads() >= 1
