@@ -53,6 +53,8 @@ def parse():
     p.add_argument("--prefill-only", action="store_true",
                    help="one synthetic layer, configs 4 and 5 prefill only (for profiling the grouped GEMM)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--ref-layers", type=int, default=8,
+                   help="layers of the reference-shape leg (H=4096, I=2048); 0 skips it")
     p.add_argument("--layout", default="rows",
                    help="expert-bank layout: rows (the reference's row-major layout, the library's default), "
                         "tiled (16-row groups) or a row-group exponent 1..7")
@@ -231,6 +233,14 @@ def main():
             if name in prefill:
                 prefill[name]["cpu_us"] = {"value": cpu["configs"][key], "kind": cpu["kind"], "cores": cpu["cores"]}
 
+    # ------------------------------------------------ reference shape leg ---
+    layout_name = layers[0].bank.layout
+    ref_shape = None
+    if args.ref_layers > 0:
+        del layers  # frees the config-2 stack (229 GB) before the I = 2048 layers are made
+        torch.cuda.empty_cache()
+        ref_shape = bench_reference_shape(args, layout, dev, torch, pkg, syn, N, packed)
+
     result = {
         "metric": "µs per MoE layer @ batch-1 decode (HBM GB/s %peak); prefill routes/s (%FP8 MFMA)",
         "value": round(us_layer, 3),
@@ -250,7 +260,7 @@ def main():
                         "BF16 residual, fresh seeded token per step, HIP-graph replay",
             "layers": L, "hidden": H, "intermediate": I, "experts": E, "top_k": k, "shared_experts": 1,
             "resident_bytes": resident, "parallelism": "single GPU",
-            "bank_layout": layers[0].bank.layout,
+            "bank_layout": layout_name,
         },
         "roofline": {
             "bound": "hbm",
@@ -287,6 +297,7 @@ def main():
         "prefill": prefill,
         "parity": parity,
         "cpu_baseline": cpu,
+        "reference_shape": ref_shape,
     }
     line = json.dumps(result)
     print(line, flush=True)
@@ -469,6 +480,114 @@ def bench_prefill(args, layer, cfg, dev, torch, np, pkg, syn):
         }
         log(f"prefill {name}: {us:.1f} us, {gbs:.0f} GB/s, {tflops:.1f} TFLOP/s")
     return out
+
+
+def bench_reference_shape(args, layout, dev, torch, pkg, syn, N, packed):
+    """The reference's own measured shape (the real checkpoint: H=4096,
+    I=2048, 288 experts top-8, one shared expert of I=2048) on `ref_layers`
+    synthetic layers.  Decode: one step (input draw + 3 launches per layer)
+    captured as a graph and replayed, as the headline; and, as the
+    reference times its operator (probe_fused_packed_gate_up_swiglu_decode.py
+    :396-411: gate, routed MoE and shared expert of one layer, then a host
+    synchronisation), the median wall time of single host-synchronised
+    eager layer calls.  Prefill: SortedGroupedFP8MoE at 256 tokens, routed
+    near-uniformly and onto 51 experts (the count of the reference's
+    layer-3 run, m3ultra512-grouped-fp8-layer3-20260828.json:149-152),
+    event-timed and host-synchronised."""
+    cfg = syn.layer_config(intermediate=2048)
+    H, I, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    L = args.ref_layers
+    t0 = time.perf_counter()
+    layers = []
+    for layer in range(L):
+        bank, shared, gate = syn.synth_layer(cfg, SEED + 1, layer, dev, layout=layout)
+        layers.append(SimpleNamespace(bank=bank, shared=shared, gate=gate,
+                                      plan=packed.DecodePlan(H, I, I, E, k, cfg.swiglu_limit)))
+    torch.cuda.synchronize()
+    log(f"reference shape: generated {L} layers (H={H}, I={I}) in {time.perf_counter() - t0:.1f} s")
+
+    x = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = N.lib()
+
+    def step():
+        N.check(lib.glm53_synth_step_input(N.ptr(x), H, SEED + 1, 1.0, N.ptr(counter), N.stream_handle(dev)))
+        for l in layers:
+            l.plan.step(l.bank, l.shared, l.gate, x, x, x, N.STAGE_ALL, dev)
+
+    reps = max(16, args.steps // 2)
+    us_layer = time_graph(step, reps, torch) / L
+    nbytes = decode_layer_bytes(H, I, I, E, k)["total"]
+    gbs = nbytes / (us_layer * 1e-6) / 1e9
+
+    # single host-synchronised layer calls, as the reference's operator timing
+    xs = [syn.normal_bf16((H,), syn.key(SEED + 1, "eager", i), device=dev) for i in range(4 * L)]
+    out = torch.empty_like(xs[0])
+    wall = []
+    for i, xi in enumerate(xs):
+        l = layers[i % L]
+        t = time.perf_counter()
+        l.plan.step(l.bank, l.shared, l.gate, xi, None, out, N.STAGE_ALL, dev)
+        torch.cuda.synchronize()
+        if i >= L:  # the first pass over the layers is the warm-up
+            wall.append((time.perf_counter() - t) * 1e6)
+    errors = [l.plan.error_flag() for l in layers]
+    if any(errors):
+        raise RuntimeError(f"reference-shape decode error flags: {errors}")
+    log(f"reference shape decode: {us_layer:.2f} us/layer in a graph ({gbs:.0f} GB/s), "
+        f"{statistics.median(wall):.1f} us per host-synchronised call")
+
+    tokens = 256
+    l0 = layers[0]
+    keep = torch.randperm(E, generator=torch.Generator().manual_seed(SEED))[:51]
+    bias51 = torch.full((E,), -1.0, dtype=torch.float32)
+    bias51[keep] = 0.0
+    prefill = {}
+    for name, gate in (("near_uniform", l0.gate),
+                       ("51_experts", pkg.Float32Gate(l0.gate.weight, bias51.to(dev), top_k=k))):
+        moe = pkg.SortedGroupedFP8MoE(l0.bank, cfg, gate, l0.shared)
+        xp = syn.normal_bf16((1, tokens, H), syn.key(SEED + 1, "prefill", name), device=dev)
+        ids, _ = gate(xp.reshape(tokens, H))
+        counts = torch.bincount(ids.reshape(-1).long(), minlength=E).cpu()
+        for _ in range(2):
+            moe(xp)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(args.prefill_iters):
+            y = moe(xp)
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) * 1000.0 / args.prefill_iters
+        synced = []
+        for _ in range(5):
+            t = time.perf_counter()
+            y = moe(xp)
+            torch.cuda.synchronize()
+            synced.append((time.perf_counter() - t) * 1e6)
+        touched = int((counts > 0).sum())
+        prefill[name] = {"us": round(us, 1), "host_synchronised_us": round(statistics.median(synced), 1),
+                         "touched_experts": touched, "max_expert_routes": int(counts.max()),
+                         "routes_per_expert_mean": round(tokens * k / touched, 2),
+                         "finite": bool(torch.isfinite(y.float()).all().item())}
+        log(f"reference shape prefill {name}: {us:.1f} us ({touched} experts)")
+    return {
+        "shape": {"hidden": H, "intermediate": I, "shared_intermediate": I, "experts": E, "top_k": k,
+                  "layers": L, "bank_layout": l0.bank.layout},
+        "decode_us_per_layer": round(us_layer, 3),
+        "decode_GBps": round(gbs, 1),
+        "decode_hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+        "decode_layer_bytes": nbytes,
+        "decode_host_synchronised_us": round(statistics.median(wall), 1),
+        "prefill_256_tokens": prefill,
+        "reference_m3_ultra": {
+            "decode_layer_ms": 1.0629, "prefill_256_tokens_ms": 22.0797,
+            "source": "bench-results/m3ultra512-fused-packed-gate-up-swiglu-decode-20260901.json "
+                      "(operator.3.with_shared_expert.fused.median_ms: router + routed + shared of real layer 3, "
+                      "host-synchronised) and m3ultra512-grouped-fp8-layer3-20260828.json (grouped_seconds median "
+                      "at 256 tokens, 51 experts touched)"},
+        "note": "context only, not vs_baseline: other hardware, real checkpoint weights vs synthetic ones",
+    }
 
 
 def cpu_baseline(args, layers, cfg, dev, torch, np, syn):
