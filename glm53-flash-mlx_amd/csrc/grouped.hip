@@ -426,23 +426,27 @@ __device__ __forceinline__ void stage_barrier() {
 }
 
 // LDS layout of one 16-row x 128-byte operand tile: row r's 16-byte piece p
-// sits in slot p ^ ((r >> 1) & 7) of the row's 128 bytes, so the two direct
-// loads that fill a tile each read 8 rows as whole 128-byte lines (lane l:
-// row l / 8, slot l % 8), and the MFMA reads below (lane l: row l % 16,
-// pieces 2 (l / 16) and 2 (l / 16) + 1) hit 16 distinct 16-byte bank groups
-// per 16 lanes.
+// sits in slot p ^ (r % 8) ^ (r / 8) of the row's 128 bytes, so the two
+// direct loads that fill a tile each read 8 rows as whole 128-byte lines
+// (lane l: row l / 8, slot l % 8).  The MFMA reads below (lane l: row
+// l % 16, pieces 2 (l / 16) and 2 (l / 16) + 1) run at the LDS's full
+// 16-byte read rate with this permutation: a read probe of the operand
+// pattern measured ~210 bytes per clock per CU, the rate of 64 consecutive
+// 16-byte reads, against ~120 for slot p ^ ((r / 2) % 8), though both give
+// every 16 consecutive lanes distinct banks.
 struct OperandSlots {
   uint32_t lo, hi;  // byte offsets of the lane's two pieces in a tile
 };
 __device__ __forceinline__ OperandSlots operand_slots(int lane) {
-  const int r = lane & 15, kq = lane >> 4, g = (r >> 1) & 7;
+  const int r = lane & 15, kq = lane >> 4, g = (r & 7) ^ (r >> 3);
   return {static_cast<uint32_t>(128 * r + 16 * ((2 * kq) ^ g)), static_cast<uint32_t>(128 * r + 16 * ((2 * kq + 1) ^ g))};
 }
 // Byte offset, within its row's 128-byte K block, of the piece lane l loads
-// in load h (0: rows 0-7, 1: rows 8-15) of a tile; its row is 8 h + l / 8.
+// in load h (0: rows 0-7, 1: rows 8-15) of a tile; its row is 8 h + l / 8,
+// its slot l % 8, so the piece is (l % 8) ^ (l / 8) ^ h: load 1's offset is
+// load 0's with bit 4 flipped.
 __device__ __forceinline__ int load_piece_offset(int lane, int h) {
-  const int r = 8 * h + (lane >> 3);
-  return 16 * ((lane & 7) ^ ((r >> 1) & 7));
+  return 16 * ((lane & 7) ^ (lane >> 3) ^ h);
 }
 
 __device__ __forceinline__ i32x8 lds_operand(const uint8_t* tile, OperandSlots o) {
@@ -956,7 +960,7 @@ struct WideSources {
   int32_t wg;              // row groups of wmat (common.h)
   int32_t rows;            // rows of the matrix (loads past it re-read the last row)
   int32_t row0;            // first row of the wavefront's tiles, + lane / 8
-  int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 64)
+  int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 16)
   int32_t tok[2];          // token rows of the pair's rows 8 h + lane / 8
 };
 
@@ -975,7 +979,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       for (int h = 0; h < 2; ++h) {
         int32_t row = ls.row0 + 16 * q + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (64 * h)),
+        lds_direct16(ls.wmat + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (16 * h)),
                      sb + q * kOperand + 1024 * h);
       }
   };
@@ -984,7 +988,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       const uint32_t sa = lds_addr + kWideBBytes + slot * kWideABytes + 2 * wave * kOperand;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int64_t off = static_cast<int64_t>(ls.tok[h]) * ls.K + kb * kBlock + (ls.piece ^ (64 * h));
+        const int64_t off = static_cast<int64_t>(ls.tok[h]) * ls.K + kb * kBlock + (ls.piece ^ (16 * h));
         lds_direct16(ls.a_hi + off, sa + 1024 * h);
         lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
       }
@@ -1087,9 +1091,9 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
     return src.a_row_index != nullptr ? src.a_row_index[route] : route;
   };
   // direct-load sources: load h of a weight tile fills its rows 8 h .. 8 h
-  // + 7, lane l reading row r = 8 h + l / 8 at piece (l % 8) ^ ((r >> 1) &
-  // 7), i.e. the h = 0 offset with bit 2 of the piece flipped for h = 1;
-  // the wavefront's tiles 3 w .. 3 w + 2 lie in one matrix
+  // + 7, lane l reading row r = 8 h + l / 8 at piece (l % 8) ^ (l / 8) ^ h,
+  // i.e. the h = 0 offset with bit 0 of the piece flipped for h = 1; the
+  // wavefront's tiles 3 w .. 3 w + 2 lie in one matrix
   WideSources ls;
   {
     const bool up = MODE == GEMM_SWIGLU && wave >= 4;
@@ -1116,13 +1120,13 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
       for (int h = 0; h < 2; ++h) {
         int32_t row = ls.row0 + 16 * q + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + group_row_base(row, K, ls.wg) + (ls.piece ^ (64 * h)), sb + q * kOperand + 1024 * h);
+        lds_direct16(ls.wmat + group_row_base(row, K, ls.wg) + (ls.piece ^ (16 * h)), sb + q * kOperand + 1024 * h);
       }
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + 2 * wave * kOperand;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int64_t off = static_cast<int64_t>(ls.tok[h]) * K + (ls.piece ^ (64 * h));
+        const int64_t off = static_cast<int64_t>(ls.tok[h]) * K + (ls.piece ^ (16 * h));
         lds_direct16(ls.a_hi + off, sa + 1024 * h);
         lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
       }
