@@ -395,13 +395,16 @@ namespace {
 constexpr int kTileRows = 128;                     // weight rows per work item
 constexpr int kOperand = 2048;                     // one 16-row x 128-byte operand tile in LDS
 constexpr int kStageB = (kTileRows / 16) * kOperand;  // 16 KB
-// LDS ring depth of each shape: 32-route descriptors keep 2 stages in
-// flight in 72 KB, 64-route descriptors 1 stage in 64 KB (two workgroups
-// per CU either way).
+// LDS ring depth of each shape: two slots (48 KB for 32-route
+// descriptors, whose stages stream through registers kRegAhead stages
+// ahead; 64 KB for 64-route descriptors, whose direct loads keep one stage
+// in flight); two workgroups per CU either way.
 template <int GPW>
 constexpr int ring_stages() {
-  return GPW == 1 ? 3 : 2;
+  return 2;
 }
+// Stages the register-staged shape (GPW = 1) keeps in flight in registers
+constexpr int kRegAhead = 3;
 // Descriptors of 32 GPW routes: 2 GPW pairs of 16, i.e. 4 GPW activation
 // operand tiles (hi and lo rows of each pair) per stage
 template <int GPW>
@@ -653,15 +656,8 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[0][t][i] = 0.0f;
 
-  constexpr int kStages = ring_stages<GPW>();
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < KB) issue(s, s);
-  int slot = 0;
-  for (int64_t kb = 0; kb < KB; ++kb) {
-    if (kb + kStages - 2 < KB) stage_barrier<P * (kStages - 2)>();
-    else stage_barrier<0>();
-    if (kb + kStages - 1 < KB) issue(kb + kStages - 1, slot == 0 ? kStages - 1 : slot - 1);
+  // one stage's MFMAs on the operands in LDS slot `slot`
+  auto compute = [&](int64_t kb, int slot) {
     if (NP > 0) {
       const uint8_t* st = lds + slot * kStage;
       const i32x8 ahi = lds_operand(st + kStageB + (2 * pair) * kOperand, slots);
@@ -696,7 +692,102 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
       }
       fold(T - 1);
     }
-    slot = slot == kStages - 1 ? 0 : slot + 1;
+  };
+
+  constexpr int kStages = ring_stages<GPW>();
+  if constexpr (GPW == 1) {
+    // Register-staged stream: each stage's operand bytes come with plain
+    // 16-byte loads (the same 8 rows x 128 bytes per instruction as the
+    // direct loads) kRegAhead stages ahead into registers and are written to
+    // the LDS slot at the positions the direct loads would fill; a 2-slot
+    // ring, one barrier per stage.  Every load is compiler-visible, so each
+    // wait is the exact one.  A weight-streaming read probe moved 6.4-6.5
+    // TB/s this way against 5.6-5.8 TB/s with direct loads.
+    static_assert(kStages == 2, "the register-staged shape double-buffers its LDS");
+    struct Staged {
+      u32x4 b[4];
+      u32x4 a[NL > 0 ? 2 * NL : 1];
+    };
+    auto load = [&](int64_t kb, Staged& r) {
+      const int64_t ko = kb * kBlock;
+      const int64_t kw = kb << (7 + src.wg);
+      r.b[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb[0][0] + kw));
+      r.b[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb[0][1] + kw));
+      r.b[2] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb[1][0] + kw));
+      r.b[3] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gb[1][1] + kw));
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        r.a[2 * j] = *reinterpret_cast<const u32x4*>(ga[j][0] + ko);
+        r.a[2 * j + 1] = *reinterpret_cast<const u32x4*>(ga[j][1] + ko);
+      }
+    };
+    auto store = [&](int slot, const Staged& r) {
+      uint8_t* sb = lds + slot * kStage + 2 * wave * kOperand + 16 * lane;
+      *reinterpret_cast<u32x4*>(sb) = r.b[0];
+      *reinterpret_cast<u32x4*>(sb + 1024) = r.b[1];
+      *reinterpret_cast<u32x4*>(sb + kOperand) = r.b[2];
+      *reinterpret_cast<u32x4*>(sb + kOperand + 1024) = r.b[3];
+      uint8_t* sa = lds + slot * kStage + kStageB + GPW * wave * kOperand + 16 * lane;
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        *reinterpret_cast<u32x4*>(sa + j * kOperand) = r.a[2 * j];
+        *reinterpret_cast<u32x4*>(sa + j * kOperand + 1024) = r.a[2 * j + 1];
+      }
+    };
+    // stage kb's bytes sit in r[kb % kRegAhead] until written to slot kb % 2;
+    // stages past the last K block are never loaded or written
+    // prologue loads are unconditional too: a block index past the last
+    // K block re-reads the last one (only when KB <= kRegAhead), never stored
+    auto clamp_kb = [&](int64_t kb) { return kb < KB ? kb : KB - 1; };
+    Staged r[kRegAhead];
+#pragma unroll
+    for (int q = 0; q < kRegAhead; ++q) load(clamp_kb(q), r[q]);
+    store(0, r[0]);
+    load(clamp_kb(kRegAhead), r[0]);
+    // Each stage: wait at the barrier (slot kb % 2 written by every
+    // wavefront, all done reading slot (kb + 1) % 2, stage kb - 1), write
+    // stage kb + 1 into that slot, load stage kb + 1 + kRegAhead into the
+    // registers it leaves, multiply stage kb.  The main loop's loads are
+    // unconditional, so the compiler's count of the loads in flight stays
+    // exact (a conditional load made it wait for all of them).
+    int64_t kb0 = 0;
+    for (; kb0 + 2 * kRegAhead < KB; kb0 += kRegAhead) {
+#pragma unroll
+      for (int q = 0; q < kRegAhead; ++q) {
+        const int64_t kb = kb0 + q;
+        const int qn = (q + 1) % kRegAhead;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        store(static_cast<int>((kb + 1) & 1), r[qn]);
+        load(kb + 1 + kRegAhead, r[qn]);
+        compute(kb, static_cast<int>(kb & 1));
+      }
+    }
+    for (; kb0 < KB; kb0 += kRegAhead) {
+#pragma unroll
+      for (int q = 0; q < kRegAhead; ++q) {
+        const int64_t kb = kb0 + q;
+        if (kb >= KB) break;
+        const int qn = (q + 1) % kRegAhead;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kb + 1 < KB) {
+          store(static_cast<int>((kb + 1) & 1), r[qn]);
+          if (kb + 1 + kRegAhead < KB) load(kb + 1 + kRegAhead, r[qn]);
+        }
+        compute(kb, static_cast<int>(kb & 1));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < KB) issue(s, s);
+    int slot = 0;
+    for (int64_t kb = 0; kb < KB; ++kb) {
+      if (kb + kStages - 2 < KB) stage_barrier<P * (kStages - 2)>();
+      else stage_barrier<0>();
+      if (kb + kStages - 1 < KB) issue(kb + kStages - 1, slot == 0 ? kStages - 1 : slot - 1);
+      compute(kb, slot);
+      slot = slot == kStages - 1 ? 0 : slot + 1;
+    }
   }
 
   // epilogue: lane holds routes 16 pair + 4 kq + i, column 16 tile + l % 16
