@@ -404,7 +404,7 @@ constexpr int ring_stages() {
   return 2;
 }
 // Stages the register-staged shape (GPW = 1) keeps in flight in registers
-constexpr int kRegAhead = 3;
+constexpr int kRegAhead = 2;
 // Descriptors of 32 GPW routes: 2 GPW pairs of 16, i.e. 4 GPW activation
 // operand tiles (hi and lo rows of each pair) per stage
 template <int GPW>
