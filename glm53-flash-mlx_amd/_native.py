@@ -67,6 +67,8 @@ class Router(ctypes.Structure):
         ("top_k", I64),
         ("routed_scaling_factor", F32),
         ("norm_topk_prob", I32),
+        ("n_group", I32),
+        ("topk_group", I32),
     ]
 
 

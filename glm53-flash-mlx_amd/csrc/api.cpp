@@ -136,13 +136,31 @@ int check_layout_args(int64_t matrices, int64_t rows, int64_t cols, int32_t from
   return GLM53_OK;
 }
 
+// Group-limited selection of a router (0 in either field reads as 1, the
+// ungrouped selection).
+int router_groups(const glm53_router* r) { return r->n_group > 0 ? r->n_group : 1; }
+int router_topk_groups(const glm53_router* r) { return r->topk_group > 0 ? r->topk_group : 1; }
+
+int check_groups(const glm53_router* r) {
+  const int64_t n = router_groups(r), t = router_topk_groups(r), E = r->experts;
+  CHECK_ARG(n <= 64, "n_group must be at most 64");
+  CHECK_ARG(t <= n, "topk_group %lld exceeds n_group %lld", (long long)t, (long long)n);
+  if (n > 1) {
+    CHECK_ARG(E % n == 0 && E / n >= 2, "n_group %lld must divide %lld experts into groups of two or more",
+              (long long)n, (long long)E);
+    CHECK_ARG(r->top_k <= t * (E / n), "top_k %lld exceeds the %lld experts of %lld kept groups", (long long)r->top_k,
+              (long long)(t * (E / n)), (long long)t);
+  }
+  return GLM53_OK;
+}
+
 int check_router(const glm53_router* r, int64_t H, int64_t E, int64_t k) {
   CHECK_ARG(r != nullptr && r->weight != nullptr && r->bias != nullptr, "router weight/bias is null");
   CHECK_ARG(E <= kMaxRouterExperts, "router experts must be at most %d", kMaxRouterExperts);
   CHECK_ARG(r->hidden == H && r->experts == E, "router shape [%lld, %lld] != [%lld, %lld]", (long long)r->experts,
             (long long)r->hidden, (long long)E, (long long)H);
   CHECK_ARG(r->top_k == k, "router top_k %lld != plan top_k %lld", (long long)r->top_k, (long long)k);
-  return GLM53_OK;
+  return check_groups(r);
 }
 
 int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, float* scores, hipStream_t st,
@@ -157,6 +175,8 @@ int topk(const float* logits, const glm53_router* r, int64_t T, int32_t* ids, fl
   a.top_k = static_cast<int>(r->top_k);
   a.routed_scaling_factor = r->routed_scaling_factor;
   a.norm_topk_prob = r->norm_topk_prob;
+  a.n_group = router_groups(r);
+  a.topk_group = router_topk_groups(r);
   a.ids_out = ids;
   a.scores_out = scores;
   HIP_TRY(launch_topk(a, st), "topk launch");
@@ -422,6 +442,7 @@ int glm53_router_topk(const glm53_router* router, const void* x, int64_t tokens,
             kMaxRouterExperts);
   CHECK_ARG(router->top_k > 0 && router->top_k <= kMaxTopK && router->top_k <= router->experts,
             "top_k must be in [1, %d]", kMaxTopK);
+  if (int rc = check_groups(router)) return rc;
   CHECK_ARG(tokens >= 0, "tokens < 0");
   if (tokens == 0) return GLM53_OK;
   CHECK_ARG(x && ids && scores, "null pointer argument");
@@ -658,6 +679,8 @@ int run_decode(glm53_decode_plan* p, const glm53_bank* bank, const glm53_shared_
       g.router_bias = topk_router->bias;
       g.routed_scaling_factor = topk_router->routed_scaling_factor;
       g.norm_topk_prob = topk_router->norm_topk_prob;
+      g.n_group = router_groups(topk_router);
+      g.topk_group = router_topk_groups(topk_router);
       g.ids_out = p->ids;
       g.scores_out = p->scores;
     }
@@ -817,6 +840,8 @@ int run_step(const StepContext& c, const glm53_bank* bank, const glm53_shared_ex
     a.router_bias = router->bias;
     a.routed_scaling_factor = router->routed_scaling_factor;
     a.norm_topk_prob = router->norm_topk_prob;
+    a.n_group = router_groups(router);
+    a.topk_group = router_topk_groups(router);
     a.ids = c.ids;
     a.scores = c.scores;
     a.router_wgs = static_cast<int>(cdiv(c.E, 4));

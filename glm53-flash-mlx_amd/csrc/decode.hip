@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void gate_up_swiglu_kernel(GateUpArgs a) {
     if (a.router_logits != nullptr) {  // uniform per workgroup
       if (wave == 0) {
         wave_topk_narrow(a.router_logits, a.router_bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
-                  lane, s_ids, s_w);
+                         lane, s_ids, s_w, GroupLimit{a.n_group, a.topk_group});
         if (lane == 0 && bid == 0) {
           for (int s = 0; s < a.top_k; ++s) {
             a.ids_out[s] = s_ids[s];
@@ -425,7 +425,7 @@ __device__ __forceinline__ void topk_token_partials(const TopkArgs& a, int64_t t
     }
   }
   wave_topk_words_sorted<P>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, a.ids_out + t * a.top_k,
-                            a.scores_out + t * a.top_k, scratch);
+                            a.scores_out + t * a.top_k, scratch, GroupLimit{a.n_group, a.topk_group}, a.experts);
 }
 
 // kPartials: logits come as a.splits partial planes; otherwise whole.
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     else topk_token_partials<kMaxRouterExperts / 64>(a, t, lane, sc);
   } else {
     wave_topk(a.logits + t * a.experts, a.bias, a.experts, a.top_k, a.routed_scaling_factor, a.norm_topk_prob,
-              lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k);
+              lane, a.ids_out + t * a.top_k, a.scores_out + t * a.top_k, GroupLimit{a.n_group, a.topk_group});
   }
 }
 

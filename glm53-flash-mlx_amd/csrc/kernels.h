@@ -36,6 +36,7 @@ struct GateUpArgs {
   const float* router_bias;       // [E]
   float routed_scaling_factor;
   int norm_topk_prob;
+  int n_group, topk_group;        // group-limited selection (stream_gemv.h GroupLimit)
   int32_t* ids_out;               // [top_k], written by workgroup 0
   float* scores_out;              // [top_k]
   // device code flags (0 = no 0x7F/0xFF code, register decode allowed)
@@ -77,6 +78,7 @@ struct StepArgs {
   const float* router_bias;       // [E]
   float routed_scaling_factor;
   int norm_topk_prob;
+  int n_group, topk_group;        // group-limited selection (stream_gemv.h GroupLimit)
   unsigned long long* route_words;  // [E] launch 1 exchange: sigmoid bits << 32 | selection key
   uint32_t* router_count;         // arrival counter of launch 1 (self-resetting)
   int32_t* ids;                   // [top_k]: launch 1 writes (router) or given
@@ -177,6 +179,7 @@ struct TopkArgs {
   int top_k;
   float routed_scaling_factor;
   int norm_topk_prob;
+  int n_group, topk_group;  // group-limited selection (stream_gemv.h GroupLimit)
   int32_t* ids_out;       // [tokens, top_k]
   float* scores_out;      // [tokens, top_k]
 };

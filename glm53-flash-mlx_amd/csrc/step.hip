@@ -250,7 +250,8 @@ __global__ __launch_bounds__(256) void step_router_shared_kernel(StepArgs a) {
         const int64_t c = lane + 64 * i;
         wd[i] = c < a.experts ? atomicOr(a.route_words + c, 0ull) : 0ull;
       }
-      wave_topk_words_sorted<5>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids, s_w, s_topk);
+      wave_topk_words_sorted<5>(wd, a.top_k, a.routed_scaling_factor, a.norm_topk_prob, lane, s_ids, s_w, s_topk,
+                                GroupLimit{a.n_group, a.topk_group}, a.experts);
       if (lane < a.top_k) {
         a.ids[lane] = s_ids[lane];
         a.scores[lane] = s_w[lane];

@@ -241,6 +241,74 @@ __device__ __forceinline__ uint32_t orderable_bits(float v) {
 // (so a score computed where the logit is made equals one computed later).
 __device__ __forceinline__ float router_sigmoid(float logit) { return 1.0f / (1.0f + expf(-logit)); }
 
+// The float an orderable image stands for (inverse of orderable_bits).
+__device__ __forceinline__ float orderable_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
+// Group-limited selection, the DeepSeek-V3 rule that mlx-vlm's
+// dsv32.group_expert_select applies when n_group > 1 (patch.py:134-142
+// passes n_group and topk_group): the experts form n_group groups of
+// experts / n_group consecutive ids; a group's score is the FP32 sum of its
+// two largest biased scores; the n_group - topk_group groups of lowest score
+// have every biased score replaced by 0.0 before the top-k.  Ties between
+// group scores keep the lower group index (MLX's argpartition leaves them
+// unspecified).  n_group = 1 selects over all experts unchanged.
+struct GroupLimit {
+  int n_group = 1;
+  int topk_group = 1;
+};
+
+// Applies a GroupLimit to the keys of one token held as in wave_topk_regs
+// (key[i] of expert lane + 64 i; 0 = absent).  One pass per group: each lane's
+// two largest keys in the group, a wave max for the largest, a second wave
+// max over every lane's next candidate (the second key of one lane holding
+// the largest, the largest of the others) for the runner-up.  n_group <= 64,
+// experts / n_group >= 2.
+template <int PER_LANE>
+__device__ __forceinline__ void group_limit_keys(uint32_t (&key)[PER_LANE], int64_t experts, GroupLimit gl, int lane) {
+  const int64_t per = experts / gl.n_group;
+  float gscore = 0.0f;  // lane g < n_group: the score of group g
+#pragma unroll 1
+  for (int g = 0; g < gl.n_group; ++g) {
+    uint32_t b1 = 0u, b2 = 0u;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) {
+      const int64_t c = lane + 64 * i;
+      if (c < experts && c / per == g) {
+        const uint32_t k = key[i];
+        if (k > b1) {
+          b2 = b1;
+          b1 = k;
+        } else if (k > b2) {
+          b2 = k;
+        }
+      }
+    }
+    const uint32_t m1 = wave_max_u32(b1);
+    const unsigned long long holders = __ballot(b1 == m1);
+    const int first = __ffsll(static_cast<long long>(holders)) - 1;
+    const uint32_t m2 = wave_max_u32(lane == first ? b2 : b1);
+    if (lane == g) gscore = __fadd_rn(orderable_value(m1), orderable_value(m2));
+  }
+  bool keep = false;
+  if (lane < gl.n_group) {
+    int rank = 0;
+#pragma unroll 1
+    for (int h = 0; h < gl.n_group; ++h) {
+      const float sh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), h));
+      rank += (sh > gscore || (sh == gscore && h < lane)) ? 1 : 0;
+    }
+    keep = rank < gl.topk_group;
+  }
+  const unsigned long long kept = __ballot(keep);
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) {
+    const int64_t c = lane + 64 * i;
+    if (c < experts && !((kept >> (c / per)) & 1ull)) key[i] = 0x80000000u;  // orderable image of +0.0
+  }
+}
+
 // Core selection over logits already in registers: lg[i] is the logit of
 // expert lane + 64 * i (ignored when that is >= experts).  Each of the top_k
 // rounds is two DPP reductions: the largest biased score (as its orderable
@@ -249,7 +317,7 @@ __device__ __forceinline__ float router_sigmoid(float logit) { return 1.0f / (1.
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], const float* __restrict__ bias,
                                                int64_t experts, int top_k, float scaling, int norm, int lane,
-                                               int32_t* ids_dst, float* w_dst) {
+                                               int32_t* ids_dst, float* w_dst, GroupLimit gl = {}) {
   uint32_t key[PER_LANE];  // orderable image of the biased score; 0 = taken / absent
   float sigs[PER_LANE];
 #pragma unroll
@@ -263,6 +331,7 @@ __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], cons
     }
     sigs[i] = sg;
   }
+  if (gl.n_group > 1) group_limit_keys<PER_LANE>(key, experts, gl, lane);
   float total = 0.0f;
   float w_mine = 0.0f;  // lane `slot` keeps the weight of its slot
 #pragma unroll 1
@@ -305,7 +374,8 @@ __device__ __forceinline__ void wave_topk_regs(const float (&lg)[PER_LANE], cons
 // the winning lane drops that entry and recomputes its head.
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_words(const unsigned long long (&wd)[PER_LANE], int top_k, float scaling,
-                                                int norm, int lane, int32_t* ids_dst, float* w_dst) {
+                                                int norm, int lane, int32_t* ids_dst, float* w_dst,
+                                                GroupLimit gl = {}, int64_t experts = 0) {
   uint32_t key[PER_LANE];
   float sig[PER_LANE];
 #pragma unroll
@@ -313,6 +383,7 @@ __device__ __forceinline__ void wave_topk_words(const unsigned long long (&wd)[P
     key[i] = static_cast<uint32_t>(wd[i]);
     sig[i] = __uint_as_float(static_cast<uint32_t>(wd[i] >> 32));
   }
+  if (gl.n_group > 1) group_limit_keys<PER_LANE>(key, experts, gl, lane);
   uint32_t hk;
   int hi;
   float hs;
@@ -439,16 +510,19 @@ struct TopkScratch {
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_words_sorted(const unsigned long long (&wd)[PER_LANE], int top_k,
                                                        float scaling, int norm, int lane, int32_t* ids_dst,
-                                                       float* w_dst, TopkScratch& s) {
+                                                       float* w_dst, TopkScratch& s, GroupLimit gl = {},
+                                                       int64_t experts = 0) {
   uint32_t key[PER_LANE];
   float sig[PER_LANE];
-  uint32_t head = 0;
 #pragma unroll
   for (int i = 0; i < PER_LANE; ++i) {
     key[i] = static_cast<uint32_t>(wd[i]);
     sig[i] = __uint_as_float(static_cast<uint32_t>(wd[i] >> 32));
-    head = max(head, key[i]);
   }
+  if (gl.n_group > 1) group_limit_keys<PER_LANE>(key, experts, gl, lane);
+  uint32_t head = 0;
+#pragma unroll
+  for (int i = 0; i < PER_LANE; ++i) head = max(head, key[i]);
   const uint32_t bound = __builtin_amdgcn_readlane(wave_sort_desc(head, lane), top_k - 1);
   unsigned long long mask[PER_LANE];
   int count = 0;
@@ -458,7 +532,7 @@ __device__ __forceinline__ void wave_topk_words_sorted(const unsigned long long 
     count += __popcll(mask[i]);
   }
   if (count > 64) {
-    wave_topk_words<PER_LANE>(wd, top_k, scaling, norm, lane, ids_dst, w_dst);
+    wave_topk_words<PER_LANE>(wd, top_k, scaling, norm, lane, ids_dst, w_dst, gl, experts);
     return;
   }
   int base = 0;
@@ -500,22 +574,22 @@ __device__ __forceinline__ void wave_topk_words_sorted(const unsigned long long 
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk_emit(const float* __restrict__ logits, const float* __restrict__ bias,
                                                int64_t experts, int top_k, float scaling, int norm, int lane,
-                                               int32_t* ids_dst, float* w_dst) {
+                                               int32_t* ids_dst, float* w_dst, GroupLimit gl) {
   float lg[PER_LANE];
 #pragma unroll
   for (int i = 0; i < PER_LANE; ++i) {
     const int64_t c = lane + 64 * i;
     lg[i] = c < experts ? logits[c] : 0.0f;
   }
-  wave_topk_regs<PER_LANE>(lg, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+  wave_topk_regs<PER_LANE>(lg, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
 }
 
 __device__ __forceinline__ void wave_topk(const float* __restrict__ logits, const float* __restrict__ bias,
                                           int64_t experts, int top_k, float scaling, int norm, int lane,
-                                          int32_t* ids_dst, float* w_dst) {
-  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else if (experts <= 320) wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else wave_topk_emit<kMaxRouterExperts / 64>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+                                          int32_t* ids_dst, float* w_dst, GroupLimit gl) {
+  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
+  else if (experts <= 320) wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
+  else wave_topk_emit<kMaxRouterExperts / 64>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
 }
 
 // Narrow form for the gate/up prologue (experts <= 320; wider routers select
@@ -523,9 +597,9 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ logits, cons
 // register count.
 __device__ __forceinline__ void wave_topk_narrow(const float* __restrict__ logits, const float* __restrict__ bias,
                                                  int64_t experts, int top_k, float scaling, int norm, int lane,
-                                                 int32_t* ids_dst, float* w_dst) {
-  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
-  else wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst);
+                                                 int32_t* ids_dst, float* w_dst, GroupLimit gl) {
+  if (experts <= 128) wave_topk_emit<2>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
+  else wave_topk_emit<5>(logits, bias, experts, top_k, scaling, norm, lane, ids_dst, w_dst, gl);
 }
 
 }  // namespace glm53

@@ -9,7 +9,7 @@ and FakeTensor / meta propagation gets the output shapes without a device.
 * ``glm53::block_fp8_linear(x, weight, scale_inv, code_flags?)`` -- fp8.py
   ``block_fp8_linear``;
 * ``glm53::router_topk(x, weight, bias, top_k, routed_scaling_factor,
-  norm_topk_prob)`` -- ``Float32Gate``;
+  norm_topk_prob, n_group, topk_group)`` -- ``Float32Gate``;
 * ``glm53::moe_decode(x, owner, expert_ids?, scores?)`` -- one token through
   a ``PackedFP8MoE`` (router + routed + shared, or caller routing);
 * ``glm53::moe_prefill(x, owner, expert_ids?, scores?)`` -- the grouped
@@ -63,14 +63,14 @@ def _(x, weight, scale_inv, code_flags):
 
 @torch.library.custom_op("glm53::router_topk", mutates_args=())
 def router_topk(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, top_k: int, routed_scaling_factor: float,
-                norm_topk_prob: bool) -> tuple[torch.Tensor, torch.Tensor]:
+                norm_topk_prob: bool, n_group: int = 1, topk_group: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
     from .router import native_router_topk
 
-    return native_router_topk(x, weight, bias, top_k, routed_scaling_factor, norm_topk_prob)
+    return native_router_topk(x, weight, bias, top_k, routed_scaling_factor, norm_topk_prob, n_group, topk_group)
 
 
 @router_topk.register_fake
-def _(x, weight, bias, top_k, routed_scaling_factor, norm_topk_prob):
+def _(x, weight, bias, top_k, routed_scaling_factor, norm_topk_prob, n_group=1, topk_group=1):
     lead = x.shape[:-1]
     return (x.new_empty((*lead, top_k), dtype=torch.int32), x.new_empty((*lead, top_k), dtype=torch.float32))
 

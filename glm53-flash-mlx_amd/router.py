@@ -5,9 +5,13 @@ logits = x_f32 @ W_f32^T, sigma = sigmoid(logits), choice = sigma + bias
 expert id asc), weights = sigma[ids] normalised when ``norm_topk_prob`` and
 multiplied by ``routed_scaling_factor``.  The selection rule is the
 DeepSeek-V3 auxiliary-loss-free rule that mlx-vlm's
-``dsv32.group_expert_select`` implements, with n_group = 1; the slot order
-(MLX leaves argpartition order unspecified) is this build's documented tie
-policy.  One token runs a one-workgroup-per-logit kernel, several tokens an
+``dsv32.group_expert_select`` implements: with n_group > 1 the experts form
+n_group groups of consecutive ids, each scored by the FP32 sum of its two
+largest biased scores, and the biased scores outside the topk_group best
+groups become 0.0 before the top-k.  The slot order and the order of equal
+group scores (MLX leaves argpartition order unspecified) are this build's
+documented tie policy: (choice desc, expert id asc), lower group index
+kept.  One token runs a one-workgroup-per-logit kernel, several tokens an
 LDS-tiled BF16-MFMA GEMM over the exact three-way BF16 split of the FP32
 weights; then a wavefront-per-token top-k.
 """
@@ -29,15 +33,14 @@ class Float32Gate(torch.nn.Module):
             raise ValueError("router weight must be a 2-D float32 [experts, hidden] tensor")
         if bias.dtype != torch.float32 or bias.shape != (weight.shape[0],):
             raise ValueError("e_score_correction_bias must be float32 [experts]")
-        if n_group != 1 or topk_group != 1:
-            raise ValueError("grouped expert selection (n_group > 1) is not part of this path")
+        check_groups(weight.shape[0], int(top_k), int(n_group), int(topk_group))
         self.register_buffer("weight", weight.contiguous())
         self.register_buffer("e_score_correction_bias", bias.contiguous())
         self.top_k = int(top_k)
         self.routed_scaling_factor = float(routed_scaling_factor)
         self.norm_topk_prob = bool(norm_topk_prob)
-        self.n_group = n_group
-        self.topk_group = topk_group
+        self.n_group = int(n_group)
+        self.topk_group = int(topk_group)
 
     @property
     def n_routed_experts(self) -> int:
@@ -45,7 +48,8 @@ class Float32Gate(torch.nn.Module):
 
     def as_c_struct(self) -> N.Router:
         return N.Router(self.weight.data_ptr(), self.e_score_correction_bias.data_ptr(), self.weight.shape[0],
-                        self.weight.shape[1], self.top_k, self.routed_scaling_factor, int(self.norm_topk_prob))
+                        self.weight.shape[1], self.top_k, self.routed_scaling_factor, int(self.norm_topk_prob),
+                        self.n_group, self.topk_group)
 
     def forward(self, x):
         N.require_device(x, self.weight)
@@ -55,10 +59,25 @@ class Float32Gate(torch.nn.Module):
         if x.shape[-1] != hidden:
             raise ValueError(f"input width {x.shape[-1]} != router width {hidden}")
         return torch.ops.glm53.router_topk(x, self.weight, self.e_score_correction_bias, self.top_k,
-                                           self.routed_scaling_factor, self.norm_topk_prob)
+                                           self.routed_scaling_factor, self.norm_topk_prob, self.n_group,
+                                           self.topk_group)
 
 
-def native_router_topk(x, weight, bias, top_k: int, routed_scaling_factor: float, norm_topk_prob: bool):
+def check_groups(experts: int, top_k: int, n_group: int, topk_group: int) -> None:
+    """ValueError unless (n_group, topk_group) is a selection the kernels take:
+    1 <= topk_group <= n_group <= 64, n_group dividing the experts into
+    groups of two or more, and top_k experts available in the kept groups."""
+    if not 1 <= topk_group <= n_group <= 64:
+        raise ValueError(f"need 1 <= topk_group <= n_group <= 64, got n_group={n_group}, topk_group={topk_group}")
+    if n_group > 1:
+        if experts % n_group or experts // n_group < 2:
+            raise ValueError(f"n_group={n_group} must split {experts} experts into equal groups of two or more")
+        if top_k > topk_group * (experts // n_group):
+            raise ValueError(f"top_k={top_k} exceeds the {topk_group * (experts // n_group)} experts of the kept groups")
+
+
+def native_router_topk(x, weight, bias, top_k: int, routed_scaling_factor: float, norm_topk_prob: bool,
+                       n_group: int = 1, topk_group: int = 1):
     """The native call behind the glm53::router_topk op."""
     hidden = weight.shape[1]
     flat = x.reshape(-1, hidden).contiguous()
@@ -69,7 +88,7 @@ def native_router_topk(x, weight, bias, top_k: int, routed_scaling_factor: float
     ws_bytes = lib.glm53_router_workspace_bytes(tokens, hidden, weight.shape[0])
     ws = N.workspace(ws_bytes, x.device)
     router = N.Router(weight.data_ptr(), bias.data_ptr(), weight.shape[0], hidden, top_k, float(routed_scaling_factor),
-                      int(norm_topk_prob))
+                      int(norm_topk_prob), int(n_group), int(topk_group))
     N.check(lib.glm53_router_topk(N.ctypes.byref(router), N.ptr(flat), tokens, N.ptr(ids), N.ptr(scores),
                                   N.ptr(ws), ws_bytes, N.stream_handle(x.device)))
     lead = x.shape[:-1]

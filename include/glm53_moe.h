@@ -144,6 +144,15 @@ typedef struct glm53_router {
   int64_t top_k;
   float routed_scaling_factor;
   int32_t norm_topk_prob;
+  /* Group-limited selection (patch.py:134-142 passes n_group and
+   * topk_group to group_expert_select): the experts form n_group groups of
+   * consecutive ids, a group scores the FP32 sum of its two largest biased
+   * scores, and the biased scores of all but the topk_group best groups
+   * (ties: lower group index kept) become 0.0 before the top-k.  0 or 1 in
+   * both: no grouping.  n_group <= 64, dividing experts into groups of at
+   * least two; top_k <= topk_group * experts / n_group. */
+  int32_t n_group;
+  int32_t topk_group;
 } glm53_router;
 
 const char* glm53_last_error(void);
@@ -174,7 +183,8 @@ int glm53_fp8_linear(const void* x, int64_t M, int64_t K, const uint8_t* weight,
 
 /* ------------------------------------------------------------------------
  * Router -- replaces patch.py:131-142 `Float32Gate.__call__` (with the
- * selection half of mlx-vlm dsv32.group_expert_select, n_group = 1).
+ * selection half of mlx-vlm dsv32.group_expert_select, group-limited when
+ * the router's n_group > 1).
  * x bf16 [tokens, H] -> ids int32 [tokens, top_k], scores f32 [tokens, top_k].
  * The workspace holds, for several tokens, the FP32 partial sums of the
  * BF16-MFMA logits (up to 16 K chunks x tokens x experts floats) and FP32

@@ -217,8 +217,42 @@ void glm53o_swiglu(const uint16_t* gate, const uint16_t* up, int64_t n, float li
  * leaves slot order unspecified.  `choice_out` (optional, [T, E]) returns the
  * biased scores for near-tie analysis.
  */
+/*
+ * Group-limited selection (the DeepSeek-V3 rule of mlx-vlm
+ * dsv32.group_expert_select for n_group > 1; patch.py:134-142 passes
+ * n_group and topk_group): groups of E / n_group consecutive experts, group
+ * score = FP32 sum of the group's two largest biased scores, and the biased
+ * scores of every group outside the topk_group best (equal scores: the lower
+ * group index ranks first) set to 0.0 before the top-k.
+ */
+static void group_limit(float* choice, int64_t E, int64_t n_group, int64_t topk_group) {
+    if (n_group <= 1) return;
+    const int64_t per = E / n_group;
+    float gs[64];
+    for (int64_t g = 0; g < n_group; ++g) {
+        float m1 = -INFINITY, m2 = -INFINITY;
+        for (int64_t e = g * per; e < (g + 1) * per; ++e) {
+            const float v = choice[e];
+            if (v > m1) {
+                m2 = m1;
+                m1 = v;
+            } else if (v > m2) {
+                m2 = v;
+            }
+        }
+        gs[g] = m1 + m2;
+    }
+    for (int64_t g = 0; g < n_group; ++g) {
+        int64_t rank = 0;
+        for (int64_t h = 0; h < n_group; ++h)
+            if (gs[h] > gs[g] || (gs[h] == gs[g] && h < g)) ++rank;
+        if (rank >= topk_group)
+            for (int64_t e = g * per; e < (g + 1) * per; ++e) choice[e] = 0.0f;
+    }
+}
+
 void glm53o_router(const uint16_t* x, int64_t T, int64_t H, const float* w, const float* bias,
-                   int64_t E, int64_t top_k, float scaling, int norm,
+                   int64_t E, int64_t top_k, float scaling, int norm, int64_t n_group, int64_t topk_group,
                    int32_t* ids_out, float* scores_out, float* choice_out) {
     float* xf = (float*)malloc(sizeof(float) * (size_t)(T * H));
     float* logits = (float*)malloc(sizeof(float) * (size_t)(T * E));
@@ -232,9 +266,11 @@ void glm53o_router(const uint16_t* x, int64_t T, int64_t H, const float* w, cons
             double l = logits[t * E + e];
             sig[e] = (float)(1.0 / (1.0 + exp(-l)));
             choice[e] = sig[e] + bias[e];
-            if (choice_out) choice_out[t * E + e] = choice[e];
             taken[e] = 0;
         }
+        group_limit(choice, E, n_group, topk_group);
+        if (choice_out)
+            for (int64_t e = 0; e < E; ++e) choice_out[t * E + e] = choice[e];
         float total = 0.0f;
         for (int64_t slot = 0; slot < top_k; ++slot) {
             int64_t best = -1;

@@ -73,7 +73,7 @@ def _declare(L):
     L.glm53o_sigmoid_bf16.restype = ctypes.c_uint16
     L.glm53o_sigmoid_bf16.argtypes = [ctypes.c_uint16]
     L.glm53o_swiglu.argtypes = [P, P, I64, ctypes.c_float, P]
-    L.glm53o_router.argtypes = [P, I64, I64, P, P, I64, I64, ctypes.c_float, ctypes.c_int, P, P, P]
+    L.glm53o_router.argtypes = [P, I64, I64, P, P, I64, I64, ctypes.c_float, ctypes.c_int, I64, I64, P, P, P]
     L.glm53o_weighted_reduction.argtypes = [P, P, I64, I64, P]
     L.glm53o_add_bf16.argtypes = [P, P, I64, P]
     L.glm53o_hc_expand.argtypes = [P, P, P, P, I64, I64, P]
@@ -207,12 +207,15 @@ def swiglu(gate_bits: np.ndarray, up_bits: np.ndarray, limit: float) -> np.ndarr
 # ---------------------------------------------------------------- router ---
 
 def router(x_bits, weight, bias, *, top_k=8, routed_scaling_factor=1.0, norm_topk_prob=True,
-           return_choice=False):
+           return_choice=False, n_group=1, topk_group=1):
     """patch.py:131-142 FP32 router + DeepSeek-V3 aux-loss-free selection.
 
     Selection parity with mlx-vlm's ``group_expert_select`` is unpinned (the
-    module is absent); the rule here is the published one with n_group = 1 and
-    the tie policy (biased score desc, expert id asc).
+    module is absent); the rule here is the published one -- with n_group > 1
+    groups of consecutive experts scored by the sum of their two largest
+    biased scores, all but the topk_group best zeroed -- and the tie policy
+    (biased score desc, expert id asc; equal group scores: lower group kept).
+    ``choice`` (return_choice) is the biased score after the group limit.
     """
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     lead = x.shape[:-1]
@@ -226,7 +229,7 @@ def router(x_bits, weight, bias, *, top_k=8, routed_scaling_factor=1.0, norm_top
     scores = np.zeros((t, top_k), dtype=np.float32)
     choice = np.zeros((t, e), dtype=np.float32)
     lib().glm53o_router(_p(x2), t, h, _p(w), _p(b), e, top_k, float(routed_scaling_factor),
-                        int(bool(norm_topk_prob)), _p(ids), _p(scores), _p(choice))
+                        int(bool(norm_topk_prob)), int(n_group), int(topk_group), _p(ids), _p(scores), _p(choice))
     ids = ids.reshape(*lead, top_k)
     scores = scores.reshape(*lead, top_k)
     if return_choice:

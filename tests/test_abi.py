@@ -130,12 +130,45 @@ def test_invalid_arguments_fail_before_any_device_work(N, libso):
         (lambda: libso.glm53_decode_plan_identities(None, 0, None, 0, P(16)), "null pointer"),
         (lambda: libso.glm53_prefill_plan_identities(None, None, 0, P(16)), "null pointer"),
     ]
+    def grouped(experts, top_k, n_group, topk_group):  # a router struct with fake (never read) pointers
+        return ctypes.byref(N.Router(16, 16, experts, 64, top_k, 1.0, 1, n_group, topk_group))
+
+    cases += [
+        (lambda: libso.glm53_router_topk(grouped(288, 8, 7, 2), P(16), 0, P(16), P(16), P(16), 1 << 20, None),
+         "groups of two or more"),
+        (lambda: libso.glm53_router_topk(grouped(288, 8, 8, 9), P(16), 0, P(16), P(16), P(16), 1 << 20, None),
+         "exceeds n_group"),
+        (lambda: libso.glm53_router_topk(grouped(32, 8, 8, 1), P(16), 0, P(16), P(16), P(16), 1 << 20, None),
+         "kept groups"),
+        (lambda: libso.glm53_router_topk(grouped(256, 8, 128, 8), P(16), 0, P(16), P(16), P(16), 1 << 20, None),
+         "at most 64"),
+    ]
     for call, fragment in cases:
         assert call() == N.INVALID_ARGUMENT, fragment
         assert fragment in libso.glm53_last_error().decode(), (fragment, libso.glm53_last_error())
         with pytest.raises(ValueError):
             N.check(N.INVALID_ARGUMENT)
     assert libso.glm53_split_activations(P(16), 0, 128, 128, P(16), P(16), P(16), None) == N.OK  # empty: no work
+    # zero-filled group fields (a caller built against the struct without them) select ungrouped
+    assert libso.glm53_router_topk(grouped(288, 8, 0, 0), P(16), 0, P(16), P(16), P(16), 1 << 20, None) == N.OK
+
+
+def test_float32_gate_refuses_unsupported_groups():
+    """Float32Gate(n_group, topk_group) takes what the kernels take and
+    raises ValueError otherwise (the reference forwards both to
+    group_expert_select, patch.py:134-142)."""
+    import torch
+
+    from conftest import pkg
+
+    M = pkg()
+    w, b = torch.zeros(288, 64), torch.zeros(288)
+    M.Float32Gate(w, b, top_k=8, n_group=8, topk_group=4)
+    for n_group, topk_group, top_k in ((7, 2, 8), (8, 9, 8), (8, 0, 8), (96, 8, 8), (8, 1, 37)):
+        with pytest.raises(ValueError):
+            M.Float32Gate(w, b, top_k=top_k, n_group=n_group, topk_group=topk_group)
+    with pytest.raises(ValueError):
+        M.Float32Gate(torch.zeros(7, 64), torch.zeros(7), top_k=2, n_group=7, topk_group=1)  # groups of one
 
 
 def test_product_refuses_cpu_tensors():

@@ -274,6 +274,79 @@ def test_router_brute_force_selection_bias_and_ties(O):
     assert np.allclose(scores.sum(-1), 2.5, rtol=1e-5)
 
 
+def _biased_router(bias_rows):
+    """A router whose biased scores are 0.5 + bias exactly: zero weights make
+    every logit 0 and every sigmoid 0.5, for one token per bias row."""
+    from oracle import oracle
+
+    bias_rows = np.asarray(bias_rows, dtype=np.float32)
+    e = bias_rows.shape[-1]
+    x = oracle.f32_to_bf16(np.ones((1, 8), dtype=np.float32))
+    return x, np.zeros((e, 8), dtype=np.float32), bias_rows
+
+
+def test_router_group_limited_known_answers(O):
+    """Group-limited selection (patch.py:134-142 passes n_group, topk_group to
+    mlx-vlm's group_expert_select; the published DeepSeek-V3 rule): groups of
+    consecutive experts scored by the sum of their two largest biased scores,
+    all but the topk_group best groups zeroed, then the top-k.  Known answers
+    on constructed scores (16 experts, 4 groups of 4):
+
+    group 0: 0.90 0.89 0.20 0.20 -> 1.79   group 1: 0.95 0.30 0.30 0.30 -> 1.25
+    group 2: 0.80 0.80 0.80 0.80 -> 1.60   group 3: 0.60 0.60 0.60 0.60 -> 1.20
+
+    keeps groups 0 and 2, so the top-4 is experts 0, 1, 8, 9: expert 4 (the
+    largest score, 0.95) is dropped with its group, and ungrouped selection
+    (n_group = 1) picks 4, 0, 1, 8 instead.  A group's second score counts
+    even when it equals the first (group 2 scores 1.60, not 0.80)."""
+    b = np.array([0.40, 0.39, -0.30, -0.30, 0.45, -0.20, -0.20, -0.20,
+                  0.30, 0.30, 0.30, 0.30, 0.10, 0.10, 0.10, 0.10])
+    x, w, bias = _biased_router(b)
+    ids, sc, choice = O.router(x, w, bias, top_k=4, n_group=4, topk_group=2, return_choice=True)
+    assert ids[0].tolist() == [0, 1, 8, 9]
+    assert np.allclose(sc[0], 0.25)  # equal sigmoids, normalised
+    assert np.all(choice[0, 4:8] == 0.0) and np.all(choice[0, 12:] == 0.0)
+    assert O.router(x, w, bias, top_k=4)[0][0].tolist() == [4, 0, 1, 8]
+    # topk_group = n_group keeps every group: the ungrouped answer
+    assert O.router(x, w, bias, top_k=4, n_group=4, topk_group=4)[0][0].tolist() == [4, 0, 1, 8]
+    # one group kept: group 0 alone
+    assert O.router(x, w, bias, top_k=4, n_group=4, topk_group=1)[0][0].tolist() == [0, 1, 2, 3]
+    # equal group scores: the lower group index is kept
+    b2 = np.array([0.2, 0.1, 0.0, 0.0, 0.1, 0.2, 0.3, -0.4])  # groups of 4: 0.7+0.6 = 1.3 against 0.8+0.7 = 1.5
+    x, w, bias = _biased_router(b2)
+    assert O.router(x, w, bias, top_k=2, n_group=2, topk_group=1)[0][0].tolist() == [6, 5]
+    b3 = np.array([0.3, 0.2, 0.0, 0.0, 0.2, 0.3, 0.0, 0.0])  # both groups 0.8 + 0.7
+    x, w, bias = _biased_router(b3)
+    assert O.router(x, w, bias, top_k=2, n_group=2, topk_group=1)[0][0].tolist() == [0, 1]
+
+
+def test_router_group_limited_equals_restricted_selection(O):
+    """Property on random scores: when every kept group has at least top_k
+    positive biased scores, the group-limited top-k equals the ungrouped top-k
+    restricted to the experts of the kept groups, and each kept group's score
+    is at least every dropped group's."""
+    from oracle import oracle
+
+    rng = np.random.default_rng(5)
+    T, H, E, G, keep, k = 12, 64, 64, 8, 3, 6
+    x = oracle.f32_to_bf16(rng.normal(size=(T, H)).astype(np.float32))
+    w = (rng.normal(size=(E, H)) * 0.1).astype(np.float32)
+    bias = (rng.normal(size=E) * 0.05).astype(np.float32)
+    ids, _, _ = O.router(x, w, bias, top_k=k, n_group=G, topk_group=keep, return_choice=True)
+    _, _, choice0 = O.router(x, w, bias, top_k=k, return_choice=True)
+    per = E // G
+    for t in range(T):
+        grp = choice0[t].reshape(G, per)
+        top2 = np.sort(grp, axis=1)[:, -2:]
+        gscore = (top2[:, 1] + top2[:, 0]).astype(np.float32)
+        kept = sorted(range(G), key=lambda g: (-float(gscore[g]), g))[:keep]
+        assert min(gscore[kept]) >= max(np.delete(gscore, kept))
+        allowed = [e for e in range(E) if e // per in kept]
+        assert all(choice0[t, e] > 0 for e in allowed)
+        order = sorted(allowed, key=lambda e: (-float(choice0[t, e]), e))[:k]
+        assert ids[t].tolist() == order
+
+
 # ------------------------------------------------------------ tile plan ---
 
 def test_tile_plan_reference_kat():
