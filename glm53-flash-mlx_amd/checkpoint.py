@@ -233,7 +233,8 @@ def layer_config(root) -> SimpleNamespace:
                            num_experts_per_tok=int(text["num_experts_per_tok"]),
                            n_shared_experts=int(text.get("n_shared_experts") or 0),
                            routed_scaling_factor=float(text.get("routed_scaling_factor", 1.0)),
-                           norm_topk_prob=bool(text.get("norm_topk_prob", True)))
+                           norm_topk_prob=bool(text.get("norm_topk_prob", True)),
+                           n_group=int(text.get("n_group") or 1), topk_group=int(text.get("topk_group") or 1))
 
 
 def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = None, *, layout=None):
@@ -304,5 +305,7 @@ def load_moe_layer(root, layer: int, device, config: SimpleNamespace | None = No
     weight = torch.from_numpy(np.array(_float32(root, tensors[keys.router]))).to(device)
     bias = torch.from_numpy(np.array(_float32(root, tensors[keys.bias]))).to(device)
     gate = Float32Gate(weight, bias, top_k=config.num_experts_per_tok,
-                       routed_scaling_factor=config.routed_scaling_factor, norm_topk_prob=config.norm_topk_prob)
+                       routed_scaling_factor=config.routed_scaling_factor, norm_topk_prob=config.norm_topk_prob,
+                       n_group=int(getattr(config, "n_group", 1) or 1),
+                       topk_group=int(getattr(config, "topk_group", 1) or 1))
     return bank, shared, gate
