@@ -801,8 +801,8 @@ __device__ __forceinline__ void grouped_gemm_loop(const GroupedGemmArgs& a, cons
 
 // Activation block scales of a work item's ROUTES routes into LDS as E8M0
 // codes, K-block-major: [kb][r], or for the wide shape (WIDE)
-// [kb][wr][r % 16][j] with r = 16 (wr + 2 j) + r % 16, so that a wavefront
-// of row wr reads the codes of its four pairs as one word.  THREADS / ROUTES
+// [kb][r % 16][r / 16], so that a lane reads the codes of its row in all
+// eight pairs as one 8-byte word.  THREADS / ROUTES
 // threads per route, each with its route's token row, eight loads in
 // flight per thread, then the stores; indices past the last K block are
 // clamped to it, so every load and store is unconditional (a clamped store
@@ -818,7 +818,7 @@ __device__ __forceinline__ void load_activation_scales(const ItemSource& src, in
   const int64_t route = start + (r < len ? r : len - 1);
   const int64_t token = src.a_row_index != nullptr ? src.a_row_index[route] : route;
   const float* row = src.a_scale + token * KB;
-  const int64_t pos = WIDE ? ((((r >> 4) & 1) * 16 + (r & 15)) * 4 + (r >> 5)) : r;
+  const int64_t pos = WIDE ? ((r & 15) * 8 + (r >> 4)) : r;
   constexpr int64_t kStride = WIDE ? 128 : ROUTES;  // bytes per K block
   for (int64_t kb0 = sub; kb0 < KB; kb0 += 8 * TPR) {
     float v[8];
@@ -1005,31 +1005,32 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
 // ------------------------------------------ grouped GEMM, wide shape --
 //
 // For plans whose experts carry many routes: work item = one 128-route
-// descriptor (8 pairs of 16 routes) x 384 weight rows (PLAIN: 384 output
-// columns; SWIGLU: 192 gate rows and the matching 192 up rows), one
-// 512-thread workgroup per CU (8 wavefronts, two per SIMD).  Against the
-// 64-route x 128-row item a heavy expert's weight tile streams once per 128
-// routes instead of 64 and an activation row once per 384 weight rows
-// instead of 128.  Wavefront w = 4 wr + wc multiplies pairs wr, wr + 2,
-// wr + 4, wr + 6 against six 16-row weight tiles (PLAIN: tiles 6 wc .. 6 wc
-// + 5; SWIGLU: gate tiles 3 wc .. 3 wc + 2 and up tiles 12 + 3 wc .. 12 + 3
-// wc + 2): per stage 12 KB of B and 16 KB of A operand reads for 48 MFMAs.
-// The LDS holds one B stage (24 tiles, 48 KB) and a 2-stage A ring (2 x 32
-// KB): each wavefront reads its six B tiles into registers at the start of
-// a stage, a second barrier then frees the B buffer and the next stage's
-// weight tiles stream into it behind this stage's MFMAs.  Each wavefront
-// issues the direct loads of weight tiles 3 w .. 3 w + 2 and of pair w's hi
-// and lo tiles (none when the pair holds no routes).  The arithmetic per
-// output element is that of the narrower shapes, so every shape gives the
-// same bits.
+// descriptor (8 pairs of 16 routes) x 512 weight rows (PLAIN: 512 output
+// columns; SWIGLU: 256 gate rows and the matching 256 up rows), one
+// 512-thread workgroup per CU (8 wavefronts, two per SIMD).  Wavefront w
+// multiplies every pair of the descriptor against its own four 16-row
+// weight tiles (PLAIN: output columns 64 w .. 64 w + 63 of the item;
+// SWIGLU: gate rows 32 w .. 32 w + 31 and the matching up rows), so all
+// wavefronts carry the same work whatever the descriptor's route count.
+// The wavefront loads its four tiles itself (direct loads into its own
+// 8 KB of a single-buffered 64 KB B stage) and reads them into registers at
+// the start of each stage; once those reads have returned it issues the
+// next stage's tiles into the same bytes, so the weight stream needs no
+// workgroup barrier and runs a whole stage ahead.  The activations come
+// through a 2-stage ring of 32 KB stages (wavefront w loads pair w's hi and
+// lo tiles); one barrier per stage makes a stage's activation tiles
+// visible and frees the other slot.  Per stage 8 KB of B and 32 KB of A
+// operand reads for 64 MFMAs per wavefront.  The arithmetic per output
+// element is that of the narrower shapes, so every shape gives the same
+// bits.
 namespace {
 constexpr int kWidePairs = kGemmWideRows / 16;            // 8
-constexpr int kWideTilesPerWave = 6;                      // weight tiles per wavefront
-constexpr int kWideBTiles = 4 * kWideTilesPerWave;        // 24 tiles: 384 rows
-constexpr int kWideBBytes = kWideBTiles * kOperand;       // 48 KB
+constexpr int kWideTilesPerWave = 4;                      // weight tiles per wavefront
+constexpr int kWideBTiles = 8 * kWideTilesPerWave;        // 32 tiles: 512 rows
+constexpr int kWideBBytes = kWideBTiles * kOperand;       // 64 KB
 constexpr int kWideABytes = 2 * kWidePairs * kOperand;    // 32 KB per A stage
-constexpr int kWidePlainRows = kWideBTiles * 16;          // 384
-constexpr int kWideGateRows = kWidePlainRows / 2;         // 192
+constexpr int kWidePlainRows = kWideBTiles * 16;          // 512
+constexpr int kWideGateRows = kWidePlainRows / 2;         // 256
 }  // namespace
 
 size_t gemm_wide_lds_bytes(int64_t K) {
@@ -1039,18 +1040,19 @@ size_t gemm_wide_lds_bytes(int64_t K) {
          (kGemmWideRows + 4 * sizeof(float)) * static_cast<size_t>(K / kBlock);
 }
 
-// Direct-load sources of a wavefront, formed per load from few registers:
-// its three weight tiles' rows come from one matrix (wmat, wave-uniform)
-// starting at row row0 + 8 h + l / 8 (+ 16 q for tile q, clamped to the
-// last row), its pair's hi / lo rows from token rows tok[h].
+// Direct-load sources of a wavefront: its tiles q = 0, 1 come from matrix
+// wlo starting at row rlo (+ 16 q), tiles 2, 3 from whi at row rhi (+ 16 (q -
+// 2)), each + 8 h + lane / 8 for load h and clamped to the last row; its
+// pair's hi / lo rows from token rows tok[h].
 struct WideSources {
-  const uint8_t* wmat;     // the expert's gate, up or plain matrix
+  const uint8_t* wlo;      // PLAIN: the expert's matrix; SWIGLU: its gate rows
+  const uint8_t* whi;      // PLAIN: the same matrix; SWIGLU: its up rows
   const uint8_t* a_hi;
   const uint8_t* a_lo;
   int64_t K;
-  int32_t wg;              // row groups of wmat (common.h)
+  int32_t wg;              // row groups of the matrices (common.h)
   int32_t rows;            // rows of the matrix (loads past it re-read the last row)
-  int32_t row0;            // first row of the wavefront's tiles, + lane / 8
+  int32_t rlo, rhi;        // first rows of tiles 0 and 2, + lane / 8
   int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 16)
   int32_t tok[2];          // token rows of the pair's rows 8 h + lane / 8
 };
@@ -1060,18 +1062,19 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
                                                 int32_t start, int32_t len, int64_t KB, const WideSources& ls,
                                                 bool loads_pair, uint8_t* lds, uint32_t lds_addr, const uint8_t* lds_se,
                                                 const float* lds_sw, int wave, int lane) {
-  const int wr = wave >> 2, wc = wave & 3;
+  constexpr int T = kWideTilesPerWave;
   const OperandSlots slots = operand_slots(lane);
+  const uint32_t b_own = static_cast<uint32_t>(wave) * T * kOperand;  // this wavefront's tiles in the B stage
   auto issue_b = [&](int64_t kb) {
-    const uint32_t sb = lds_addr + 3 * wave * kOperand;
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
+    for (int q = 0; q < T; ++q)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        int32_t row = ls.row0 + 16 * q + 8 * h;
+        int32_t row = (q < 2 ? ls.rlo : ls.rhi) + 16 * (q & 1) + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (16 * h)),
-                     sb + q * kOperand + 1024 * h);
+        const uint8_t* m = q < 2 ? ls.wlo : ls.whi;
+        lds_direct16(m + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (16 * h)),
+                     lds_addr + b_own + q * kOperand + 1024 * h);
       }
   };
   auto issue_a = [&](int64_t kb, int slot) {
@@ -1085,23 +1088,17 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       }
     }
   };
-  // the LDS tile of the wavefront's weight tile tt (0..5) and the weight
-  // scale row (of lds_sw) its rows lie in
-  auto tile_of = [&](int tt) {
-    return MODE == GEMM_PLAIN ? kWideTilesPerWave * wc + tt : (tt < 3 ? 3 * wc + tt : 12 + 3 * wc + tt - 3);
-  };
-  auto sw_row = [&](int tt) -> int {
-    if (MODE == GEMM_PLAIN) return (kWideTilesPerWave * wc + tt) >> 3;
-    const int g = 3 * wc + (tt < 3 ? tt : tt - 3);                   // gate tile of the output columns
-    const int rb = (64 * static_cast<int>(ntile & 1) + 16 * g) >> 7;  // its 128-row block in the item's first
-    return (tt < 3 ? 0 : 2) + rb;
-  };
+  // weight scale row (of lds_sw) of the wavefront's tile q: PLAIN its
+  // 64 rows lie in block (64 w) / 128 of the item; SWIGLU gate tiles in
+  // gate block (32 w) / 128, up tiles in the same up block
+  const int sw_lo = MODE == GEMM_PLAIN ? (64 * wave) >> 7 : (32 * wave) >> 7;
+  const int sw_hi = MODE == GEMM_PLAIN ? sw_lo : 2 + sw_lo;
 
-  float acc[NP > 0 ? NP : 1][kWideTilesPerWave][4];
+  float acc[NP][T][4];
 #pragma unroll
   for (int j = 0; j < NP; ++j)
 #pragma unroll
-    for (int t = 0; t < kWideTilesPerWave; ++t)
+    for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
@@ -1110,58 +1107,52 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
   for (int64_t kb = 0; kb < KB; ++kb) {
     stage_barrier<0>();  // stage kb landed; every wavefront is done with stage kb - 1
     if (kb + 1 < KB) issue_a(kb + 1, slot ^ 1);
-    i32x8 bq[kWideTilesPerWave];
-    float sw[kWideTilesPerWave];
-    int se = 0;
-    if (NP > 0) {
+    i32x8 bq[T];
 #pragma unroll
-      for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
-        bq[tt] = lds_operand(lds + tile_of(tt) * kOperand, slots);
-        sw[tt] = lds_sw[sw_row(tt) * KB + kb];
-      }
-      // byte j: the E8M0 scale of this lane's route in pair wr + 2 j
-      se = *reinterpret_cast<const int*>(lds_se + kb * kGemmWideRows + (wr * 16 + (lane & 15)) * 4);
-    }
-    // every wavefront holds its B operands: the B buffer takes the next stage
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int q = 0; q < T; ++q) bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
+    const float w_lo = lds_sw[sw_lo * KB + kb], w_hi = lds_sw[sw_hi * KB + kb];
+    // bytes j: the E8M0 scales of this lane's route in pairs j (lo word) and 4 + j (hi word)
+    const uint2 se2 = *reinterpret_cast<const uint2*>(lds_se + kb * kGemmWideRows + (lane & 15) * 8);
+    // the wavefront's own tiles are in registers: its bytes of the B stage
+    // take the next stage (no other wavefront reads them)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (kb + 1 < KB) issue_b(kb + 1);
-    if (NP > 0) {
-      const uint8_t* st = lds + kWideBBytes + slot * kWideABytes;
-      f32x4 c[kWideTilesPerWave];
-      auto fold = [&](int j, int tt) {
+    const uint8_t* st = lds + kWideBBytes + slot * kWideABytes;
+    f32x4 c[T];
+    auto fold = [&](int j, int q) {
+      const float sw = q < 2 ? w_lo : w_hi;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[j][tt][i] = fmaf(c[tt][i], sw[tt], acc[j][tt][i]);
-      };
+      for (int i = 0; i < 4; ++i) acc[j][q][i] = fmaf(c[q][i], sw, acc[j][q][i]);
+    };
 #pragma unroll
-      for (int j = 0; j < NP; ++j) {
-        const int pp = wr + 2 * j;
-        const i32x8 ahi = lds_operand(st + (2 * pp) * kOperand, slots);
-        const i32x8 alo = lds_operand(st + (2 * pp + 1) * kOperand, slots);
+    for (int j = 0; j < NP; ++j) {
+      const int se = static_cast<int>(j < 4 ? se2.x : se2.y);
+      const i32x8 ahi = lds_operand(st + (2 * j) * kOperand, slots);
+      const i32x8 alo = lds_operand(st + (2 * j + 1) * kOperand, slots);
 #pragma unroll
-        for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
-          if (j > 0) fold(j - 1, tt);
-          i32x8 b = bq[tt], bc;
-          weight_operand<FIX>(b, bc);
-          c[tt] = pair_pass_byte<FIX, 127>(j, ahi, b, bc, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
-        }
-#pragma unroll
-        for (int tt = 0; tt < kWideTilesPerWave; ++tt) {
-          i32x8 b = bq[tt], bc;
-          weight_operand<FIX>(b, bc);
-          c[tt] = pair_pass_byte<FIX, 123>(j, alo, b, bc, c[tt], se);
-        }
+      for (int q = 0; q < T; ++q) {
+        if (j > 0) fold(j - 1, q);
+        i32x8 b = bq[q], bc;
+        weight_operand<FIX>(b, bc);
+        c[q] = pair_pass_byte<FIX, 127>(j & 3, ahi, b, bc, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
       }
 #pragma unroll
-      for (int tt = 0; tt < kWideTilesPerWave; ++tt) fold(NP - 1, tt);
+      for (int q = 0; q < T; ++q) {
+        i32x8 b = bq[q], bc;
+        weight_operand<FIX>(b, bc);
+        c[q] = pair_pass_byte<FIX, 123>(j & 3, alo, b, bc, c[q], se);
+      }
     }
+#pragma unroll
+    for (int q = 0; q < T; ++q) fold(NP - 1, q);
     slot ^= 1;
   }
 
-  // epilogue: lane holds columns 16 tile + l % 16 of routes 16 p + 4 kq + i
+  // epilogue: lane holds columns 16 tile + l % 16 of routes 16 j + 4 kq + i
   if (MODE == GEMM_PLAIN) {
-    plain_epilogue<NP, kWideTilesPerWave>(a, src, start, len, wr, 2, ntile * kWidePlainRows + 16 * kWideTilesPerWave * wc, acc, lane);
+    plain_epilogue<NP, T>(a, src, start, len, 0, 1, ntile * kWidePlainRows + 64 * wave, acc, lane);
   } else {
-    swiglu_epilogue<NP, kWideTilesPerWave / 2>(a, src, start, len, wr, 2, ntile * kWideGateRows + 48 * wc, acc, lane);
+    swiglu_epilogue<NP, T / 2>(a, src, start, len, 0, 1, ntile * kWideGateRows + 32 * wave, acc, lane);
   }
 }
 
@@ -1175,7 +1166,7 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   const int64_t K = a.K;
   const int64_t KB = K / kBlock;
   const int pairs = (len + 15) >> 4;
-  uint8_t* lds_se = lds + kWideBBytes + 2 * kWideABytes;                        // [KB][128]
+  uint8_t* lds_se = lds + kWideBBytes + 2 * kWideABytes;                    // [KB][128]
   float* lds_sw = reinterpret_cast<float*>(lds_se + kGemmWideRows * KB);    // [4][KB]
   auto token_of = [&](int r) -> int64_t {
     const int64_t route = start + (r < len ? r : len - 1);
@@ -1183,14 +1174,19 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   };
   // direct-load sources: load h of a weight tile fills its rows 8 h .. 8 h
   // + 7, lane l reading row r = 8 h + l / 8 at piece (l % 8) ^ (l / 8) ^ h,
-  // i.e. the h = 0 offset with bit 0 of the piece flipped for h = 1; the
-  // wavefront's tiles 3 w .. 3 w + 2 lie in one matrix
+  // i.e. the h = 0 offset with bit 0 of the piece flipped for h = 1
   WideSources ls;
   {
-    const bool up = MODE == GEMM_SWIGLU && wave >= 4;
-    ls.wmat = (up ? src.weight_up : src.weight) + static_cast<int64_t>(expert) * a.w_expert_stride;
-    const int t0 = MODE == GEMM_PLAIN ? 3 * wave : 3 * (wave & 3);
-    ls.row0 = static_cast<int32_t>(ntile * (MODE == GEMM_PLAIN ? kWidePlainRows : kWideGateRows)) + 16 * t0 + (lane >> 3);
+    const uint8_t* e0 = src.weight + static_cast<int64_t>(expert) * a.w_expert_stride;
+    ls.wlo = e0;
+    ls.whi = MODE == GEMM_SWIGLU ? src.weight_up + static_cast<int64_t>(expert) * a.w_expert_stride : e0;
+    if (MODE == GEMM_PLAIN) {
+      ls.rlo = static_cast<int32_t>(ntile * kWidePlainRows) + 64 * wave + (lane >> 3);
+      ls.rhi = ls.rlo + 32;
+    } else {
+      ls.rlo = static_cast<int32_t>(ntile * kWideGateRows) + 32 * wave + (lane >> 3);
+      ls.rhi = ls.rlo;
+    }
     ls.rows = static_cast<int32_t>(a.N);
     ls.K = K;
     ls.wg = src.wg;
@@ -1204,14 +1200,15 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   // stage 0's direct loads fly while the block scales are gathered
   {
-    const uint32_t sb = lds_addr + 3 * wave * kOperand;
+    const uint32_t b_own = static_cast<uint32_t>(wave) * kWideTilesPerWave * kOperand;
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
+    for (int q = 0; q < kWideTilesPerWave; ++q)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        int32_t row = ls.row0 + 16 * q + 8 * h;
+        int32_t row = (q < 2 ? ls.rlo : ls.rhi) + 16 * (q & 1) + 8 * h;
         row = row < ls.rows ? row : ls.rows - 1;
-        lds_direct16(ls.wmat + group_row_base(row, K, ls.wg) + (ls.piece ^ (16 * h)), sb + q * kOperand + 1024 * h);
+        const uint8_t* m = q < 2 ? ls.wlo : ls.whi;
+        lds_direct16(m + group_row_base(row, K, ls.wg) + (ls.piece ^ (16 * h)), lds_addr + b_own + q * kOperand + 1024 * h);
       }
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + 2 * wave * kOperand;
@@ -1224,10 +1221,10 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
     }
   }
   load_activation_scales<kGemmWideRows, 512, true>(src, start, len, KB, lds_se);
-  // weight scale rows: PLAIN the item's three 128-row blocks; SWIGLU the
-  // (at most two) blocks its 192 gate rows span, then the same up blocks
+  // weight scale rows: PLAIN the item's four 128-row blocks; SWIGLU the two
+  // blocks its 256 gate rows span, then the same up blocks
   const int64_t srows = (a.N + 127) / 128;
-  const int64_t b0 = MODE == GEMM_PLAIN ? 3 * ntile : (ntile * kWideGateRows) >> 7;
+  const int64_t b0 = MODE == GEMM_PLAIN ? 4 * ntile : 2 * ntile;
   for (int64_t i = threadIdx.x; i < 4 * KB; i += 512) {
     const int64_t r = i / KB, k = i - r * KB;
     int64_t blk = b0 + (MODE == GEMM_PLAIN ? r : (r & 1));
@@ -1237,17 +1234,20 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   }
   __syncthreads();
 
-  int np = (pairs - (wave >> 2) + 1) >> 1;  // pairs this wavefront multiplies: wr, wr + 2, ...
-  np = np < 0 ? 0 : (np > 4 ? 4 : np);
 #define GLM53_WIDE(n) \
   wide_gemm_loop<MODE, FIX, n>(a, src, ntile, start, len, KB, ls, loads_pair, lds, lds_addr, lds_se, lds_sw, wave, lane)
   // rows past the descriptor's routes (in its last pair) hold stale
   // activations: their products are never stored
-  if (np == 0) GLM53_WIDE(0);
-  else if (np > 3) GLM53_WIDE(4);
-  else if (np == 3) GLM53_WIDE(3);
-  else if (np == 2) GLM53_WIDE(2);
-  else GLM53_WIDE(1);
+  switch (pairs) {
+    case 1: GLM53_WIDE(1); break;
+    case 2: GLM53_WIDE(2); break;
+    case 3: GLM53_WIDE(3); break;
+    case 4: GLM53_WIDE(4); break;
+    case 5: GLM53_WIDE(5); break;
+    case 6: GLM53_WIDE(6); break;
+    case 7: GLM53_WIDE(7); break;
+    default: GLM53_WIDE(8); break;
+  }
 #undef GLM53_WIDE
 }
 
