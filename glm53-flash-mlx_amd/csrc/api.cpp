@@ -1606,7 +1606,9 @@ static int prefill_run(glm53_prefill_plan* p, const glm53_bank* bank, const glm5
   // when experts average at least 48 routes, 64-route ones from 32 (fewer
   // re-reads of each weight tile), 32-route ones (a deeper load ring per
   // workgroup) below
-  const int tile = R >= 48 * E ? kGemmWideRows : R >= 32 * E ? kGemmTileRows : kGemmMinTileRows;
+  const int64_t act_rows = R > T ? R : T;
+  const bool wide_fits = wide_offsets_fit(I, H, act_rows) && wide_offsets_fit(H, I, act_rows);
+  const int tile = R >= 48 * E && wide_fits ? kGemmWideRows : R >= 32 * E ? kGemmTileRows : kGemmMinTileRows;
   const int64_t cap = cdiv(R, tile) + E;
   if ((rc = route_plan_impl(ids, sc, R, k, E, tile, p->sorted_route, p->inverse, p->sorted_expert,
                             p->sorted_token, p->sorted_score, p->route_offsets, p->tile_offsets, p->tile_expert,

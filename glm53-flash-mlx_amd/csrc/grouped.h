@@ -14,6 +14,16 @@ constexpr int kGemmWideRows = 128;     // its wide form (128-route descriptors x
 constexpr int kMaxReduceTopK = 16;
 enum { GEMM_PLAIN = 0, GEMM_SWIGLU = 1 };
 
+// The wide shape's direct loads address a weight matrix of `rows` rows and
+// an activation plane of `act_rows` rows (K bytes each) through unsigned
+// 32-bit offsets from a wave-uniform base, and split each weight row index
+// into a wave-uniform multiple of 8 and the lane's 0 .. 7; it is taken only
+// where both stay under 2 GiB and rows is a multiple of 8.
+inline bool wide_offsets_fit(int64_t rows, int64_t K, int64_t act_rows) {
+  const int64_t limit = int64_t{1} << 31;
+  return rows % 8 == 0 && rows >= 8 && (rows + 128) * K < limit && act_rows * K < limit;
+}
+
 struct RoutePlanArgs {
   const int32_t* expert_ids;  // [routes] flat (token-major, slot-minor)
   const float* scores;        // [routes] or null

@@ -421,6 +421,14 @@ __device__ __forceinline__ void lds_direct16(const uint8_t* g, uint32_t lds_base
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
 }
 
+// The same load addressed as base + off: base wave-uniform (held in SGPRs),
+// off a per-lane unsigned 32-bit offset, so a loop-invariant source costs
+// one VGPR instead of a 64-bit address pair.
+__device__ __forceinline__ void lds_direct16_at(const uint8_t* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_base)
+               : "memory", "m0");
+}
+
 // Waits until at most N of this wavefront's vector-memory loads are in
 // flight and its LDS reads have returned, then joins the workgroup barrier.
 template <int N>
@@ -1040,22 +1048,34 @@ size_t gemm_wide_lds_bytes(int64_t K) {
          (kGemmWideRows + 4 * sizeof(float)) * static_cast<size_t>(K / kBlock);
 }
 
-// Direct-load sources of a wavefront: its tiles q = 0, 1 come from matrix
-// wlo starting at row rlo (+ 16 q), tiles 2, 3 from whi at row rhi (+ 16 (q -
-// 2)), each + 8 h + lane / 8 for load h and clamped to the last row; its
-// pair's hi / lo rows from token rows tok[h].
+// Direct-load sources of a wavefront.  Load h of its tile q covers rows U +
+// 0 .. 7 with U = (q < 2 ? rlo : rhi) + 16 (q % 2) + 8 h (a multiple of 8,
+// clamped to rows - 8, rows being a multiple of 8); lane l reads row U + l /
+// 8 at its piece, and since U is a multiple of 8, group_row_base(U + l / 8)
+// = group_row_base(U) + group_row_base(l / 8).  So the wave-uniform part
+// wrow[2 q + h] = group_row_base(U) (+ (kb << (7 + wg)) for stage kb) goes
+// into the SGPR base and the lane adds woff (h = 0; h = 1 flips bit 4 of the
+// piece: woff ^ 16).  Load h of its pair's hi / lo rows reads a_hi / a_lo at
+// aoff[h] (token row tok[h] at the lane's piece) + 128 kb.
 struct WideSources {
   const uint8_t* wlo;      // PLAIN: the expert's matrix; SWIGLU: its gate rows
   const uint8_t* whi;      // PLAIN: the same matrix; SWIGLU: its up rows
   const uint8_t* a_hi;
   const uint8_t* a_lo;
-  int64_t K;
   int32_t wg;              // row groups of the matrices (common.h)
-  int32_t rows;            // rows of the matrix (loads past it re-read the last row)
-  int32_t rlo, rhi;        // first rows of tiles 0 and 2, + lane / 8
-  int32_t piece;           // lane's piece offset in its row for h = 0 (h = 1: piece ^ 16)
-  int32_t tok[2];          // token rows of the pair's rows 8 h + lane / 8
+  int64_t wrow[2 * kWideTilesPerWave];
+  uint32_t woff;
+  uint32_t aoff[2];
 };
+
+// A wave-uniform pointer as the compiler can prove it uniform (so that it
+// lives in SGPRs).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 template <int MODE, bool FIX, int NP>
 __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const ItemSource src, int64_t ntile,
@@ -1066,25 +1086,22 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
   const OperandSlots slots = operand_slots(lane);
   const uint32_t b_own = static_cast<uint32_t>(wave) * T * kOperand;  // this wavefront's tiles in the B stage
   auto issue_b = [&](int64_t kb) {
+    const uint8_t* mlo = ls.wlo + (kb << (7 + ls.wg));
+    const uint8_t* mhi = ls.whi + (kb << (7 + ls.wg));
 #pragma unroll
     for (int q = 0; q < T; ++q)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int32_t row = (q < 2 ? ls.rlo : ls.rhi) + 16 * (q & 1) + 8 * h;
-        row = row < ls.rows ? row : ls.rows - 1;
-        const uint8_t* m = q < 2 ? ls.wlo : ls.whi;
-        lds_direct16(m + group_row_base(row, ls.K, ls.wg) + (kb << (7 + ls.wg)) + (ls.piece ^ (16 * h)),
-                     lds_addr + b_own + q * kOperand + 1024 * h);
-      }
+      for (int h = 0; h < 2; ++h)
+        lds_direct16_at((q < 2 ? mlo : mhi) + ls.wrow[2 * q + h], ls.woff ^ (16 * h),
+                        lds_addr + b_own + q * kOperand + 1024 * h);
   };
   auto issue_a = [&](int64_t kb, int slot) {
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + slot * kWideABytes + 2 * wave * kOperand;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int64_t off = static_cast<int64_t>(ls.tok[h]) * ls.K + kb * kBlock + (ls.piece ^ (16 * h));
-        lds_direct16(ls.a_hi + off, sa + 1024 * h);
-        lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
+        lds_direct16_at(ls.a_hi + kb * kBlock, ls.aoff[h], sa + 1024 * h);
+        lds_direct16_at(ls.a_lo + kb * kBlock, ls.aoff[h], sa + kOperand + 1024 * h);
       }
     }
   };
@@ -1174,27 +1191,34 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
   };
   // direct-load sources: load h of a weight tile fills its rows 8 h .. 8 h
   // + 7, lane l reading row r = 8 h + l / 8 at piece (l % 8) ^ (l / 8) ^ h,
-  // i.e. the h = 0 offset with bit 0 of the piece flipped for h = 1
+  // i.e. the h = 0 offset with bit 0 of the piece flipped for h = 1.  The
+  // offsets fit 32 bits: the launcher takes this shape only for matrices
+  // and activation planes under 2 GiB (and rows a multiple of 8).
   WideSources ls;
   {
     const uint8_t* e0 = src.weight + static_cast<int64_t>(expert) * a.w_expert_stride;
-    ls.wlo = e0;
-    ls.whi = MODE == GEMM_SWIGLU ? src.weight_up + static_cast<int64_t>(expert) * a.w_expert_stride : e0;
-    if (MODE == GEMM_PLAIN) {
-      ls.rlo = static_cast<int32_t>(ntile * kWidePlainRows) + 64 * wave + (lane >> 3);
-      ls.rhi = ls.rlo + 32;
-    } else {
-      ls.rlo = static_cast<int32_t>(ntile * kWideGateRows) + 32 * wave + (lane >> 3);
-      ls.rhi = ls.rlo;
-    }
-    ls.rows = static_cast<int32_t>(a.N);
-    ls.K = K;
+    ls.wlo = uniform_ptr(e0);
+    ls.whi = MODE == GEMM_SWIGLU ? uniform_ptr(src.weight_up + static_cast<int64_t>(expert) * a.w_expert_stride)
+                                 : ls.wlo;
+    ls.a_hi = uniform_ptr(src.a_hi);
+    ls.a_lo = uniform_ptr(src.a_lo);
     ls.wg = src.wg;
-    ls.piece = load_piece_offset(lane, 0);
-    ls.a_hi = src.a_hi;
-    ls.a_lo = src.a_lo;
+    const int64_t rows = a.N;
+    const int32_t piece = load_piece_offset(lane, 0);
+    const int64_t rlo = MODE == GEMM_PLAIN ? ntile * kWidePlainRows + 64 * wave : ntile * kWideGateRows + 32 * wave;
+    const int64_t rhi = MODE == GEMM_PLAIN ? rlo + 32 : rlo;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) ls.tok[h] = static_cast<int32_t>(token_of(16 * wave + 8 * h + (lane >> 3)));
+    for (int q = 0; q < kWideTilesPerWave; ++q)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int64_t u = (q < 2 ? rlo : rhi) + 16 * (q & 1) + 8 * h;
+        u = u < rows - 8 ? u : rows - 8;
+        ls.wrow[2 * q + h] = group_row_base(u, K, ls.wg);
+      }
+    ls.woff = static_cast<uint32_t>(group_row_base(lane >> 3, K, ls.wg) + piece);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      ls.aoff[h] = static_cast<uint32_t>(token_of(16 * wave + 8 * h + (lane >> 3)) * K + (piece ^ (16 * h)));
   }
   const bool loads_pair = wave < pairs;  // wave-uniform
   const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -1204,19 +1228,15 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
 #pragma unroll
     for (int q = 0; q < kWideTilesPerWave; ++q)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int32_t row = (q < 2 ? ls.rlo : ls.rhi) + 16 * (q & 1) + 8 * h;
-        row = row < ls.rows ? row : ls.rows - 1;
-        const uint8_t* m = q < 2 ? ls.wlo : ls.whi;
-        lds_direct16(m + group_row_base(row, K, ls.wg) + (ls.piece ^ (16 * h)), lds_addr + b_own + q * kOperand + 1024 * h);
-      }
+      for (int h = 0; h < 2; ++h)
+        lds_direct16_at((q < 2 ? ls.wlo : ls.whi) + ls.wrow[2 * q + h], ls.woff ^ (16 * h),
+                        lds_addr + b_own + q * kOperand + 1024 * h);
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + 2 * wave * kOperand;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int64_t off = static_cast<int64_t>(ls.tok[h]) * K + (ls.piece ^ (16 * h));
-        lds_direct16(ls.a_hi + off, sa + 1024 * h);
-        lds_direct16(ls.a_lo + off, sa + kOperand + 1024 * h);
+        lds_direct16_at(ls.a_hi, ls.aoff[h], sa + 1024 * h);
+        lds_direct16_at(ls.a_lo, ls.aoff[h], sa + kOperand + 1024 * h);
       }
     }
   }
@@ -1466,6 +1486,8 @@ hipError_t launch_grouped_gemm(const GroupedGemmArgs& a, int mode, int64_t descr
     const unsigned grid = static_cast<unsigned>(8 * ((items + 7) / 8));
     const size_t lds = gemm_wide_lds_bytes(a.K);
     if (a.K % kBlock != 0 || a.K <= 0 || lds > 160 * 1024) return hipErrorInvalidValue;
+    // its direct loads take 32-bit offsets into each matrix and activation plane
+    if (!wide_offsets_fit(a.N, a.K, a.routes > a.x_routes ? a.routes : a.x_routes)) return hipErrorInvalidValue;
     if (mode == GEMM_PLAIN) hipLaunchKernelGGL(grouped_gemm_wide_kernel<GEMM_PLAIN>, dim3(grid), dim3(512), lds, st, g);
     else hipLaunchKernelGGL(grouped_gemm_wide_kernel<GEMM_SWIGLU>, dim3(grid), dim3(512), lds, st, g);
     return hipGetLastError();
