@@ -1480,7 +1480,9 @@ int glm53_prefill_plan_create(int64_t hidden, int64_t intermediate, int64_t shar
   size_t o_pws = take(glm53_route_plan_workspace_bytes(R, experts));
   size_t o_sr = take(4 * R), o_inv = take(4 * R), o_se = take(4 * R), o_st = take(4 * R), o_ss = take(4 * R);
   size_t o_ro = take(4 * (experts + 1)), o_to = take(4 * (experts + 1)), o_status = take(8);
-  size_t o_te = take(4 * p->capacity_max), o_ts = take(4 * p->capacity_max), o_tl = take(4 * p->capacity_max);
+  // the descriptor arrays back to back: int32 [3, capacity_max]
+  const size_t o_te = take(4 * 3 * p->capacity_max), o_ts = o_te + 4 * p->capacity_max,
+               o_tl = o_ts + 4 * p->capacity_max;
   size_t o_h = take(2 * RH * intermediate), o_down = take(2 * R * hidden), o_hs = take(2 * T * Ism);
   size_t o_so = take(2 * T * hidden), o_flags = take(32);
   p->arena_bytes = off;

@@ -325,14 +325,15 @@ class WeightedGate:
 
 @pytest.mark.parametrize("inter,codes_480", [(384, False), (384, True), (256, True)])
 def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, inter, codes_480):
-    """The wide GEMM shape (128-route descriptors x 384 weight rows: 192 gate
-    rows with the matching 192 up rows for gate/up, 384 output columns for
+    """The wide GEMM shape (128-route descriptors x 512 weight rows: 256 gate
+    rows with the matching 256 up rows for gate/up, 512 output columns for
     down; taken when experts average at least 48 routes): 300 tokens x top-4
     over 8 experts with skewed counts (descriptors full, part-filled and
-    single groups), hidden 640 (the down GEMM's second item ends 128 rows
-    past the matrix, its last scale block clamped), intermediate 384 (two
-    whole gate/up items) or 256 (the second gate/up item half past the
-    matrix: a partial last gate tile), the shared expert as dense
+    single groups), hidden 640 (the down GEMM's second item ends 384 rows
+    past the matrix: whole wavefronts past it re-read its last 8 rows, its
+    last scale block clamped), intermediate 384 (the second gate/up item
+    half past the matrix: a partial last gate tile) or 256 (one whole
+    gate/up item), the shared expert as dense
     descriptors in the same launches; with 0x7F / 0xFF codes in the routed
     gate/up and down weights, the fixup path of both modes (also on the
     partial gate tile at intermediate 256).  Against the oracle's Direct
