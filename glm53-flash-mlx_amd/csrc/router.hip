@@ -209,8 +209,11 @@ RouterGemmShape router_gemm_shape(int64_t tokens, int64_t hidden, int64_t expert
   s.expert_groups = (experts + kTileExperts - 1) / kTileExperts;
   const int64_t groups = s.token_groups * s.expert_groups;
   const int64_t blocks = hidden / 128;
-  // Two work items per CU where K allows, at most kMaxRouterSplits partial planes.
-  int64_t want = (512 + groups - 1) / groups;
+  // At most 512 work items (two per CU, one round) where K allows: a 513th
+  // item would cost a whole second round (e.g. 2,048 tokens x 288 experts,
+  // 48 groups over K = 4,096: 11 planes were 528 items, 8 planes are 384),
+  // and at most kMaxRouterSplits partial planes.
+  int64_t want = 512 / groups;
   if (want > kMaxRouterSplits) want = kMaxRouterSplits;
   if (want > blocks) want = blocks;
   if (want < 1) want = 1;
