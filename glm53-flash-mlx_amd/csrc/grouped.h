@@ -10,7 +10,7 @@ constexpr int kPlanMaxExperts = 1024;
 constexpr int kGroupedTileRows = 32;   // routes per descriptor of the reference (grouped_fp8.py:20)
 constexpr int kGemmTileRows = 64;      // routes per descriptor of the MFMA grouped GEMM (many routes per expert)
 constexpr int kGemmMinTileRows = 32;   // its narrow form (one group per wavefront, deeper ring)
-constexpr int kGemmWideRows = 128;     // its wide form (128-route descriptors x 384 weight rows per item)
+constexpr int kGemmWideRows = 128;     // its wide form (128-route descriptors x 512 weight rows per item)
 constexpr int kMaxReduceTopK = 16;
 enum { GEMM_PLAIN = 0, GEMM_SWIGLU = 1 };
 
