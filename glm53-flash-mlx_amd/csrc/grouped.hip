@@ -1141,11 +1141,16 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][q][i] = fmaf(c[q][i], sw, acc[j][q][i]);
     };
+    // A operands half a pair ahead at no register cost: pair j's lo rows
+    // are read as its hi pass starts, pair j + 1's hi rows as its lo pass
+    // starts (each into the registers the operand before it just freed)
+    i32x8 ahi_next = lds_operand(st, slots);
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       const int se = static_cast<int>(j < 4 ? se2.x : se2.y);
-      const i32x8 ahi = lds_operand(st + (2 * j) * kOperand, slots);
+      const i32x8 ahi = ahi_next;
       const i32x8 alo = lds_operand(st + (2 * j + 1) * kOperand, slots);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < T; ++q) {
         if (j > 0) fold(j - 1, q);
@@ -1153,12 +1158,16 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         weight_operand<FIX>(b, bc);
         c[q] = pair_pass_byte<FIX, 127>(j & 3, ahi, b, bc, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 1 < NP) ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < T; ++q) {
         i32x8 b = bq[q], bc;
         weight_operand<FIX>(b, bc);
         c[q] = pair_pass_byte<FIX, 123>(j & 3, alo, b, bc, c[q], se);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int q = 0; q < T; ++q) fold(NP - 1, q);
