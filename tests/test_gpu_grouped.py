@@ -18,7 +18,7 @@ def test_route_plan_is_stable_sort(O, dev):
 
     grouped = submodule("grouped_fp8")
     rng = np.random.default_rng(4)
-    for tokens, experts in ((256, 288), (2048, 288), (3, 8), (1000, 64)):
+    for tokens, experts in ((256, 288), (2048, 288), (3, 8), (1000, 64), (2100, 288)):
         ids = np.stack([rng.choice(experts, size=8, replace=False) for _ in range(tokens)]).astype(np.int32)
         scores = rng.uniform(size=ids.shape).astype(np.float32)
         plan = grouped._route_plan(torch.from_numpy(ids).to(dev), torch.from_numpy(scores).to(dev), 8, experts)
@@ -52,6 +52,43 @@ def test_tile_plan_kat_sparse_edge_buckets(M, dev):
     counts = np.bincount(sorted_experts.cpu().numpy(), minlength=288)
     assert int(np.sum(counts == 0)) == 285
     np.testing.assert_array_equal(route_offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(counts)]))
+
+
+@pytest.mark.parametrize("tokens,experts,skew", [(2048, 288, False), (2049, 288, False), (2048, 16, True),
+                                                 (2300, 16, True), (130, 1024, False)])
+def test_route_plan_with_invalid_ids(dev, tokens, experts, skew):
+    """The route plan (count / scan / scatter) on ids with ~1% out of range
+    (negative or >= experts), uniform or skewed (long runs of one expert in
+    every 256-route block), up to 1,024 experts: valid routes in stable
+    expert order (numpy's stable argsort), invalid ones with inverse -1 and
+    counted in status[0]."""
+    import torch
+
+    grouped = submodule("grouped_fp8")
+    rng = np.random.default_rng(tokens + experts)
+    if skew:
+        p = 1.0 / np.arange(1, experts + 1) ** 2
+        ids = rng.choice(experts, size=(tokens, 8), p=p / p.sum()).astype(np.int32)
+    else:
+        ids = rng.integers(0, experts, size=(tokens, 8)).astype(np.int32)
+    bad = rng.uniform(size=ids.shape) < 0.01
+    ids[bad] = np.where(rng.uniform(size=bad.sum()) < 0.5, -1, experts + 3)
+    scores = rng.uniform(size=ids.shape).astype(np.float32)
+    plan = grouped._route_plan(torch.from_numpy(ids).to(dev), torch.from_numpy(scores).to(dev), 8, experts)
+    flat = ids.reshape(-1)
+    valid = (flat >= 0) & (flat < experts)
+    order = np.nonzero(valid)[0][np.argsort(flat[valid], kind="stable")]
+    n = order.size
+    np.testing.assert_array_equal(plan["order"].cpu().numpy()[:n], order)
+    inverse = np.full(flat.size, -1, np.int64)
+    inverse[order] = np.arange(n)
+    np.testing.assert_array_equal(plan["inverse"].cpu().numpy(), inverse)
+    np.testing.assert_array_equal(plan["sorted_experts"].cpu().numpy()[:n], flat[order])
+    np.testing.assert_array_equal(plan["token_ids"].cpu().numpy()[:n], order // 8)
+    np.testing.assert_array_equal(plan["sorted_scores"].cpu().numpy()[:n], scores.reshape(-1)[order])
+    counts = np.bincount(flat[valid], minlength=experts)
+    np.testing.assert_array_equal(plan["route_offsets"].cpu().numpy(), np.concatenate([[0], np.cumsum(counts)]))
+    assert int(plan["status"][0]) == int((~valid).sum())
 
 
 def test_route_plan_flags_invalid_ids(dev):
