@@ -1119,21 +1119,27 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
-  // stage 0 (B and A) was issued by wide_gemm_body, before the block scales
+  // Stage 0 (B and A) was issued by wide_gemm_body, before the block
+  // scales.  The wavefront's B tiles of a stage are read into registers
+  // during the previous stage's last pair, each as soon as that pair's
+  // last MFMA on the tile has issued (its own direct loads waited for; no
+  // barrier: no other wavefront reads them), so a stage starts on its
+  // MFMAs right after the barrier and its B bytes take the next stage at
+  // once.
+  i32x8 bq[T];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int q = 0; q < T; ++q) bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
     stage_barrier<0>();  // stage kb landed; every wavefront is done with stage kb - 1
-    if (kb + 1 < KB) issue_a(kb + 1, slot ^ 1);
-    i32x8 bq[T];
-#pragma unroll
-    for (int q = 0; q < T; ++q) bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
+    if (kb + 1 < KB) {
+      issue_a(kb + 1, slot ^ 1);
+      issue_b(kb + 1);
+    }
     const float w_lo = lds_sw[sw_lo * KB + kb], w_hi = lds_sw[sw_hi * KB + kb];
     // bytes j: the E8M0 scales of this lane's route in pairs j (lo word) and 4 + j (hi word)
     const uint2 se2 = *reinterpret_cast<const uint2*>(lds_se + kb * kGemmWideRows + (lane & 15) * 8);
-    // the wavefront's own tiles are in registers: its bytes of the B stage
-    // take the next stage (no other wavefront reads them)
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (kb + 1 < KB) issue_b(kb + 1);
     const uint8_t* st = lds + kWideBBytes + slot * kWideABytes;
     f32x4 c[T];
     auto fold = [&](int j, int q) {
@@ -1166,6 +1172,12 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         i32x8 b = bq[q], bc;
         weight_operand<FIX>(b, bc);
         c[q] = pair_pass_byte<FIX, 123>(j & 3, alo, b, bc, c[q], se);
+        if (j == NP - 1) {
+          // unconditional (the last stage rereads its own tiles, unused),
+          // so that no tile stays live beside its successor
+          if (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next stage's B (and A) landed
+          bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
