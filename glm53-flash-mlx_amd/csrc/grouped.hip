@@ -1164,6 +1164,18 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         weight_operand<FIX>(b, bc);
         c[q] = pair_pass_byte<FIX, 127>(j & 3, ahi, b, bc, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, se);
       }
+      if constexpr (!FIX) {
+        // each tile's fold right before its first MFMA (the fold of tile q
+        // waits only for tile q's last MFMA of the previous pair, not for
+        // tile T - 1's)
+        if (j > 0) {
+#pragma unroll
+          for (int q = 0; q < T; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU: fold(j - 1, q)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA: tile q's hi pass
+          }
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NP) ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
       __builtin_amdgcn_sched_barrier(0);
