@@ -429,6 +429,18 @@ __global__ __launch_bounds__(512) void step_down_kernel(StepArgs a) {
   const int slot = threadIdx.x >> 6;
   const int64_t I = a.intermediate;
   const int64_t h0 = static_cast<int64_t>(blockIdx.x) * 16;
+  // The reduction's operands of output row h0 + r (threads r < 16): the
+  // slot weights and the shared and residual rows, loaded before the
+  // weight rows so that their round trips (cold: written by the earlier
+  // launches) overlap the stream instead of following the barrier.
+  float pre_score[kMaxTopK];
+  float pre_shared = 0.0f, pre_residual = 0.0f;
+  if (threadIdx.x < 16) {
+#pragma unroll
+    for (int sl = 0; sl < kMaxTopK; ++sl) pre_score[sl] = sl < a.top_k ? a.scores[sl] : 0.0f;
+    if (a.shared_down_weight != nullptr) pre_shared = bf16_to_f32(a.shared_out[h0 + threadIdx.x]);
+    if (a.residual != nullptr) pre_residual = bf16_to_f32(a.residual[h0 + threadIdx.x]);
+  }
   if (slot < a.top_k) {
     const int32_t e = a.ids[slot];
     if (e < 0 || e >= a.experts) {
@@ -465,10 +477,12 @@ __global__ __launch_bounds__(512) void step_down_kernel(StepArgs a) {
   if (r < 16) {
     const int64_t h = h0 + r;
     float total = 0.0f;
-    for (int sl = 0; sl < a.top_k; ++sl) total = __fadd_rn(total, __fmul_rn(parked[sl][r], a.scores[sl]));
+#pragma unroll
+    for (int sl = 0; sl < kMaxTopK; ++sl)
+      if (sl < a.top_k) total = __fadd_rn(total, __fmul_rn(parked[sl][r], pre_score[sl]));
     float result = bf16_round(total);
-    if (a.shared_down_weight != nullptr) result = __fadd_rn(result, bf16_to_f32(a.shared_out[h]));
-    if (a.residual != nullptr) result = __fadd_rn(bf16_to_f32(a.residual[h]), bf16_round(result));
+    if (a.shared_down_weight != nullptr) result = __fadd_rn(result, pre_shared);
+    if (a.residual != nullptr) result = __fadd_rn(pre_residual, bf16_round(result));
     a.out[h] = f32_to_bf16(result);
   }
 }
