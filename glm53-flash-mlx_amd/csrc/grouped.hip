@@ -1021,14 +1021,18 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GroupedGemmArgs a) {
 // SWIGLU: gate rows 32 w .. 32 w + 31 and the matching up rows), so all
 // wavefronts carry the same work whatever the descriptor's route count.
 // The wavefront loads its four tiles itself (direct loads into its own
-// 8 KB of a single-buffered 64 KB B stage) and reads them into registers at
-// the start of each stage; once those reads have returned it issues the
-// next stage's tiles into the same bytes, so the weight stream needs no
-// workgroup barrier and runs a whole stage ahead.  The activations come
+// 8 KB of a single-buffered 64 KB B stage) and reads them into registers
+// during the previous stage's last pair; once those reads have returned it
+// issues the next stage's tiles into the same bytes, so the weight stream
+// needs no workgroup barrier and runs a stage ahead.  The activations come
 // through a 2-stage ring of 32 KB stages (wavefront w loads pair w's hi and
-// lo tiles); one barrier per stage makes a stage's activation tiles
-// visible and frees the other slot.  Per stage 8 KB of B and 32 KB of A
-// operand reads for 64 MFMAs per wavefront.  The arithmetic per output
+// lo tiles).  One barrier per stage, after each wavefront's last
+// activation read of the stage and before its last pair's MFMAs, makes the
+// next stage's activation tiles visible and frees this stage's slot; the
+// wavefronts leave it with that pair's MFMAs in hand, so the MFMA pipes
+// have work while the next stage starts (3-4% faster than a barrier at the
+// stage start).  Per stage 8 KB of B and 32 KB of A operand reads for 64
+// MFMAs per wavefront.  The arithmetic per output
 // element is that of the narrower shapes, so every shape gives the same
 // bits.
 namespace {
@@ -1120,20 +1124,25 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       for (int i = 0; i < 4; ++i) acc[j][t][i] = 0.0f;
 
   // Stage 0 (B and A) was issued by wide_gemm_body, before the block
-  // scales.  The wavefront's B tiles of a stage are read into registers
-  // during the previous stage's last pair, each as soon as that pair's
-  // last MFMA on the tile has issued (its own direct loads waited for; no
-  // barrier: no other wavefront reads them), so a stage starts on its
-  // MFMAs right after the barrier and its B bytes take the next stage at
-  // once.
+  // scales, and has landed in every wavefront (the body waited for its own
+  // loads before the barrier that published the scales).  The wavefront's
+  // B tiles of a stage are read into registers during the previous stage's
+  // last pair, each as soon as that pair's last MFMA on the tile has
+  // issued (its own direct loads waited for; no barrier: no other
+  // wavefront reads them), so a stage starts on its MFMAs at once and its
+  // B bytes take the next stage.
   i32x8 bq[T];
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
   for (int q = 0; q < T; ++q) bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
+  i32x8 ahi_next = lds_operand(lds + kWideBBytes, slots);
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
-    stage_barrier<0>();  // stage kb landed; every wavefront is done with stage kb - 1
+    // the other slot's stage (kb - 1) was read out by every wavefront before
+    // the barrier in its last pair, and this wavefront's B tiles of stage kb
+    // are in registers: stage kb + 1 goes in, A first (the barrier's count
+    // leaves B's 2 T loads in flight)
     if (kb + 1 < KB) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue_a(kb + 1, slot ^ 1);
       issue_b(kb + 1);
     }
@@ -1147,15 +1156,21 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][q][i] = fmaf(c[q][i], sw, acc[j][q][i]);
     };
+    const uint8_t* st_next = lds + kWideBBytes + (slot ^ 1) * kWideABytes;
     // A operands half a pair ahead at no register cost: pair j's lo rows
-    // are read as its hi pass starts, pair j + 1's hi rows as its lo pass
-    // starts (each into the registers the operand before it just freed)
-    i32x8 ahi_next = lds_operand(st, slots);
+    // are read as its hi pass starts, pair j + 1's hi rows (after the last
+    // pair: the next stage's first) as its lo pass starts (each into the
+    // registers the operand before it just freed)
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       const int se = static_cast<int>(j < 4 ? se2.x : se2.y);
       const i32x8 ahi = ahi_next;
       const i32x8 alo = lds_operand(st + (2 * j + 1) * kOperand, slots);
+      // Every wavefront has read this stage's A and its own share of the
+      // next stage's A has landed: the next stage's A is complete, and this
+      // stage's slot is free for the stage after.  Each wavefront still
+      // holds its last pair's MFMAs, so the pipes have work at the release.
+      if (j == NP - 1) stage_barrier<2 * T>();
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < T; ++q) {
@@ -1178,6 +1193,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       }
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NP) ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
+      else ahi_next = lds_operand(st_next, slots);  // unused after the last stage
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < T; ++q) {
@@ -1187,7 +1203,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         if (j == NP - 1) {
           // unconditional (the last stage rereads its own tiles, unused),
           // so that no tile stays live beside its successor
-          if (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next stage's B (and A) landed
+          if (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next stage's B landed
           bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
         }
       }
@@ -1285,6 +1301,7 @@ __device__ __forceinline__ void wide_gemm_body(const GroupedGemmArgs& a, const I
     const float* sc = (MODE == GEMM_SWIGLU && r >= 2) ? src.scale_up : src.scale;
     lds_sw[i] = sc[static_cast<int64_t>(expert) * a.s_expert_stride + blk * a.s_cols + k];
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's stage-0 loads landed
   __syncthreads();
 
 #define GLM53_WIDE(n) \
