@@ -1099,6 +1099,12 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         lds_direct16_at((q < 2 ? mlo : mhi) + ls.wrow[2 * q + h], ls.woff ^ (16 * h),
                         lds_addr + b_own + q * kOperand + 1024 * h);
   };
+  auto issue_b_tile = [&](int64_t kb, int q) {
+    const uint8_t* m = (q < 2 ? ls.wlo : ls.whi) + (kb << (7 + ls.wg));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      lds_direct16_at(m + ls.wrow[2 * q + h], ls.woff ^ (16 * h), lds_addr + b_own + q * kOperand + 1024 * h);
+  };
   auto issue_a = [&](int64_t kb, int slot) {
     if (loads_pair) {
       const uint32_t sa = lds_addr + kWideBBytes + slot * kWideABytes + 2 * wave * kOperand;
@@ -1140,12 +1146,18 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
     // the other slot's stage (kb - 1) was read out by every wavefront before
     // the barrier in its last pair, and this wavefront's B tiles of stage kb
     // are in registers: stage kb + 1 goes in, A first (the barrier's count
-    // leaves B's 2 T loads in flight)
+    // leaves B's 2 T loads in flight).  With more than T pairs the B tiles
+    // go out one per pair instead, each after the pair's hi pass: twelve
+    // direct loads at a stage start had the wavefronts stall on the vector
+    // memory queue (gate/up -3%, down -4%).  Those issues are unconditional
+    // (a branch in the pair loop made the compiler spill), so the last stage
+    // reloads its own tiles, unused.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (kb + 1 < KB) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue_a(kb + 1, slot ^ 1);
-      issue_b(kb + 1);
+      if constexpr (NP <= T) issue_b(kb + 1);
     }
+    const int64_t kb_next = kb + 1 < KB ? kb + 1 : kb;
     const float w_lo = lds_sw[sw_lo * KB + kb], w_hi = lds_sw[sw_hi * KB + kb];
     // bytes j: the E8M0 scales of this lane's route in pairs j (lo word) and 4 + j (hi word)
     const uint2 se2 = *reinterpret_cast<const uint2*>(lds_se + kb * kGemmWideRows + (lane & 15) * 8);
@@ -1166,6 +1178,13 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       const int se = static_cast<int>(j < 4 ? se2.x : se2.y);
       const i32x8 ahi = ahi_next;
       const i32x8 alo = lds_operand(st + (2 * j + 1) * kOperand, slots);
+      // Issue priority falls as a wavefront gets ahead in its stage, so of
+      // the two on a SIMD the one behind gets the MFMA pipe and they reach
+      // the barrier closer together (gate/up -2%).
+      if (j == 0) __builtin_amdgcn_s_setprio(3);
+      else if (j == 2) __builtin_amdgcn_s_setprio(2);
+      else if (j == 4) __builtin_amdgcn_s_setprio(1);
+      else if (j == 6) __builtin_amdgcn_s_setprio(0);
       // Every wavefront has read this stage's A and its own share of the
       // next stage's A has landed: the next stage's A is complete, and this
       // stage's slot is free for the stage after.  Each wavefront still
@@ -1190,6 +1209,10 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA: tile q's hi pass
           }
         }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NP > T) {  // tiles 0 .. T - 1 at pairs 0 .. T - 1: all before the last pair's barrier
+        if (j < T) issue_b_tile(kb_next, j);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NP) ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
