@@ -360,7 +360,7 @@ class WeightedGate:
                 torch.from_numpy(sc).to(x.device).reshape(*x.shape[:-1], self.top_k))
 
 
-@pytest.mark.parametrize("inter,codes_480", [(384, False), (384, True), (256, True)])
+@pytest.mark.parametrize("inter,codes_480", [(384, False), (384, True), (256, True), (128, True)])
 def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, inter, codes_480):
     """The wide GEMM shape (128-route descriptors x 512 weight rows: 256 gate
     rows with the matching 256 up rows for gate/up, 512 output columns for
@@ -369,8 +369,9 @@ def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, inter, codes_480
     single groups), hidden 640 (the down GEMM's second item ends 384 rows
     past the matrix: whole wavefronts past it re-read its last 8 rows, its
     last scale block clamped), intermediate 384 (the second gate/up item
-    half past the matrix: a partial last gate tile) or 256 (one whole
-    gate/up item), the shared expert as dense
+    half past the matrix: a partial last gate tile), 256 (one whole
+    gate/up item) or 128 (the down GEMM one 128-deep stage, so its first
+    stage is its last), the shared expert as dense
     descriptors in the same launches; with 0x7F / 0xFF codes in the routed
     gate/up and down weights, the fixup path of both modes (also on the
     partial gate tile at intermediate 256).  Against the oracle's Direct
