@@ -394,6 +394,31 @@ def test_wide_gemm_shape_ragged_tiles_matches_oracle(M, O, dev, inter, codes_480
     assert_parity(to_bits(y).reshape(T, -1), want, O)
 
 
+def test_wide_gemm_full_width_with_480_codes_matches_oracle(M, O, dev):
+    """The wide GEMM shape at the model's widths (hidden 4,096: 32 stages of
+    the gate/up K loop; intermediate 1,536: 12 of the down one), 8 experts
+    with skewed counts, so that descriptors of every pair count from full
+    (the next stage's weight tiles issued one per pair) to one pair run,
+    with 0x7F / 0xFF codes in the routed gate/up and down weights (the
+    fixup path of both modes) and the shared expert as dense descriptors.
+    Against the oracle's Direct MoE."""
+    syn = submodule("synthetic")
+    cfg = syn.layer_config(hidden=4096, intermediate=1536, experts=8, top_k=4, limit=7.0)
+    bank, shared, _ = syn.synth_layer(cfg, seed=171, device=dev)
+    bank.gate_up_weight[3, ::11, ::29] = 0x7F
+    bank.gate_up_weight[0, 7::13, 5::31] = 0xFF
+    bank.down_weight[1, ::17, 2::11] = 0xFF
+    gate = WeightedGate(8, 4, seed=17)
+    T = 300
+    x = syn.normal_bf16((1, T, cfg.hidden_size), syn.key(171, "wide-full"), device=dev)
+    ids, sc = (t.reshape(T, 4).cpu().numpy() for t in gate(x))
+    counts = np.bincount(ids.reshape(-1), minlength=8)
+    assert counts.max() > 128 and counts.min() < 96, counts
+    y = M.SortedGroupedFP8MoE(bank, cfg, gate, shared)(x)
+    want = O.direct_moe(to_bits(x).reshape(T, -1), host_bank(bank), ids, sc, cfg.swiglu_limit, host_shared(shared))
+    assert_parity(to_bits(y).reshape(T, -1), want, O)
+
+
 @pytest.mark.parametrize("shared_experts", [1, 2])
 def test_prefill_shared_expert_merged_or_separate_matches_oracle(M, O, dev, shared_experts):
     """A shared expert of the routed width runs as extra dense descriptors
