@@ -1141,6 +1141,7 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
 #pragma unroll
   for (int q = 0; q < T; ++q) bq[q] = lds_operand(lds + b_own + q * kOperand, slots);
   i32x8 ahi_next = lds_operand(lds + kWideBBytes, slots);
+  i32x8 alo_next = lds_operand(lds + kWideBBytes + kOperand, slots);
   int slot = 0;
   for (int64_t kb = 0; kb < KB; ++kb) {
     // the other slot's stage (kb - 1) was read out by every wavefront before
@@ -1169,15 +1170,16 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
       for (int i = 0; i < 4; ++i) acc[j][q][i] = fmaf(c[q][i], sw, acc[j][q][i]);
     };
     const uint8_t* st_next = lds + kWideBBytes + (slot ^ 1) * kWideABytes;
-    // A operands half a pair ahead at no register cost: pair j's lo rows
-    // are read as its hi pass starts, pair j + 1's hi rows (after the last
-    // pair: the next stage's first) as its lo pass starts (each into the
-    // registers the operand before it just freed)
+    // A operands a whole pair ahead: pair j + 1's hi and lo rows (after the
+    // last pair: the next stage's first) are read as pair j's lo pass
+    // starts, so each pair's operands have had a whole pair's MFMAs to
+    // arrive (8 VGPRs more than reading the lo rows at the pair's own start:
+    // gate/up -3%, down -3.5%)
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       const int se = static_cast<int>(j < 4 ? se2.x : se2.y);
       const i32x8 ahi = ahi_next;
-      const i32x8 alo = lds_operand(st + (2 * j + 1) * kOperand, slots);
+      const i32x8 alo = alo_next;
       // Issue priority falls as a wavefront gets ahead in its stage, so of
       // the two on a SIMD the one behind gets the MFMA pipe and they reach
       // the barrier closer together (gate/up -2%).
@@ -1215,8 +1217,13 @@ __device__ __forceinline__ void wide_gemm_loop(const GroupedGemmArgs& a, const I
         if (j < T) issue_b_tile(kb_next, j);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (j + 1 < NP) ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
-      else ahi_next = lds_operand(st_next, slots);  // unused after the last stage
+      if (j + 1 < NP) {
+        ahi_next = lds_operand(st + (2 * j + 2) * kOperand, slots);
+        alo_next = lds_operand(st + (2 * j + 3) * kOperand, slots);
+      } else {  // unused after the last stage
+        ahi_next = lds_operand(st_next, slots);
+        alo_next = lds_operand(st_next + kOperand, slots);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < T; ++q) {
